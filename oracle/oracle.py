@@ -1,0 +1,237 @@
+"""ctypes binding of the CPU oracle (liboracle.so) -- test infrastructure only.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this module; the
+product path never does.  See fa_oracle.h for what each function restates (reference
+file:line) and how it is pinned.  ``ref_numeric()`` loads the reference's own codec source
+(src/core/numeric.cpp) compiled into _ref/ by this directory's Makefile, when present.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import subprocess
+from typing import Optional, Sequence
+
+import numpy as np
+
+ORACLE_DIR = pathlib.Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "liboracle.so"
+REF_PATH = ORACLE_DIR / "_ref" / "libref_numeric.so"
+
+F32, F16, Q8_0 = 0, 1, 8
+
+
+class View(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_int64 * 4),
+    ]
+
+
+class Pcg32(ctypes.Structure):
+    _fields_ = [("state", ctypes.c_uint64), ("inc", ctypes.c_uint64)]
+
+
+_lib = None
+_ref = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR), "liboracle.so"], check=True)
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        lib = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, u64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64
+        VP = ctypes.POINTER(View)
+        lib.oracle_set_simd.argtypes = [ctypes.c_int]
+        lib.oracle_set_simd.restype = ctypes.c_int
+        lib.oracle_have_simd.restype = ctypes.c_int
+        lib.oracle_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        lib.oracle_fp16_to_fp32.restype = ctypes.c_float
+        lib.oracle_fp32_to_fp16.argtypes = [ctypes.c_float]
+        lib.oracle_fp32_to_fp16.restype = ctypes.c_uint16
+        lib.oracle_fp32_to_fp16_row.argtypes = [vp, vp, i64]
+        lib.oracle_fp16_to_fp32_row.argtypes = [vp, vp, i64]
+        lib.oracle_quantize_row_q8_0.argtypes = [vp, vp, i64]
+        lib.oracle_quantize_row_q8_0.restype = ctypes.c_int
+        lib.oracle_dequantize_row_q8_0.argtypes = [vp, vp, i64]
+        lib.oracle_vec_dot_f16.argtypes = [i64, vp, vp]
+        lib.oracle_vec_dot_f16.restype = ctypes.c_float
+        lib.oracle_vec_dot_q8_0.argtypes = [i64, vp, vp]
+        lib.oracle_vec_dot_q8_0.restype = ctypes.c_float
+        lib.oracle_flash_attn_ext.argtypes = [VP, VP, VP, VP, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                              vp, ctypes.c_int, ctypes.c_int]
+        lib.oracle_flash_attn_ext.restype = ctypes.c_int
+        lib.oracle_build_kq_mask.argtypes = [vp, i64, i64, i64, vp, vp, ctypes.c_int]
+        lib.oracle_build_kq_mask.restype = ctypes.c_int
+        lib.oracle_pcg32_seed.argtypes = [ctypes.POINTER(Pcg32), u64, u64]
+        lib.oracle_pcg32_next.argtypes = [ctypes.POINTER(Pcg32)]
+        lib.oracle_pcg32_next.restype = ctypes.c_uint32
+        lib.oracle_pcg32_uniform01.argtypes = [ctypes.POINTER(Pcg32)]
+        lib.oracle_pcg32_uniform01.restype = ctypes.c_double
+        lib.oracle_fill_normal_f32.argtypes = [u64, u64, ctypes.c_float, vp, i64]
+        _lib = lib
+    return _lib
+
+
+def ref_numeric() -> Optional[ctypes.CDLL]:
+    """The reference's own fp16/q8_0 codecs (oracle/_ref), or None when not built."""
+    global _ref
+    if _ref is None and REF_PATH.exists():
+        lib = ctypes.CDLL(str(REF_PATH))
+        lib.ref_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        lib.ref_fp16_to_fp32.restype = ctypes.c_float
+        lib.ref_fp32_to_fp16.argtypes = [ctypes.c_float]
+        lib.ref_fp32_to_fp16.restype = ctypes.c_uint16
+        lib.ref_fp32_to_fp16_row.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        lib.ref_quantize_row_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        lib.ref_quantize_row_q8_0.restype = ctypes.c_int
+        lib.ref_q8_0_block_bytes.restype = ctypes.c_int
+        _ref = lib
+    return _ref
+
+
+# ---------------------------------------------------------------------------------------
+def fp32_to_fp16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    load().oracle_fp32_to_fp16_row(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def fp16_bits_to_fp32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    load().oracle_fp16_to_fp32_row(h.ctypes.data, out.ctypes.data, h.size)
+    return out
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size // 32 * 34, dtype=np.uint8)
+    if load().oracle_quantize_row_q8_0(x.ctypes.data, out.ctypes.data, x.size) != 0:
+        raise ValueError("q8_0 needs a multiple of 32 elements")
+    return out
+
+
+def dequantize_q8_0(b: np.ndarray, n: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    load().oracle_dequantize_row_q8_0(b.ctypes.data, out.ctypes.data, n)
+    return out
+
+
+def fill_normal(seed: int, seq: int, n: int, mul: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    load().oracle_fill_normal_f32(seed, seq, mul, out.ctypes.data, n)
+    return out
+
+
+def pcg32_u32(seed: int, seq: int, n: int) -> list:
+    lib = load()
+    r = Pcg32()
+    lib.oracle_pcg32_seed(ctypes.byref(r), seed, seq)
+    return [lib.oracle_pcg32_next(ctypes.byref(r)) for _ in range(n)]
+
+
+def view(arr: np.ndarray, type_id: int, head_dim: Optional[int] = None, tokens_heads: bool = True) -> View:
+    """ggml view of a 4-d numpy array whose last axis is innermost.
+
+    tokens_heads=True: arr is (S, tokens, heads, D) and the view is ggml's [D, tokens, heads, S]
+    (how llama.cpp permutes Q/K/V); False: the plain reversal (out [D, H, n_q, S], mask)."""
+    assert arr.ndim == 4
+    v = View()
+    v.data = arr.ctypes.data
+    v.type = type_id
+    order = (3, 1, 2, 0) if tokens_heads else (3, 2, 1, 0)
+    ne = [arr.shape[i] for i in order]
+    nb = [arr.strides[i] for i in order]
+    if type_id == Q8_0:
+        ne[0] = head_dim
+        nb[0] = 34
+    for i in range(4):
+        v.ne[i] = ne[i]
+        v.nb[i] = nb[i]
+    return v
+
+
+def build_kq_mask(n_kv: int, n_q_pad: int, kv_len: Sequence[int], q_len: Sequence[int],
+                  causal: bool = True) -> np.ndarray:
+    """llama-style f16 mask [S, 1, n_q_pad, n_kv] (f16 bits as uint16)."""
+    S = len(kv_len)
+    kl = np.ascontiguousarray(kv_len, dtype=np.int32)
+    ql = np.ascontiguousarray(q_len, dtype=np.int32)
+    m = np.empty((S, 1, n_q_pad, n_kv), dtype=np.uint16)
+    if load().oracle_build_kq_mask(m.ctypes.data, n_kv, n_q_pad, S, kl.ctypes.data, ql.ctypes.data,
+                                   1 if causal else 0) != 0:
+        raise ValueError("stream cells exceed n_kv")
+    return m
+
+
+def flash_attn_ext(q: np.ndarray, k: np.ndarray, v: np.ndarray, kv_type: int = F16,
+                   mask: Optional[np.ndarray] = None, scale: Optional[float] = None,
+                   max_bias: float = 0.0, logit_softcap: float = 0.0, v_acc_f16: bool = False,
+                   n_threads: int = 0) -> np.ndarray:
+    """out[S, n_q, H, D] = ggml CPU flash_attn_ext(q[S,n_q,H,D] f32, k/v[S,n_kv,Hkv,D|D/32*34])."""
+    q = np.asarray(q, dtype=np.float32)
+    S, n_q, H, D = q.shape
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    out = np.empty((S, n_q, H, D), dtype=np.float32)
+    qv = view(q, F32)
+    kv_ = view(k, kv_type, D)
+    vv = view(v, kv_type, D)
+    mv = view(mask, F16, tokens_heads=False) if mask is not None else None
+    rc = load().oracle_flash_attn_ext(ctypes.byref(qv), ctypes.byref(kv_), ctypes.byref(vv),
+                                      ctypes.byref(mv) if mv is not None else None,
+                                      float(scale), float(max_bias), float(logit_softcap),
+                                      out.ctypes.data, 1 if v_acc_f16 else 0, int(n_threads))
+    if rc != 0:
+        raise ValueError(f"oracle_flash_attn_ext rejected the description ({rc})")
+    return out
+
+
+def attention_for_workload(host: dict, kv_type: int, streams: Optional[Sequence[int]] = None,
+                           causal: bool = True, v_acc_f16: bool = False, n_threads: int = 0,
+                           scale: Optional[float] = None) -> np.ndarray:
+    """Oracle output for (a subset of) the streams of a synthetic workload."""
+    idx = list(range(host["q"].shape[0])) if streams is None else list(streams)
+    q = host["q"][idx]
+    if q.dtype == np.float16:
+        q = q.astype(np.float32)
+    kl = host["kv_len"][idx]
+    ql = host["q_len"][idx]
+    n_kv = int((kl + ql).max())
+    k = np.ascontiguousarray(host["k"][idx][:, :n_kv])
+    v = np.ascontiguousarray(host["v"][idx][:, :n_kv])
+    mask = build_kq_mask(n_kv, q.shape[1], kl, ql, causal)
+    return flash_attn_ext(np.ascontiguousarray(q), k, v, kv_type, mask, scale=scale,
+                          v_acc_f16=v_acc_f16, n_threads=n_threads)
+
+
+def diff_metrics(ref: np.ndarray, out: np.ndarray) -> dict:
+    """max-abs, rel-L2 (||out-ref|| / ||ref||) and cosine in float64 (after numeric.cpp:701-791)."""
+    r = np.asarray(ref, dtype=np.float64).ravel()
+    o = np.asarray(out, dtype=np.float64).ravel()
+    d = o - r
+    nr = np.linalg.norm(r)
+    return {
+        "max_abs": float(np.max(np.abs(d))) if d.size else 0.0,
+        "rel_l2": float(np.linalg.norm(d) / nr) if nr > 0 else float(np.linalg.norm(d)),
+        "cosine": float(np.dot(r, o) / (nr * np.linalg.norm(o))) if nr > 0 and np.linalg.norm(o) > 0 else 1.0,
+    }
+
+
+def cpu_threads() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1

@@ -1,0 +1,254 @@
+// sixi_attn_abi.cpp -- the C ABI of include/sixi_attn.h: validation, workspace sizing and
+// kernel choice on the host; the kernels themselves live in fa_splitk.hip and
+// fa_prefill.hip.
+//
+// Errors follow the reference's convention of returning a status instead of aborting
+// (include/sixi_asi/common.hpp:40-67, codes negated), where ggml_flash_attn_ext would
+// GGML_ASSERT.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#include "fa_internal.hpp"
+#include "sixi_attn.h"
+
+namespace {
+
+using sixi::FaArgs;
+
+constexpr size_t kWsAlign = 256;
+constexpr int kMaxHeadDim = 128;       // head dims built for gfx950 in this library
+constexpr int kSplitMaxRows = 96;      // G * n_q handled by the split-K kernel
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+bool mul_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_mul_overflow(a, b, out); }
+bool add_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_add_overflow(a, b, out); }
+
+// Largest byte offset touched by a view (0 for empty), or -1 on overflow.
+int64_t view_span(const sixi_view& v, int64_t row_bytes) {
+    int64_t span = row_bytes, t = 0;
+    for (int d = 1; d < 4; ++d) {
+        if (v.ne[d] <= 0) return 0;
+        if (!mul_ok(v.ne[d] - 1, v.nb[d], &t) || !add_ok(span, t, &span)) return -1;
+    }
+    return span;
+}
+
+int elem_bytes(int32_t type) {
+    switch (type) {
+        case SIXI_TYPE_F32: return 4;
+        case SIXI_TYPE_F16: return 2;
+        default: return 0;
+    }
+}
+
+// Bytes of one head row of D elements.
+int64_t row_bytes(int32_t type, int64_t D) {
+    if (type == SIXI_TYPE_Q8_0) return D / 32 * 34;
+    return D * elem_bytes(type);
+}
+
+bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)a) == 0; }
+
+struct Plan {
+    FaArgs a{};
+    int kv_type = 0;
+    int mask_mode = 0;
+    int D = 0;
+    bool splitk = true;
+    size_t ws_bytes = 0;
+    size_t meta_bytes = 0;
+};
+
+int cu_count_cached() {
+    static int cached = -1;
+    if (cached < 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cached = n;
+        else
+            cached = 256;
+    }
+    return cached;
+}
+
+// Resolves and validates a description.  Touches no device memory.
+int resolve(const sixi_attn_params* p, Plan* out) {
+    if (!p || !out) return SIXI_E_INVALID_ARGUMENT;
+    if (p->flags != 0) return SIXI_E_INVALID_ARGUMENT;
+    const sixi_view &q = p->q, &k = p->k, &v = p->v, &o = p->out;
+    if (!q.data || !k.data || !v.data || !o.data) return SIXI_E_INVALID_ARGUMENT;
+
+    // types
+    if (q.type != SIXI_TYPE_F32 && q.type != SIXI_TYPE_F16) return SIXI_E_UNSUPPORTED;
+    if (k.type != SIXI_TYPE_F16 && k.type != SIXI_TYPE_Q8_0) return SIXI_E_UNSUPPORTED;
+    if (v.type != k.type) return SIXI_E_UNSUPPORTED;
+    if (o.type != SIXI_TYPE_F32) return SIXI_E_UNSUPPORTED;
+
+    // extents
+    for (int d = 0; d < 4; ++d)
+        if (q.ne[d] <= 0 || k.ne[d] <= 0 || v.ne[d] <= 0 || o.ne[d] <= 0) return SIXI_E_INVALID_ARGUMENT;
+    const int64_t D = q.ne[0], n_q = q.ne[1], H = q.ne[2], S = q.ne[3];
+    const int64_t n_kv = k.ne[1], Hkv = k.ne[2];
+    if (k.ne[0] != D || v.ne[0] != D) return SIXI_E_INVALID_ARGUMENT;
+    if (v.ne[1] != n_kv || v.ne[2] != Hkv || k.ne[3] != S || v.ne[3] != S) return SIXI_E_INVALID_ARGUMENT;
+    if (H % Hkv != 0) return SIXI_E_INVALID_ARGUMENT;
+    if (o.ne[0] != D || o.ne[1] != H || o.ne[2] != n_q || o.ne[3] != S) return SIXI_E_INVALID_ARGUMENT;
+    if (S > sixi::kMaxStreams || H > 4096 || n_q > (1 << 20) || n_kv > (1 << 26)) return SIXI_E_UNSUPPORTED;
+    if (D != kMaxHeadDim) return SIXI_E_UNSUPPORTED;
+    if (k.type == SIXI_TYPE_Q8_0) return SIXI_E_UNSUPPORTED;  // q8_0 kernels are not built yet
+
+    // element strides and alignment
+    const int qes = elem_bytes(q.type);
+    if (q.nb[0] != qes || o.nb[0] != 4) return SIXI_E_INVALID_ARGUMENT;
+    if (k.nb[0] != (k.type == SIXI_TYPE_Q8_0 ? 34 : 2) || v.nb[0] != k.nb[0]) return SIXI_E_INVALID_ARGUMENT;
+    for (int d = 1; d < 4; ++d) {
+        if (q.nb[d] <= 0 || k.nb[d] <= 0 || v.nb[d] <= 0 || o.nb[d] <= 0) return SIXI_E_INVALID_ARGUMENT;
+        if (q.nb[d] % qes) return SIXI_E_ALIGNMENT;
+        if (k.nb[d] % 16 || v.nb[d] % 16 || o.nb[d] % 16) return SIXI_E_ALIGNMENT;
+    }
+    if (!aligned(q.data, qes) || !aligned(k.data, 16) || !aligned(v.data, 16) || !aligned(o.data, 16))
+        return SIXI_E_ALIGNMENT;
+    const int64_t kvrow = row_bytes(k.type, D);
+    if (k.nb[1] < kvrow || v.nb[1] < kvrow) return SIXI_E_INVALID_ARGUMENT;  // rows must not overlap
+    if (o.nb[1] < D * 4 || q.nb[1] < D * qes) return SIXI_E_INVALID_ARGUMENT;
+    // one stream's cells are addressed with 32-bit offsets
+    int64_t kspan = 0, vspan = 0;
+    if (!mul_ok(n_kv, k.nb[1], &kspan) || !mul_ok(n_kv, v.nb[1], &vspan) ||
+        kspan >= (int64_t)UINT32_MAX || vspan >= (int64_t)UINT32_MAX)
+        return SIXI_E_UNSUPPORTED;
+    if (view_span(q, D * qes) < 0 || view_span(k, kvrow) < 0 || view_span(v, kvrow) < 0 ||
+        view_span(o, D * 4) < 0)
+        return SIXI_E_INTEGER_OVERFLOW;
+
+    // mask
+    const int mode = p->mask_mode;
+    if (mode < SIXI_MASK_NONE || mode > SIXI_MASK_EXPLICIT) return SIXI_E_INVALID_ARGUMENT;
+    if (mode == SIXI_MASK_BLOCK_CAUSAL && (!p->kv_len || n_q > n_kv)) return SIXI_E_INVALID_ARGUMENT;
+    if (p->kv_len && n_q > n_kv) return SIXI_E_INVALID_ARGUMENT;
+    const sixi_view& m = p->mask;
+    if (mode == SIXI_MASK_EXPLICIT) {
+        if (!m.data || m.type != SIXI_TYPE_F16 || m.nb[0] != 2) return SIXI_E_INVALID_ARGUMENT;
+        if (m.ne[0] < n_kv || m.ne[1] < n_q || m.ne[2] != 1 || (m.ne[3] != 1 && m.ne[3] != S))
+            return SIXI_E_INVALID_ARGUMENT;
+        if (m.nb[1] % 2 || m.nb[3] % 2 || !aligned(m.data, 2)) return SIXI_E_ALIGNMENT;
+        if (view_span(m, m.ne[0] * 2) < 0) return SIXI_E_INTEGER_OVERFLOW;
+    }
+
+    // scalars (ggml: ALiBi slopes multiply the mask, so they need one)
+    if (!std::isfinite(p->scale) || !std::isfinite(p->max_bias) || !std::isfinite(p->logit_softcap))
+        return SIXI_E_INVALID_ARGUMENT;
+    if (p->max_bias < 0.0f || p->logit_softcap < 0.0f) return SIXI_E_INVALID_ARGUMENT;
+    if (p->max_bias > 0.0f && mode != SIXI_MASK_EXPLICIT) return SIXI_E_INVALID_ARGUMENT;
+
+    Plan pl;
+    FaArgs& a = pl.a;
+    a.q = static_cast<const char*>(q.data);
+    a.q_nb1 = q.nb[1]; a.q_nb2 = q.nb[2]; a.q_nb3 = q.nb[3];
+    a.q_es = qes;
+    a.q_f16 = (q.type == SIXI_TYPE_F16);
+    a.k = static_cast<const char*>(k.data);
+    a.k_nb1 = k.nb[1]; a.k_nb2 = k.nb[2]; a.k_nb3 = k.nb[3];
+    a.v = static_cast<const char*>(v.data);
+    a.v_nb1 = v.nb[1]; a.v_nb2 = v.nb[2]; a.v_nb3 = v.nb[3];
+    a.out = static_cast<char*>(const_cast<void*>(o.data));
+    a.o_nb1 = o.nb[1]; a.o_nb2 = o.nb[2]; a.o_nb3 = o.nb[3];
+    a.kv_len = p->kv_len;
+    a.q_len = p->q_len;
+    if (mode == SIXI_MASK_EXPLICIT) {
+        a.mask = static_cast<const char*>(m.data);
+        a.m_nb1 = m.nb[1]; a.m_nb3 = m.nb[3];
+        a.m_ne3 = (int32_t)m.ne[3];
+    } else {
+        a.m_ne3 = 1;
+    }
+    a.S = (int32_t)S; a.H = (int32_t)H; a.Hkv = (int32_t)Hkv; a.G = (int32_t)(H / Hkv);
+    a.n_q = (int32_t)n_q; a.n_kv = (int32_t)n_kv;
+    const float softcap = p->logit_softcap;
+    a.scale = softcap != 0.0f ? p->scale / softcap : p->scale;
+    a.scale_log2 = a.scale * 1.4426950408889634f;
+    a.softcap = softcap;
+    if (p->max_bias > 0.0f) {
+        int nlog2 = 1;
+        while (nlog2 * 2 <= H) nlog2 *= 2;
+        a.alibi_nlog2 = nlog2;
+        a.alibi_m0 = std::pow(2.0f, -p->max_bias / (float)nlog2);
+        a.alibi_m1 = std::pow(2.0f, -(p->max_bias / 2.0f) / (float)nlog2);
+    }
+
+    pl.kv_type = k.type;
+    pl.mask_mode = mode;
+    pl.D = (int)D;
+    const int64_t rows = (int64_t)a.G * n_q;
+    pl.splitk = rows <= kSplitMaxRows;
+    if (!pl.splitk) return SIXI_E_UNSUPPORTED;  // prefill kernel not built yet
+
+    a.rows_max = (int32_t)align_up((size_t)rows, 16);
+    a.slot_floats = (int64_t)a.rows_max * D + 2 * (int64_t)a.rows_max;
+    pl.meta_bytes = align_up(sizeof(int32_t) * (size_t)(S + 1), kWsAlign);
+    const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
+    pl.ws_bytes = pl.meta_bytes + align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
+    *out = pl;
+    return SIXI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sixi_attn_validate(const sixi_attn_params* p) {
+    Plan pl;
+    return resolve(p, &pl);
+}
+
+int sixi_attn_workspace_bytes(const sixi_attn_params* p, size_t* bytes) {
+    if (!bytes) return SIXI_E_INVALID_ARGUMENT;
+    Plan pl;
+    const int rc = resolve(p, &pl);
+    if (rc != SIXI_OK) return rc;
+    *bytes = pl.ws_bytes;
+    return SIXI_OK;
+}
+
+int sixi_attn_forward(const sixi_attn_params* p) {
+    Plan pl;
+    int rc = resolve(p, &pl);
+    if (rc != SIXI_OK) return rc;
+    if (!p->workspace || p->workspace_bytes < pl.ws_bytes) return SIXI_E_OUT_OF_BOUNDS;
+    if (!aligned(p->workspace, kWsAlign)) return SIXI_E_ALIGNMENT;
+    FaArgs& a = pl.a;
+    char* ws = static_cast<char*>(p->workspace);
+    a.meta = reinterpret_cast<int32_t*>(ws);
+    a.part = reinterpret_cast<float*>(ws + pl.meta_bytes);
+    hipStream_t stream = static_cast<hipStream_t>(p->stream);
+    hipError_t e;
+    if (pl.splitk) {
+        a.P = sixi::splitk_num_groups(a, cu_count_cached());
+        e = sixi::launch_splitk(a, pl.kv_type, pl.mask_mode, pl.D, stream);
+    } else {
+        e = sixi::launch_prefill(a, pl.kv_type, pl.mask_mode, pl.D, stream);
+    }
+    if (e == hipErrorNotSupported) return SIXI_E_UNSUPPORTED;
+    return e == hipSuccess ? SIXI_OK : SIXI_E_BACKEND;
+}
+
+const char* sixi_attn_strerror(int code) {
+    switch (code) {
+        case SIXI_OK: return "ok";
+        case SIXI_E_INVALID_ARGUMENT: return "invalid argument";
+        case SIXI_E_OUT_OF_BOUNDS: return "out of bounds (workspace too small)";
+        case SIXI_E_INTEGER_OVERFLOW: return "integer overflow in view extents";
+        case SIXI_E_ALIGNMENT: return "misaligned pointer or stride";
+        case SIXI_E_BACKEND: return "HIP launch failed";
+        case SIXI_E_UNSUPPORTED: return "shape or type not supported by the gfx950 kernels";
+        default: return "unknown status";
+    }
+}
+
+int sixi_attn_abi_version(void) { return SIXI_ATTN_ABI_VERSION; }
+
+}  // extern "C"

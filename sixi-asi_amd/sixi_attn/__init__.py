@@ -1,0 +1,230 @@
+"""Python binding of the MI355X attention hot path (libsixi_attn.so, include/sixi_attn.h).
+
+The operator mirrors ggml's ``ggml_flash_attn_ext(q, k, v, mask, scale, max_bias,
+logit_softcap)`` -- the op the reference reaches through ``llama_decode`` at
+src/core/core_execution.cpp:2074 (verify), :3536 (prefill chunk) and :3811 (decode) --
+with per-stream device lengths in place of the host-built KQ mask.  Tensors use the
+row-major mirror of ggml's views: ``q[S, n_q, H, D]``, ``k/v[S, n_kv, Hkv, D]`` (f16, or
+uint8 ``[S, n_kv, Hkv, D/32*34]`` q8_0 blocks), ``out[S, n_q, H, D]`` f32; strides are
+taken from the tensors, so cache slices and paged layouts pass through unchanged.
+
+torch provides device memory and the stream; the computation is the HIP library.  There is
+no CPU fallback: a missing library raises ``SixiAttnUnavailable``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import pathlib
+from typing import Optional
+
+PKG_DIR = pathlib.Path(__file__).resolve().parent.parent
+LIB_DIR = PKG_DIR / "lib"
+LIB_PATH = LIB_DIR / "libsixi_attn.so"
+
+# ggml type ids
+TYPE_F32, TYPE_F16, TYPE_Q8_0 = 0, 1, 8
+# mask modes
+MASK_NONE, MASK_BLOCK_CAUSAL, MASK_EXPLICIT = 0, 1, 2
+# status codes (negated sixi_asi::ErrorCode, include/sixi_asi/common.hpp:40-67)
+OK = 0
+E_INVALID_ARGUMENT = -1
+E_OUT_OF_BOUNDS = -2
+E_INTEGER_OVERFLOW = -3
+E_ALIGNMENT = -15
+E_BACKEND = -23
+E_UNSUPPORTED = -24
+
+EXPORTED_SYMBOLS = (
+    "sixi_attn_forward",
+    "sixi_attn_workspace_bytes",
+    "sixi_attn_validate",
+    "sixi_attn_strerror",
+    "sixi_attn_abi_version",
+)
+
+
+class SixiAttnUnavailable(RuntimeError):
+    """The HIP library is not built or cannot be loaded."""
+
+
+class SixiAttnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"sixi_attn status {code}: {msg}")
+        self.code = code
+
+
+class SixiView(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_int64 * 4),
+    ]
+
+
+class SixiAttnParams(ctypes.Structure):
+    _fields_ = [
+        ("q", SixiView),
+        ("k", SixiView),
+        ("v", SixiView),
+        ("out", SixiView),
+        ("kv_len", ctypes.c_void_p),
+        ("q_len", ctypes.c_void_p),
+        ("mask_mode", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("mask", SixiView),
+        ("scale", ctypes.c_float),
+        ("max_bias", ctypes.c_float),
+        ("logit_softcap", ctypes.c_float),
+        ("reserved_f", ctypes.c_float),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+
+
+def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
+    """Loads libsixi_attn.so (built in-tree by sixi-asi_amd/build.py)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = pathlib.Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise SixiAttnUnavailable(f"{p} is missing: run `python sixi-asi_amd/build.py`")
+    try:
+        lib = ctypes.CDLL(str(p))
+    except OSError as e:  # pragma: no cover - loader failure is environment specific
+        raise SixiAttnUnavailable(f"cannot load {p}: {e}") from e
+    P = ctypes.POINTER(SixiAttnParams)
+    lib.sixi_attn_forward.argtypes = [P]
+    lib.sixi_attn_forward.restype = ctypes.c_int
+    lib.sixi_attn_validate.argtypes = [P]
+    lib.sixi_attn_validate.restype = ctypes.c_int
+    lib.sixi_attn_workspace_bytes.argtypes = [P, ctypes.POINTER(ctypes.c_size_t)]
+    lib.sixi_attn_workspace_bytes.restype = ctypes.c_int
+    lib.sixi_attn_strerror.argtypes = [ctypes.c_int]
+    lib.sixi_attn_strerror.restype = ctypes.c_char_p
+    lib.sixi_attn_abi_version.argtypes = []
+    lib.sixi_attn_abi_version.restype = ctypes.c_int
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def strerror(code: int) -> str:
+    return load_library().sixi_attn_strerror(code).decode()
+
+
+def make_view(data_ptr: int, type_id: int, ne, nb) -> SixiView:
+    v = SixiView()
+    v.data = data_ptr
+    v.type = type_id
+    for i in range(4):
+        v.ne[i] = int(ne[i])
+        v.nb[i] = int(nb[i])
+    return v
+
+
+def view_of(t, type_id: Optional[int] = None, head_dim: Optional[int] = None,
+            tokens_heads: bool = True) -> SixiView:
+    """ggml view of a 4-d torch tensor whose last dim is innermost.
+
+    tokens_heads=True: t is (S, tokens, heads, D) and the view is ggml's [D, tokens, heads, S]
+    (Q, K, V as llama.cpp permutes them); False: the plain reversal (out, mask).
+    For q8_0 pass a uint8 tensor whose last dim holds the packed blocks and ``head_dim``.
+    """
+    import torch
+
+    if t.dim() != 4:
+        raise ValueError("expected a 4-d tensor")
+    es = t.element_size()
+    order = (3, 1, 2, 0) if tokens_heads else (3, 2, 1, 0)
+    nb = [t.stride(i) * es for i in order]
+    ne = [t.shape[i] for i in order]
+    if type_id is None:
+        type_id = {torch.float32: TYPE_F32, torch.float16: TYPE_F16}[t.dtype]
+    if type_id == TYPE_Q8_0:
+        if t.dtype != torch.uint8 or head_dim is None or t.shape[-1] != head_dim // 32 * 34:
+            raise ValueError("q8_0 view needs a uint8 tensor of D/32*34 bytes per row and head_dim")
+        if t.stride(-1) != 1:
+            raise ValueError("q8_0 rows must be contiguous")
+        ne[0] = head_dim
+        nb[0] = 34
+    return make_view(t.data_ptr(), type_id, ne, nb)
+
+
+class FlashAttnExt:
+    """``ggml_flash_attn_ext`` over per-stream KV caches on one gfx950 GPU.
+
+    Keeps a device workspace (grown on demand) so repeated calls allocate nothing.
+    """
+
+    def __init__(self, device=None):
+        import torch
+
+        self.lib = load_library()
+        self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self._ws = None
+
+    def params(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
+               scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None) -> SixiAttnParams:
+        import torch
+
+        D = q.shape[-1]
+        kvt = kv_type if kv_type is not None else (TYPE_Q8_0 if k.dtype == torch.uint8 else None)
+        p = SixiAttnParams()
+        p.q = view_of(q)
+        p.k = view_of(k, kvt, D if kvt == TYPE_Q8_0 else None)
+        p.v = view_of(v, kvt, D if kvt == TYPE_Q8_0 else None)
+        p.out = view_of(out, tokens_heads=False)
+        p.kv_len = kv_len.data_ptr() if kv_len is not None else None
+        p.q_len = q_len.data_ptr() if q_len is not None else None
+        p.mask_mode = mask_mode
+        p.flags = 0
+        if mask is not None:
+            # mask tensor [S or 1, 1, n_q_pad, n_kv] f16
+            p.mask = view_of(mask, TYPE_F16, tokens_heads=False)
+        p.scale = 1.0 / math.sqrt(D) if scale is None else scale
+        p.max_bias = max_bias
+        p.logit_softcap = logit_softcap
+        p.stream = stream
+        return p
+
+    def workspace_bytes(self, p: SixiAttnParams) -> int:
+        n = ctypes.c_size_t(0)
+        rc = self.lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n))
+        if rc != OK:
+            raise SixiAttnError(rc, strerror(rc))
+        return n.value
+
+    def _workspace(self, nbytes: int):
+        import torch
+
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def __call__(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
+                 scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None, check=True) -> int:
+        import torch
+
+        p = self.params(q, k, v, out, kv_len, q_len, mask_mode, mask, scale, max_bias, logit_softcap,
+                        kv_type, stream)
+        if p.stream is None:
+            p.stream = torch.cuda.current_stream(self.device).cuda_stream
+        n = ctypes.c_size_t(0)
+        rc = self.lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n))
+        if rc == OK:
+            ws = self._workspace(n.value)
+            p.workspace = ws.data_ptr()
+            p.workspace_bytes = ws.numel()
+            rc = self.lib.sixi_attn_forward(ctypes.byref(p))
+        if check and rc != OK:
+            raise SixiAttnError(rc, strerror(rc))
+        return rc
