@@ -1,22 +1,28 @@
 """Benchmark of the MI355X attention hot path (one GPU).
 
-Workload (the headline): batched speculative verify -- 32 streams x 16 drafted rows,
-block-causal, per-stream cached lengths drawn from [512, 16384] (mean ~8.4k), 24/4 heads x
-128, f16 KV in per-stream 256-cell pages, f32 Q -- one attention layer per step.  The
-chunked causal prefill (2 x 2048-row chunks over a 2048-cell cache, f16) is timed beside it
-when its kernel is built.
+Headline workload: batched speculative verify -- 32 streams x 16 drafted rows, block-causal,
+per-stream cached lengths drawn from [512, 16384], 24 q-heads / 4 kv-heads x 128, f16 KV in
+per-stream 256-cell pages, f32 Q -- one attention layer per step.  A step is one call of
+the C ABI (sixi_attn_forward), i.e. the split-K kernel plus its merge kernel, timed with
+HIP events on the stream the library launches on, inputs resident in HBM.
 
 Prints one JSON line: value = algorithmic HBM GB/s of the verify call (K/V of every attended
-cell + Q + O, counted once) with inputs resident in HBM; roofline = that rate against the
-8 TB/s HBM peak; cpu_baseline = the oracle (a restatement of ggml's CPU flash_attn_ext,
-f16 V accumulator as upstream) on the host cores, same inputs.
+cell + Q + O, counted once); roofline = that rate against the 8 TB/s HBM peak; the other
+configurations (single-stream decode and verify, long q8_0 decode/verify, chunked prefill)
+are reported beside it when their kernels are built; cpu_baseline = the oracle (a
+restatement of ggml's CPU flash_attn_ext, f16 V accumulator as upstream) on the host cores,
+same inputs.
+
+`--workload copy` instead times a plain 1 GiB device copy: the calibration run for the HBM
+byte counters (FETCH_SIZE / WRITE_SIZE) used in the traffic figures.
 """
 from __future__ import annotations
 
 import argparse
 import json
-import os
 import pathlib
+import re
+import statistics
 import sys
 import time
 
@@ -26,24 +32,26 @@ sys.path.insert(0, str(ROOT / "sixi-asi_amd"))
 METRIC = "verify-attn µs/layer & HBM GB/s (32 streams×16 tok, 8k ctx); prefill TFLOP/s"
 HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_verify_b32_counters.txt"
 
 
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_calls(fa, w, dev, steps: int, warmup: int):
-    """Per-call GPU time with events on the stream the library launches on."""
+def time_calls(fa, w, dev, steps: int, warmup: int, out=None):
+    """Per-call GPU times (ms) with events on the stream the library launches on."""
     import torch
 
     import sixi_attn as sa
 
-    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    if out is None:
+        out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
 
     def call():
         fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
-           mask_mode=sa.MASK_BLOCK_CAUSAL, stream=stream.cuda_stream)
+           mask_mode=w.mask_mode, stream=stream.cuda_stream)
 
     for _ in range(warmup):
         call()
@@ -59,35 +67,77 @@ def time_calls(fa, w, dev, steps: int, warmup: int):
     return total / steps, per
 
 
-def cpu_baseline(w, host, budget_s: float = 15.0) -> dict:
-    """The oracle on the host cores over a bounded sample of the same workload."""
-    sys.path.insert(0, str(ROOT / "oracle"))
-    import numpy as np
+def summarize(w, ms: float, per) -> dict:
+    per_sorted = sorted(per)
+    n = len(per_sorted)
+    return {
+        "us": round(ms * 1e3, 2),
+        "us_p10_p50_p90": [round(per_sorted[n // 10] * 1e3, 2), round(per_sorted[n // 2] * 1e3, 2),
+                           round(per_sorted[(9 * n) // 10] * 1e3, 2)],
+        "GBps": round(w.bytes() / (ms * 1e-3) / 1e9, 1),
+        "TFLOPs": round(w.flops() / (ms * 1e-3) / 1e12, 2),
+        "bytes": w.bytes(),
+        "flops": w.flops(),
+    }
 
+
+def cpu_baseline(w, host, repeats: int = 5) -> dict:
+    """The oracle on the host cores: the whole verify workload (all 32 streams) on every
+    core of the process affinity, median of `repeats` runs after one warm-up, plus one
+    stream on one thread."""
+    sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
     threads = oracle.cpu_threads()
-    lens = np.array(w.kv_len)
-    order = list(np.argsort(np.abs(lens - lens.mean())))  # streams nearest the mean first
+    oracle.attention_for_workload(host, w.kv_type, [0], v_acc_f16=True, n_threads=threads)
+    runs = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        oracle.attention_for_workload(host, w.kv_type, None, v_acc_f16=True, n_threads=threads)
+        runs.append(time.perf_counter() - t0)
+    dt = statistics.median(runs)
+    # one stream near the mean length on one thread
+    lens = [abs(x - sum(w.kv_len) / w.S) for x in w.kv_len]
+    s1 = lens.index(min(lens))
     t0 = time.perf_counter()
-    oracle.attention_for_workload(host, w.kv_type, order[:1], v_acc_f16=True, n_threads=threads)
-    one = time.perf_counter() - t0
-    n = int(max(1, min(w.S, budget_s / max(one, 1e-3))))
-    sample = sorted(order[:n])
-    t0 = time.perf_counter()
-    oracle.attention_for_workload(host, w.kv_type, sample, v_acc_f16=True, n_threads=threads)
-    dt = time.perf_counter() - t0
-    sub = type(w)(w.name, w.seed, len(sample), [w.kv_len[i] for i in sample], [w.q_len[i] for i in sample],
-                  H=w.H, Hkv=w.Hkv, D=w.D, kv_type=w.kv_type, q_type=w.q_type)
+    oracle.attention_for_workload(host, w.kv_type, [s1], v_acc_f16=True, n_threads=1)
+    dt1 = time.perf_counter() - t0
+    sub = type(w)(w.name, w.seed, 1, [w.kv_len[s1]], [w.q_len[s1]], H=w.H, Hkv=w.Hkv, D=w.D,
+                  kv_type=w.kv_type, q_type=w.q_type)
     return {
-        "value": round(sub.bytes() / dt / 1e9, 3),
+        "value": round(w.bytes() / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(sample)} of {w.S} streams ({sum(sub.kv_len)} cached cells, {sum(sub.q_len)} rows),"
-                  f" f16 V accumulator, {dt:.2f} s",
-        "us_per_call_sample": round(dt * 1e6, 1),
+        "sample": f"the whole workload ({w.S} streams, {sum(w.kv_len)} cached cells, {sum(w.q_len)} rows), "
+                  f"f16 V accumulator as ggml's CPU kernel, median of {repeats} runs: {dt * 1e3:.1f} ms/call",
+        "us_per_call": round(dt * 1e6, 1),
+        "one_thread": {"value": round(sub.bytes() / dt1 / 1e9, 3), "unit": "GB/s",
+                       "sample": f"stream {s1} ({w.kv_len[s1]} cached cells, {w.q_len[s1]} rows), "
+                                 f"{dt1 * 1e3:.1f} ms"},
     }
+
+
+def traffic_from_profile():
+    """HBM bytes per verify call from the committed counter summary, if present."""
+    if not TRAFFIC_PROFILE.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_call:\s*(\d+)", TRAFFIC_PROFILE.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(steps: int) -> int:
+    import torch
+
+    n = 1 << 28  # 1 GiB of f32
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(steps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"workload": "copy", "bytes_read_per_copy": n * 4, "bytes_written_per_copy": n * 4,
+                      "copies": steps}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -95,19 +145,25 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: the attention path has no multi-GPU mode "
-              "(streams would shard across GPUs with no exchange); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build runs on a single MI355X (streams would shard "
+              "across GPUs with no exchange, so N GPUs = N independent copies); run with --gpus 1",
+              file=sys.stderr)
         return 2
 
     import torch
 
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.workload == "copy":
+        return copy_calibration(max(1, args.steps))
+
     import sixi_attn as sa
     from sixi_attn import workloads as wl
 
-    assert torch.cuda.is_available(), "bench.py needs a GPU"
     fa = sa.FlashAttnExt()
     props = torch.cuda.get_device_properties(0)
     _log(f"device {props.name} CUs={props.multi_processor_count}")
@@ -118,15 +174,14 @@ def main() -> int:
     dev = wl.to_device(host)
     _log(f"timing {args.steps} steps after {args.warmup} warm-up")
     ms, per = time_calls(fa, w, dev, args.steps, args.warmup)
-    per_sorted = sorted(per)
-    med = per_sorted[len(per) // 2]
-    gbs = w.bytes() / (ms * 1e-3) / 1e9
-    tflops = w.flops() / (ms * 1e-3) / 1e12
-    _log(f"verify: {ms * 1e3:.1f} us/call, {gbs:.0f} GB/s, {tflops:.1f} TFLOP/s")
+    head = summarize(w, ms, per)
+    gbs = head["GBps"]
+    _log(f"verify: {head['us']} us/call, {gbs} GB/s, {head['TFLOPs']} TFLOP/s")
 
+    traffic = traffic_from_profile()
     result = {
         "metric": METRIC,
-        "value": round(gbs, 2),
+        "value": gbs,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -143,42 +198,56 @@ def main() -> int:
             "streams": w.S, "rows_per_stream": 16, "mean_cached_len": round(sum(w.kv_len) / w.S, 1),
             "bytes_per_call": w.bytes(), "flops_per_call": w.flops(),
         },
-        "us_per_layer": round(ms * 1e3, 2),
-        "us_per_layer_p10_p50_p90": [round(per_sorted[len(per) // 10] * 1e3, 2), round(med * 1e3, 2),
-                                     round(per_sorted[(9 * len(per)) // 10] * 1e3, 2)],
-        "verify_tflops": round(tflops, 2),
+        "us_per_layer": head["us"],
+        "us_per_layer_p10_p50_p90": head["us_p10_p50_p90"],
+        "verify_tflops": head["TFLOPs"],
         "roofline": {
             "bound": "hbm",
-            "kernel": "splitk_f16_d128 + splitk_merge_d128 (one verify call)",
-            "achieved": round(gbs, 2),
+            "kernel": "decode_f16_d128<3,2,0> + decode_merge (one sixi_attn_forward call)",
+            "achieved": gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
     }
 
-    # chunked causal prefill (2 chunks of 2048 rows), when its kernel is available
-    try:
-        pre = []
-        for name in ("prefill_chunk0", "prefill_chunk1"):
-            wp = wl.config(name)
-            hp = wl.make_host(wp)
-            dp = wl.to_device(hp)
-            msp, _ = time_calls(fa, wp, dp, max(10, args.steps // 4), max(3, args.warmup // 4))
-            pre.append((wp, msp))
-        flops = sum(wp.flops() for wp, _ in pre)
-        t = sum(msp for _, msp in pre)
-        tf = flops / (t * 1e-3) / 1e12
-        result["prefill_tflops"] = round(tf, 2)
-        result["prefill_us_two_chunks"] = round(t * 1e3, 2)
-        result["prefill_roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": F16_PEAK_TFLOPS,
-                                      "unit": "TFLOP/s", "frac": round(tf / F16_PEAK_TFLOPS, 4)}
-        _log(f"prefill: {t * 1e3:.1f} us for 2 chunks, {tf:.1f} TFLOP/s")
-    except sa.SixiAttnError as e:
-        result["prefill_tflops"] = None
-        result["prefill_note"] = f"prefill kernel unavailable: {e}"
-        _log(result["prefill_note"])
+    if not args.no_extra:
+        extra = {}
+        for name in ("decode", "verify", "long_q8_decode", "long_q8_verify"):
+            try:
+                we = wl.config(name)
+                he = wl.make_host(we)
+                de = wl.to_device(he)
+                mse, pere = time_calls(fa, we, de, max(20, args.steps // 2), max(5, args.warmup // 2))
+                extra[name] = summarize(we, mse, pere)
+                del de
+            except sa.SixiAttnError as e:
+                extra[name] = {"unavailable": str(e)}
+            _log(f"{name}: {extra[name]}")
+        result["configs"] = extra
+
+        # chunked causal prefill (2 chunks of 2048 rows on a 2048-cell cache)
+        try:
+            pre = []
+            for name in ("prefill_chunk0", "prefill_chunk1"):
+                wp = wl.config(name)
+                hp = wl.make_host(wp)
+                dp = wl.to_device(hp)
+                msp, _ = time_calls(fa, wp, dp, max(10, args.steps // 4), max(3, args.warmup // 4))
+                pre.append((wp, msp))
+            flops = sum(wp.flops() for wp, _ in pre)
+            t = sum(msp for _, msp in pre)
+            tf = flops / (t * 1e-3) / 1e12
+            result["prefill_tflops"] = round(tf, 2)
+            result["prefill_us_two_chunks"] = round(t * 1e3, 2)
+            result["prefill_roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": F16_PEAK_TFLOPS,
+                                          "unit": "TFLOP/s", "frac": round(tf / F16_PEAK_TFLOPS, 4)}
+            _log(f"prefill: {t * 1e3:.1f} us for 2 chunks, {tf:.1f} TFLOP/s")
+        except sa.SixiAttnError as e:
+            result["prefill_tflops"] = None
+            result["prefill_note"] = f"prefill kernel unavailable: {e}"
+            _log(result["prefill_note"])
 
     if not args.no_cpu:
         _log("CPU baseline (oracle on host cores)")

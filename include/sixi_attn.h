@@ -94,7 +94,8 @@ typedef struct sixi_attn_params {
     float max_bias;         /* ALiBi; 0 = off                                              */
     float logit_softcap;    /* 0 = off                                                     */
     float reserved_f;
-    void* workspace;        /* device scratch of >= sixi_attn_workspace_bytes() bytes      */
+    void* workspace;        /* device scratch of >= sixi_attn_workspace_bytes() bytes,
+                               256-byte aligned; its contents need no initialisation       */
     size_t workspace_bytes;
     void* stream;           /* hipStream_t; NULL = the null stream                         */
 } sixi_attn_params;

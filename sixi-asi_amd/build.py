@@ -34,7 +34,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
-HIP_SOURCES = ["fa_splitk.hip", "fa_prefill.hip", "sixi_attn_abi.cpp"]
+HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "sixi_attn_abi.cpp"]
 
 
 def _hipcc() -> str:

@@ -1,0 +1,673 @@
+// fa_decode.hip -- split-K flash-decoding for single-token decode and speculative verify
+// on gfx950 (head_dim 128, f16 KV).
+//
+// Work decomposition.  A segment is one (stream s, kv-head g): nt_s = ceil(cells_s / 16)
+// tiles of 16 KV cells, and all R = G*q_len_s query rows of the GQA group ride along with
+// every tile, so each K/V byte leaves HBM once for the whole group.  Segments are laid end
+// to end (stream-major, then kv-head) and the P work-groups take equal shares
+// [p*T/P, (p+1)*T/P) of the T tiles ("stream-K"), so any mix of lengths balances over the
+// CUs.  The share of work-group p inside a segment is a piece.  A work-group that owns a
+// whole segment writes the rows directly; every other piece leaves (m, l, O) in a
+// workspace slot, and a second launch (decode_merge) combines the pieces of each split
+// segment in a fixed order.  The kernel boundary orders the two launches, so neither
+// needs device-scope fences or atomics.
+//
+// Every SIMD holds two waves (<= 256 registers each), so one wave's MFMA and memory stalls
+// hide behind the other's VALU work:
+//   RS = 1 (<= 48 rows): two work-groups of four waves per CU (<= 80 KB LDS each); the
+//          waves are independent tile lanes, each with a private two-slot LDS ring, so the
+//          tile loop has no barrier;
+//   RS = 2 (49..96 rows): two work-groups of four waves per CU, each = two tile lanes x two
+//          row groups; the two waves of a lane share a three-slot ring (each stages half of
+//          every tile, two tiles in flight) and the group meets at one barrier a tile.
+// K/V tiles reach LDS by direct global->LDS loads (buffer_load_dwordx4 ... lds), so bytes
+// in flight cost no VGPRs.
+//
+// Per 16-cell tile and wave:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 cells x 32 dims straight from the ring
+//                 (lane (r, c) holds cell r, dims 32ks+8c..+7), B = Q^T from LDS;
+//                 lane (r, c) receives cells 4c..4c+3 of row r;
+//   softmax       row max over the four lane groups with v_permlane{32,16}_swap; the
+//                 exponent reference moves lazily (only when the tile max exceeds it by
+//                 more than 2^8), so the O rescale is rare; p = 2^(s*c - m*c) in one FMA;
+//   O^T += V^T P^T  v_mfma_f32_16x16x16_f16: B = P^T is exactly the lane's own four
+//                 probabilities, A = V^T from an in-register 4x8 16-bit transpose
+//                 (v_perm_b32) of the four 16-byte V rows the lane staged (cells 4c..4c+3,
+//                 dims 8r..8r+7), so output tile tt holds dims 8r + tt.
+// Only the tiles that reach past the first causal boundary (or the stream's end) apply a
+// mask; the rest run the unmasked body.
+#include "fa_device.hpp"
+
+namespace sixi {
+namespace {
+
+constexpr int kTile = kDecodeTile;  // 16 cells
+constexpr int kSlotChunks = 8;      // 4 K chunks (ks) + 4 V chunks (e), 1 KB each
+constexpr int kDmaPerTile = 8;      // 16-byte LDS-DMA loads per lane per tile
+constexpr float kLazyLog2 = 8.0f;   // headroom (log2 units) before the exponent reference moves
+
+enum { MODE_FAST = 0, MODE_GENERIC = 1 };
+
+template <int RS> struct Shape;
+template <> struct Shape<1> { static constexpr int waves = 4, lanes = 4, slots = 2, groups_per_cu = 2; };
+template <> struct Shape<2> { static constexpr int waves = 4, lanes = 2, slots = 3, groups_per_cu = 2; };
+
+template <int NT, int NS>
+struct MergeBuf {
+    f32x4 o[NS][NT * 8 * 64];  // [slot][n*8 + tt][lane]
+    float m[NS][NT * 64];
+    float l[NS][NT * 64];
+};
+
+// NTW = row tiles per wave, RS = row groups (waves that share a tile).
+template <int NTW, int RS>
+struct DecodeLds {
+    union {
+        struct {
+            u32x4 ring[Shape<RS>::lanes * Shape<RS>::slots * kSlotChunks * 64];
+            u32x4 q[NTW * RS * 4 * 64];  // Q^T B operands: [row tile][ks][lane], 8 f16 each
+        } t;
+        MergeBuf<NTW, RS * Shape<RS>::lanes / 2> mg;  // reused after the tile loop
+    };
+    int ps[kMaxStreams + 1];
+};
+
+template <int NT>
+struct Acc {
+    f32x4 o[8][NT];  // O^T tiles: lane (r,c) holds row 16n+r, dims 32c + 8i + t at o[t][n][i]
+    float m[NT];     // exponent reference: raw score (FAST) or log2 units (GENERIC, merged)
+    float l[NT];     // this lane's share of the row sum until the end of the tile loop
+};
+
+template <int NT>
+__device__ __forceinline__ void acc_clear(Acc<NT>& acc) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        acc.m[n] = neg_inf();
+        acc.l[n] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc.o[t][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+// (m, l, O) <- merge of (m, l, O) and (m2, l2, O2), log2-domain references.
+template <int K>
+__device__ __forceinline__ void merge_row(float& m, float& l, f32x4* o, float m2, float l2,
+                                          const f32x4* o2) {
+    const float mn = fmaxf(m, m2);
+    const float ms = (mn == neg_inf()) ? 0.0f : mn;
+    const float a1 = fast_exp2(m - ms);
+    const float a2 = fast_exp2(m2 - ms);
+    l = l * a1 + l2 * a2;
+    m = mn;
+#pragma unroll
+    for (int t = 0; t < K; ++t) o[t] = o[t] * a1 + o2[t] * a2;
+}
+
+template <int NT, int NS>
+__device__ __forceinline__ void acc_to_lds(MergeBuf<NT, NS>& mg, int slot, const Acc<NT>& acc, int lane) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) mg.o[slot][(n * 8 + t) * 64 + lane] = acc.o[t][n];
+        mg.m[slot][n * 64 + lane] = acc.m[n];
+        mg.l[slot][n * 64 + lane] = acc.l[n];
+    }
+}
+
+template <int NT, int NS>
+__device__ __forceinline__ void acc_merge_lds(const MergeBuf<NT, NS>& mg, int slot, Acc<NT>& acc, int lane) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        f32x4 o[8], o2[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            o[t] = acc.o[t][n];
+            o2[t] = mg.o[slot][(n * 8 + t) * 64 + lane];
+        }
+        merge_row<8>(acc.m[n], acc.l[n], o, mg.m[slot][n * 64 + lane], mg.l[slot][n * 64 + lane], o2);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc.o[t][n] = o[t];
+    }
+}
+
+// Merges the tile lanes of each row group into tile lane 0: with four lanes (2,3) -> (0,1)
+// then 1 -> 0, with two lanes 1 -> 0.  Every wave must call it.  Returns whether this wave
+// owns its rows afterwards.
+template <int NTW, int RS, int NS>
+__device__ __forceinline__ bool merge_lanes(MergeBuf<NTW, NS>& mg, Acc<NTW>& acc, int rg, int tl, int lane) {
+    constexpr int TL = Shape<RS>::lanes;
+    constexpr int H = TL / 2;  // merge slots per row group
+    if (TL == 4) {
+        if (tl >= 2) acc_to_lds(mg, H * rg + tl - 2, acc, lane);
+        __syncthreads();
+        if (tl < 2) acc_merge_lds(mg, H * rg + tl, acc, lane);
+        __syncthreads();
+    }
+    if (tl == 1) acc_to_lds(mg, H * rg, acc, lane);
+    __syncthreads();
+    if (tl == 0) acc_merge_lds(mg, H * rg, acc, lane);
+    return tl == 0;
+}
+
+// Inclusive tile prefix over streams into ps[0..S] (run by one wave).
+__device__ void build_tile_prefix(const FaArgs& a, int* ps) {
+    const int lane = threadIdx.x & 63;
+    if (lane == 0) ps[0] = 0;
+    int carry = 0;
+    for (int base = 0; base < a.S; base += 64) {
+        const int s = base + lane;
+        int x = 0;
+        if (s < a.S) x = (stream_dims(a, s).nc + kTile - 1) / kTile;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        if (s < a.S) ps[s + 1] = carry + x;
+        carry += __shfl(x, 63, 64);
+    }
+}
+
+// Per-piece constants of one lane.
+template <int NT>
+struct RowInfo {
+    int vis[NT];     // cells visible to the lane's row of tile n (non-explicit masks)
+    int j[NT];       // block row of the lane's row of tile n
+    float slope[NT]; // ALiBi slope (explicit masks)
+};
+
+// max over three floats in one instruction (no NaN canonicalisation around it)
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// One 16-cell tile from a staged ring slot.  MASKED applies the visibility of each row;
+// `after_reads` runs once the slot's LDS reads are consumed.  The phases run over all row
+// tiles at once (every QK^T, then every row max, one rare rescale branch, then every
+// exponential and PV), so each phase offers the scheduler NT independent chains.
+template <int NT, int MODE, bool MASKED, typename F>
+__device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT>& acc, const u32x4* slot,
+                                          const u32x4* qs, int c0, const RowInfo<NT>& ri,
+                                          const char* mrow, int nc, int lane, F&& after_reads) {
+    const int c = lane >> 4;
+
+    f16x8 kop[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kop[ks] = as_f16x8(slot[ks * 64 + lane]);
+    u32x4 vr[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vr[e] = slot[(4 + e) * 64 + lane];
+
+    // ---- S^T = K Q^T for every row tile ----
+    f32x4 st[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        st[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) st[n] = mfma16x16x32(kop[ks], as_f16x8(qs[(n * 4 + ks) * 64 + lane]), st[n]);
+    }
+    after_reads();
+
+    // V^T operands: tile tt holds dim 8r + tt of cells 4c..4c+3
+    u32x2 vt[8];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+        const int d2 = tt >> 1;
+        const uint32_t sel = (tt & 1) ? 0x07060302u : 0x05040100u;
+        vt[tt][0] = __builtin_amdgcn_perm(vr[1][d2], vr[0][d2], sel);
+        vt[tt][1] = __builtin_amdgcn_perm(vr[3][d2], vr[2][d2], sel);
+    }
+
+    // ---- scores (FAST: raw dot products; GENERIC: log2-domain logits) and row maxima ----
+    const float c2 = a.scale_log2;
+    float sv[NT][4];
+    float mx[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int cell = c0 + 4 * c + e;
+            float x = st[n][e];
+            if (MODE == MODE_GENERIC) {
+                x *= a.scale;
+                if (a.softcap != 0.0f) x = a.softcap * tanhf(x);
+                if (a.mask) {
+                    float mv = neg_inf();
+                    if (cell < nc) {
+                        const uint16_t bits = *reinterpret_cast<const uint16_t*>(
+                            mrow + (int64_t)ri.j[n] * a.m_nb1 + (int64_t)cell * 2);
+                        mv = ri.slope[n] * half_bits_to_float(bits);
+                    }
+                    x = (mv == neg_inf()) ? neg_inf() : x + mv;
+                } else if (cell >= ri.vis[n]) {
+                    x = neg_inf();
+                }
+                x *= kLog2e;
+            } else if (MASKED) {
+                if (cell >= ri.vis[n]) x = neg_inf();
+            }
+            sv[n][e] = x;
+        }
+        mx[n] = max4_rowgroups(max3f(sv[n][0], sv[n][1], fmaxf(sv[n][2], sv[n][3])));
+    }
+
+    // ---- lazy exponent reference: move it only when the tile max exceeds it by 2^8 ----
+    // (the first tile of a piece always moves it; O and l are zero then)
+    const float thr = (MODE == MODE_FAST) ? kLazyLog2 / c2 : kLazyLog2;
+    bool need[NT];
+    bool need_any = false;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        need[n] = mx[n] > acc.m[n] + thr;
+        need_any |= need[n];
+    }
+    if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            float alpha = 1.0f;
+            if (need[n]) {
+                alpha = fast_exp2((MODE == MODE_FAST) ? (acc.m[n] - mx[n]) * c2 : acc.m[n] - mx[n]);
+                acc.m[n] = mx[n];
+            }
+            acc.l[n] *= alpha;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc.o[t][n] *= alpha;
+        }
+    }
+
+    // ---- probabilities (f32 row sums, f16 MFMA operand) and O^T += V^T P^T ----
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const float ref = acc.m[n];
+        const float mc = (ref == neg_inf()) ? 0.0f : ((MODE == MODE_FAST) ? ref * c2 : ref);
+        f16x4 pf;
+        float ps[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            ps[e] = fast_exp2((MODE == MODE_FAST) ? fmaf(sv[n][e], c2, -mc) : sv[n][e] - mc);
+            pf[e] = (_Float16)ps[e];
+        }
+        acc.l[n] += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+
+        if (MODE == MODE_GENERIC && a.mask) {
+            // explicit masks: a cell that none of these 16 rows sees may hold NaN bits, so
+            // its V^T column is zeroed for them (0 * NaN must not reach the accumulator)
+            uint32_t keep[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint64_t b0 = __builtin_amdgcn_ballot_w64((float)pf[2 * h] != 0.0f);
+                const uint64_t b1 = __builtin_amdgcn_ballot_w64((float)pf[2 * h + 1] != 0.0f);
+                keep[h] = ((((b0 >> (16 * c)) & 0xffffull) != 0) ? 0x0000ffffu : 0u) |
+                          ((((b1 >> (16 * c)) & 0xffffull) != 0) ? 0xffff0000u : 0u);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                const u32x2 vm = {vt[tt][0] & keep[0], vt[tt][1] & keep[1]};
+                acc.o[tt][n] = mfma16x16x16(__builtin_bit_cast(f16x4, vm), pf, acc.o[tt][n]);
+            }
+        } else {
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt)
+                acc.o[tt][n] = mfma16x16x16(__builtin_bit_cast(f16x4, vt[tt]), pf, acc.o[tt][n]);
+        }
+    }
+}
+
+// Writes the normalised rows of row tiles n0 .. n0+NT-1 held by this lane.
+template <int NT>
+__device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT>& acc, int n0, int s, int g,
+                                           int R, int lane) {
+    const int r = lane & 15, c = lane >> 4;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        if (row >= R) continue;
+        const int j = row / a.G;
+        const int h = g * a.G + row % a.G;
+        const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
+        char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + c * 32 * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            st16(dst + i * 32, f32x4{acc.o[0][n][i], acc.o[1][n][i], acc.o[2][n][i], acc.o[3][n][i]} * inv);
+            st16(dst + i * 32 + 16, f32x4{acc.o[4][n][i], acc.o[5][n][i], acc.o[6][n][i], acc.o[7][n][i]} * inv);
+        }
+    }
+}
+
+// Partial slot of `rows_slot` rows: unnormalised O rows [row][128] f32, then m[row], l[row]
+// (log2-domain references).
+template <int NT>
+__device__ __forceinline__ void write_partial(float* slot, int rows_slot, int n0, int R, const Acc<NT>& acc,
+                                              int lane) {
+    const int r = lane & 15, c = lane >> 4;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        if (row >= R) continue;
+        char* dst = reinterpret_cast<char*>(slot + (int64_t)row * 128) + c * 32 * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            st16(dst + i * 32, f32x4{acc.o[0][n][i], acc.o[1][n][i], acc.o[2][n][i], acc.o[3][n][i]});
+            st16(dst + i * 32 + 16, f32x4{acc.o[4][n][i], acc.o[5][n][i], acc.o[6][n][i], acc.o[7][n][i]});
+        }
+        if (c == 0) {
+            slot[(int64_t)rows_slot * 128 + row] = acc.m[n];
+            slot[(int64_t)rows_slot * 129 + row] = acc.l[n];
+        }
+    }
+}
+
+// Work-group-uniform description of one piece.
+struct Piece {
+    int s, g, tb, te, nt_seg;
+    int64_t slot;  // partial slot (segment + logical work-group)
+};
+
+// One piece: tiles [tb, te) of segment (s, g).
+template <int NTW, int RS, int MODE>
+__device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS>& sh, int causal, const Piece& pc) {
+    constexpr int NTOT = NTW * RS;
+    constexpr int TL = Shape<RS>::lanes;       // tile lanes
+    constexpr int NSLOT = Shape<RS>::slots;
+    constexpr int NTHREADS = Shape<RS>::waves * 64;
+    constexpr int DMA = kDmaPerTile / RS;      // LDS-DMA loads per tile per wave
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int rg = w / TL;
+    const int tl = w % TL;
+    const int r = lane & 15;
+    const int c = lane >> 4;
+    const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
+    const StreamDims sd = stream_dims(a, s);
+    const int G = a.G;
+    const int R = G * sd.ql;
+    const int n0 = rg * NTW;  // first row tile of this wave
+
+    // ---- Q rows of the group -> f16 B operands in LDS (row 16n+r, dims 32ks+8c..+7) ----
+    for (int idx = tid; idx < NTOT * 16 * 16; idx += NTHREADS) {
+        const int row = idx >> 4;
+        const int chunk = idx & 15;  // 8-dim chunk: ks = chunk/4, c = chunk%4
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (row < R) {
+            const int j = row / G;
+            const int h = g * G + row % G;
+            const char* src = a.q + (int64_t)j * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3 +
+                              (int64_t)chunk * 8 * a.q_es;
+            f16x8 hv;
+            if (a.q_f16) {
+                hv = as_f16x8(ld16(src));
+            } else {
+                const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
+                const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hv[e] = (_Float16)lo[e];
+                    hv[4 + e] = (_Float16)hi[e];
+                }
+            }
+            val = as_u32x4(hv);
+        }
+        const int n = row >> 4, rr = row & 15, ks = chunk >> 2, cc = chunk & 3;
+        sh.t.q[(n * 4 + ks) * 64 + cc * 16 + rr] = val;
+    }
+    __syncthreads();
+
+    RowInfo<NTW> ri;
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        const bool valid = row < R;
+        const int j = valid ? row / G : 0;
+        ri.j[n] = j;
+        ri.vis[n] = (valid && causal) ? sd.kl + j + 1 : sd.nc;
+        ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, g * G + (valid ? row % G : 0)) : 1.0f;
+    }
+    // tiles below t_full see no masked cell for any row
+    const int t_full = (MODE == MODE_GENERIC) ? 0 : (causal ? (sd.kl + 1) / kTile : sd.nc / kTile);
+    const char* mrow = nullptr;
+    if (MODE == MODE_GENERIC && a.mask) mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3;
+    const u32x4* qs = sh.t.q + n0 * 4 * 64;
+
+    Acc<NTW> acc;
+    acc_clear(acc);
+
+    // K/V of this (stream, kv-head) through range-checked buffer resources: cells >= nc read
+    // as zeros (and are masked), so the tail tile needs no clamping and cannot fault.
+    const int64_t rowb = 128 * 2;
+    const i32x4 krs = make_rsrc_sgpr(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
+                                     (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + rowb));
+    const i32x4 vrs = make_rsrc_sgpr(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
+                                     (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + rowb));
+    const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
+
+    // tiles of this lane: tb + tl + TL*i, i < n_my; n_iter is the same for the whole group
+    const int t0 = tb + tl;
+    const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
+    const int n_iter = (te - tb + TL - 1) / TL;
+    u32x4* ring = sh.t.ring + (size_t)tl * NSLOT * kSlotChunks * 64;
+    const uint32_t ring_base = lds_addr(ring);
+
+    // Stage tile i of this lane into slot i % NSLOT.  RS = 1: all 8 chunks; RS = 2: row
+    // group 0 stages the 4 K chunks and row group 1 the 4 V chunks.
+    auto issue = [&](int i) {
+        const uint32_t c0 = (uint32_t)(t0 + i * TL) * kTile;
+        const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * (kSlotChunks * 1024);
+        if (RS == 1 || rg == 0) {
+            const uint32_t off = (c0 + r) * knb + c * 16;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) dma16_to_lds(krs, off + ks * 64, base + ks * 1024);
+        }
+        if (RS == 1 || rg == 1) {
+            const uint32_t vo = (c0 + 4 * c) * vnb + r * 16;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dma16_to_lds(vrs, vo + e * vnb, base + (4 + e) * 1024);
+        }
+    };
+    auto step = [&](int i, auto&& after_reads) {
+        const u32x4* slot = ring + (i % NSLOT) * (kSlotChunks * 64);
+        const int t = t0 + i * TL;
+        if (t < t_full)
+            tile_step<NTW, MODE, false>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
+        else
+            tile_step<NTW, MODE, true>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
+    };
+
+    if constexpr (RS == 1) {
+        // private ring: the slot just read is refilled with tile i+2
+        if (n_my > 0) issue(0);
+        if (n_my > 1) issue(1);
+#pragma unroll 1
+        for (int i = 0; i < n_my; ++i) {
+            if (i + 1 < n_my) wait_vmcnt<DMA>();
+            else wait_vmcnt<0>();
+            step(i, [&] {
+                wait_lgkmcnt0();
+                if (i + 2 < n_my) issue(i + 2);
+            });
+        }
+    } else {
+        // shared ring: tile i+NSLOT-1 goes into the slot of tile i-1, which both readers
+        // left before the barrier of iteration i
+        static_assert(NSLOT == 3 || NSLOT == 4, "ring depth");
+#pragma unroll
+        for (int i = 0; i < NSLOT - 1; ++i)
+            if (i < n_my) issue(i);
+#pragma unroll 1
+        for (int i = 0; i < n_iter; ++i) {
+            const int ahead = n_my - 1 - i;  // own tiles issued after tile i
+            if (NSLOT == 4 && ahead >= 2) wait_vmcnt<2 * DMA>();
+            else if (ahead >= 1) wait_vmcnt<DMA>();
+            else wait_vmcnt<0>();
+            __syncthreads();
+            if (i + NSLOT - 1 < n_my) issue(i + NSLOT - 1);
+            if (i < n_my) step(i, [] {});
+        }
+    }
+
+    // row sums over the lane groups; FAST references to log2 units for merging
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) {
+        acc.l[n] = sum4_rowgroups(acc.l[n]);
+        if (MODE == MODE_FAST && acc.m[n] != neg_inf()) acc.m[n] *= a.scale_log2;
+    }
+
+    __syncthreads();  // every wave is past its ring (each drained its own loads)
+    if (merge_lanes<NTW, RS>(sh.mg, acc, rg, tl, lane)) {
+        if (tb == 0 && te == pc.nt_seg)
+            write_rows(a, acc, n0, s, g, R, lane);
+        else
+            write_partial(a.part + pc.slot * a.slot_floats, NTOT * 16, n0, R, acc, lane);
+    }
+    __syncthreads();  // LDS (q, merge buffers, rings) is reused by the next piece
+}
+
+// Work-group -> tile range.  Returns false for a work-group without tiles.
+struct Partition {
+    int64_t T, P, x0, x1;
+    int p_log;
+};
+
+__device__ __forceinline__ bool partition(const FaArgs& a, const int* ps, int b, Partition& pt) {
+    pt.T = (int64_t)a.Hkv * ps[a.S];
+    pt.P = pt.T < a.P ? pt.T : a.P;  // active work-groups: every one owns >= 1 tile
+    // logical index: with the remap, consecutive tile ranges land on one XCD (work-groups
+    // are dealt round-robin over the XCDs)
+    pt.p_log = a.xcd_remap ? (b % kXcds) * (a.P / kXcds) + b / kXcds : b;
+    if (pt.p_log >= pt.P) return false;
+    pt.x0 = pt.p_log * pt.T / pt.P;
+    pt.x1 = (pt.p_log + 1) * pt.T / pt.P;
+    return true;
+}
+
+template <int NTW, int RS, int MODE>
+__global__ __launch_bounds__(Shape<RS>::waves * 64, Shape<RS>::groups_per_cu) void decode_f16_d128(FaArgs a,
+                                                                                                 int causal) {
+    __shared__ DecodeLds<NTW, RS> sh;
+    const int tid = threadIdx.x;
+    if (tid < 64) build_tile_prefix(a, sh.ps);
+    __syncthreads();
+    Partition pt;
+    if (!partition(a, sh.ps, blockIdx.x, pt)) return;
+    const int64_t Hkv = a.Hkv;
+
+    // stream holding tile x0: the largest s with Hkv*ps[s] <= x0
+    int lo = 0, hi = a.S;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (Hkv * sh.ps[mid] <= pt.x0) lo = mid; else hi = mid - 1;
+    }
+    int s = lo;
+    int64_t x = pt.x0;
+    while (x < pt.x1) {
+        while (Hkv * sh.ps[s + 1] <= x) ++s;
+        const int nt = sh.ps[s + 1] - sh.ps[s];
+        const int64_t cs = Hkv * sh.ps[s];
+        const int g = (int)((x - cs) / nt);
+        const int64_t ck = cs + (int64_t)g * nt;
+        Piece pc;
+        pc.s = s;
+        pc.g = g;
+        pc.tb = (int)(x - ck);
+        pc.te = (int)(min(pt.x1, ck + nt) - ck);
+        pc.nt_seg = nt;
+        pc.slot = (int64_t)s * Hkv + g + pt.p_log;
+        decode_piece<NTW, RS, MODE>(a, sh, causal, pc);
+        x = ck + pc.te;
+    }
+}
+
+// Combines the pieces of every segment that more than one work-group touched, in the order
+// of the work-groups.  grid = (S*Hkv segments, row blocks of 8); 256 threads = 8 rows x 32
+// four-dim chunks, so every (row, chunk) is one thread.
+__global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
+    __shared__ int ps[kMaxStreams + 1];
+    if (threadIdx.x < 64) build_tile_prefix(a, ps);
+    __syncthreads();
+    const int64_t k = blockIdx.x;
+    const int s = (int)(k / a.Hkv);
+    const int g = (int)(k % a.Hkv);
+    const int nt = ps[s + 1] - ps[s];
+    if (nt == 0) return;
+    const int64_t T = (int64_t)a.Hkv * ps[a.S];
+    const int64_t P = T < a.P ? T : a.P;
+    const int64_t ck = (int64_t)a.Hkv * ps[s] + (int64_t)g * nt;
+    const int64_t p_first = ((ck + 1) * P - 1) / T;
+    const int64_t p_last = ((ck + nt) * P - 1) / T;
+    if (p_first == p_last) return;  // written whole by its only work-group
+
+    const StreamDims sd = stream_dims(a, s);
+    const int row = blockIdx.y * 8 + (threadIdx.x >> 5);
+    if (row >= a.G * sd.ql) return;
+    const int d0 = (threadIdx.x & 31) * 4;
+    const float* base = a.part + k * a.slot_floats;
+    float M = neg_inf(), L = 0.0f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    int64_t p = p_first;
+    // two pieces per step: their loads are independent and overlap
+    for (; p + 1 <= p_last; p += 2) {
+        const float* s0 = base + p * a.slot_floats;
+        const float* s1 = s0 + a.slot_floats;
+        const f32x4 o0 = *reinterpret_cast<const f32x4*>(s0 + (int64_t)row * 128 + d0);
+        const f32x4 o1 = *reinterpret_cast<const f32x4*>(s1 + (int64_t)row * 128 + d0);
+        const float m0 = s0[(int64_t)rows_slot * 128 + row], l0 = s0[(int64_t)rows_slot * 129 + row];
+        const float m1 = s1[(int64_t)rows_slot * 128 + row], l1 = s1[(int64_t)rows_slot * 129 + row];
+        merge_row<1>(M, L, &o, m0, l0, &o0);
+        merge_row<1>(M, L, &o, m1, l1, &o1);
+    }
+    if (p <= p_last) {
+        const float* s0 = base + p * a.slot_floats;
+        const f32x4 o0 = *reinterpret_cast<const f32x4*>(s0 + (int64_t)row * 128 + d0);
+        merge_row<1>(M, L, &o, s0[(int64_t)rows_slot * 128 + row], s0[(int64_t)rows_slot * 129 + row], &o0);
+    }
+    const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+    const int j = row / a.G;
+    const int h = g * a.G + row % a.G;
+    st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
+}
+
+template <int NTW, int RS>
+hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
+    const dim3 grid(a.P), block(Shape<RS>::waves * 64);
+    if (generic)
+        hipLaunchKernelGGL((decode_f16_d128<NTW, RS, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+    else
+        hipLaunchKernelGGL((decode_f16_d128<NTW, RS, MODE_FAST>), grid, block, 0, stream, a, causal);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int rows_slot = NTW * RS * 16;
+    hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
+                       a, rows_slot);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
+    const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + kTile - 1) / kTile);
+    const int per_cu = row_tiles <= 3 ? Shape<1>::groups_per_cu : Shape<2>::groups_per_cu;
+    int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
+    if (P > kMaxSplitGroups) P = kMaxSplitGroups;
+    if (P > tiles_max) P = tiles_max;
+    return (int)(P < 1 ? 1 : P);
+}
+
+hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
+                         hipStream_t stream) {
+    if (kv_type != SIXI_TYPE_F16 || head_dim != 128) return hipErrorNotSupported;
+    const bool generic = mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f;
+    const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
+    switch (row_tiles) {
+        case 1: return launch_nt<1, 1>(a, generic, causal, stream);
+        case 2: return launch_nt<2, 1>(a, generic, causal, stream);
+        case 3: return launch_nt<3, 1>(a, generic, causal, stream);
+        case 4: return launch_nt<2, 2>(a, generic, causal, stream);
+        case 6: return launch_nt<3, 2>(a, generic, causal, stream);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace sixi

@@ -29,6 +29,12 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// D = A(16x16) * B(16x16) + C on f16 inputs, f32 accumulate.  Lane l supplies row l%16
+// of A (resp. column l%16 of B) at k = 4*(l/16) .. +3, and receives D[4*(l/16)+i][l%16].
+__device__ __forceinline__ f32x4 mfma16x16x16(f16x4 a, f16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
 // Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return 0, so the
 // tail of a stream needs no clamping and can never fault.  Word 3 = 0x00020000 is the
 // gfx9-family raw-buffer format.
@@ -98,16 +104,20 @@ __device__ __forceinline__ u32x4 ld16(const char* p) {
 }
 __device__ __forceinline__ void st16(char* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
-// Max over the four lanes l, l^16, l^32, l^48 (one MFMA column's row groups).
+// Reductions over the four lanes l, l^16, l^32, l^48 (the lane groups of one MFMA column)
+// with the gfx950 row-swap permutes (VALU only, no LDS round trip).  Each swap returns both
+// halves, so max/sum of the pair is the reduction over {l, l^32} (resp. {l, l^16}).
 __device__ __forceinline__ float max4_rowgroups(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16, 64));
-    x = fmaxf(x, __shfl_xor(x, 32, 64));
-    return x;
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum4_rowgroups(float x) {
-    x += __shfl_xor(x, 16, 64);
-    x += __shfl_xor(x, 32, 64);
-    return x;
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Per-stream extents resolved on the device from the length arrays.

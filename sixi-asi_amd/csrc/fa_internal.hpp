@@ -40,24 +40,34 @@ struct FaArgs {
     int32_t alibi_nlog2;   // 0 = ALiBi off
 
     // split-K bookkeeping (workspace)
-    float* part;           // partial slots: [slot][rows_max*D] O, then [rows_max] m, [rows_max] l
-    int32_t* meta;         // [S+1] tile prefix over streams, written by work-group 0
+    float* part;           // partial slots of slot_floats floats: O rows [rows][128], then m, l
     int32_t P;             // work-groups of the split-K launch
-    int32_t rows_max;      // G * n_q rounded up to 16
-    int64_t slot_floats;   // floats per slot
+    int32_t xcd_remap;     // 1: consecutive tile ranges go to work-groups of one XCD
+    int64_t slot_floats;   // floats per partial slot
 };
 
-// Host-side launchers (defined in the .hip files).
-hipError_t launch_splitk(const FaArgs& a, int kv_type, int mask_mode, int head_dim,
+// Host-side launchers (defined in the .hip files).  hipErrorNotSupported = not built.
+hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream);
 hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim,
                           hipStream_t stream);
 
 // Sizing rules shared by the dispatcher and the launchers.
-constexpr int kSplitTile = 32;        // KV cells per wave step of the split-K kernel
-constexpr int kSplitWaves = 4;        // waves per split-K work-group
-constexpr int kMaxStreams = 1024;     // LDS prefix table bound
-constexpr int kMaxSplitGroups = 1024; // work-groups of a split-K launch (workspace bound)
-int splitk_num_groups(const FaArgs& a, int cu_count);
+constexpr int kDecodeTile = 16;        // KV cells per wave step of the decode kernel
+constexpr int kDecodeMaxRowTiles = 6;  // 16-row MFMA tiles per (stream, kv-head): G*q_len <= 96
+constexpr int kMaxStreams = 512;       // LDS prefix table bound
+constexpr int kMaxSplitGroups = 2048;  // work-groups of a split-K launch (workspace bound)
+constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
+int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles);
+// Row tiles the decode kernel runs for `rows` = G * n_q rows: up to 3 per wave; beyond
+// that two row groups of equal size (so 5 tiles run as 6).
+inline int decode_row_tiles(int64_t rows) {
+    const int rt = (int)((rows + 15) / 16);
+    return rt <= 3 ? rt : 2 * ((rt + 1) / 2);
+}
+inline int64_t decode_slot_floats(int row_tiles) {
+    // O rows [16*row_tiles][128] f32, then m and l per row
+    return (int64_t)row_tiles * 16 * (128 + 2);
+}
 
 }  // namespace sixi

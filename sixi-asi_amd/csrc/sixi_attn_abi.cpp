@@ -1,5 +1,5 @@
 // sixi_attn_abi.cpp -- the C ABI of include/sixi_attn.h: validation, workspace sizing and
-// kernel choice on the host; the kernels themselves live in fa_splitk.hip and
+// kernel choice on the host; the kernels themselves live in fa_decode.hip and
 // fa_prefill.hip.
 //
 // Errors follow the reference's convention of returning a status instead of aborting
@@ -20,7 +20,7 @@ using sixi::FaArgs;
 
 constexpr size_t kWsAlign = 256;
 constexpr int kMaxHeadDim = 128;       // head dims built for gfx950 in this library
-constexpr int kSplitMaxRows = 96;      // G * n_q handled by the split-K kernel
+constexpr int kSplitMaxRows = 16 * sixi::kDecodeMaxRowTiles;  // G * n_q of the split-K kernel
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -59,8 +59,8 @@ struct Plan {
     int mask_mode = 0;
     int D = 0;
     bool splitk = true;
+    int row_tiles = 0;
     size_t ws_bytes = 0;
-    size_t meta_bytes = 0;
 };
 
 int cu_count_cached() {
@@ -116,9 +116,9 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     const int64_t kvrow = row_bytes(k.type, D);
     if (k.nb[1] < kvrow || v.nb[1] < kvrow) return SIXI_E_INVALID_ARGUMENT;  // rows must not overlap
     if (o.nb[1] < D * 4 || q.nb[1] < D * qes) return SIXI_E_INVALID_ARGUMENT;
-    // one stream's cells are addressed with 32-bit offsets
+    // one stream's cells (plus one tile of read-ahead) are addressed with 32-bit offsets
     int64_t kspan = 0, vspan = 0;
-    if (!mul_ok(n_kv, k.nb[1], &kspan) || !mul_ok(n_kv, v.nb[1], &vspan) ||
+    if (!mul_ok(n_kv + sixi::kDecodeTile, k.nb[1], &kspan) || !mul_ok(n_kv + sixi::kDecodeTile, v.nb[1], &vspan) ||
         kspan >= (int64_t)UINT32_MAX || vspan >= (int64_t)UINT32_MAX)
         return SIXI_E_UNSUPPORTED;
     if (view_span(q, D * qes) < 0 || view_span(k, kvrow) < 0 || view_span(v, kvrow) < 0 ||
@@ -187,11 +187,10 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.splitk = rows <= kSplitMaxRows;
     if (!pl.splitk) return SIXI_E_UNSUPPORTED;  // prefill kernel not built yet
 
-    a.rows_max = (int32_t)align_up((size_t)rows, 16);
-    a.slot_floats = (int64_t)a.rows_max * D + 2 * (int64_t)a.rows_max;
-    pl.meta_bytes = align_up(sizeof(int32_t) * (size_t)(S + 1), kWsAlign);
+    pl.row_tiles = sixi::decode_row_tiles(rows);
+    a.slot_floats = sixi::decode_slot_floats(pl.row_tiles);
     const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
-    pl.ws_bytes = pl.meta_bytes + align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
+    pl.ws_bytes = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
     *out = pl;
     return SIXI_OK;
 }
@@ -222,13 +221,13 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     if (!aligned(p->workspace, kWsAlign)) return SIXI_E_ALIGNMENT;
     FaArgs& a = pl.a;
     char* ws = static_cast<char*>(p->workspace);
-    a.meta = reinterpret_cast<int32_t*>(ws);
-    a.part = reinterpret_cast<float*>(ws + pl.meta_bytes);
+    a.part = reinterpret_cast<float*>(ws);
     hipStream_t stream = static_cast<hipStream_t>(p->stream);
     hipError_t e;
     if (pl.splitk) {
-        a.P = sixi::splitk_num_groups(a, cu_count_cached());
-        e = sixi::launch_splitk(a, pl.kv_type, pl.mask_mode, pl.D, stream);
+        a.P = sixi::decode_num_groups(a, cu_count_cached(), pl.row_tiles);
+        a.xcd_remap = 0;
+        e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D, pl.row_tiles, stream);
     } else {
         e = sixi::launch_prefill(a, pl.kv_type, pl.mask_mode, pl.D, stream);
     }

@@ -126,14 +126,18 @@ def test_mask_none_matches_ggml_without_mask(fa):
     assert m["max_abs"] <= MAX_ABS and m["rel_l2"] <= REL_L2
 
 
-def test_explicit_llama_mask_equals_block_causal_bitwise(fa):
+def test_explicit_llama_mask_matches_block_causal(fa):
+    """The ggml-style explicit mask (general path: logits in log2 units, per-cell mask
+    reads) and the block-causal lengths (fast path) select the same cells: both agree with
+    the oracle and with each other far inside the parity bar."""
     _say("explicit llama mask vs block-causal")
     w, host, dev = _small()
     a = _run(fa, w, dev)
     n_kv = dev["k"].shape[1]
     mask = torch.from_numpy(oracle.build_kq_mask(n_kv, w.n_q, w.kv_len, w.q_len, True)).view(torch.float16).cuda()
     b = _run(fa, w, dev, mask_mode=sa.MASK_EXPLICIT, mask=mask)
-    assert np.array_equal(a, b)
+    _check(w, host, b, label="explicit mask")
+    assert np.max(np.abs(a - b)) <= 1e-3
 
 
 def test_repeatable_bitwise_over_20_launches(fa):
