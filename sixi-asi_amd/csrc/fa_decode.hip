@@ -45,6 +45,7 @@ constexpr int kTile = kDecodeTile;  // 16 cells
 constexpr int kSlotChunks = 8;      // 4 K chunks (ks) + 4 V chunks (e), 1 KB each
 constexpr int kDmaPerTile = 8;      // 16-byte LDS-DMA loads per lane per tile
 constexpr float kLazyLog2 = 8.0f;   // headroom (log2 units) before the exponent reference moves
+constexpr int kMaxPieces = 16;      // target bound on the pieces of one full-length segment
 
 enum { MODE_FAST = 0, MODE_GENERIC = 1 };
 
@@ -606,22 +607,21 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    int64_t p = p_first;
-    // two pieces per step: their loads are independent and overlap
-    for (; p + 1 <= p_last; p += 2) {
-        const float* s0 = base + p * a.slot_floats;
-        const float* s1 = s0 + a.slot_floats;
-        const f32x4 o0 = *reinterpret_cast<const f32x4*>(s0 + (int64_t)row * 128 + d0);
-        const f32x4 o1 = *reinterpret_cast<const f32x4*>(s1 + (int64_t)row * 128 + d0);
-        const float m0 = s0[(int64_t)rows_slot * 128 + row], l0 = s0[(int64_t)rows_slot * 129 + row];
-        const float m1 = s1[(int64_t)rows_slot * 128 + row], l1 = s1[(int64_t)rows_slot * 129 + row];
-        merge_row<1>(M, L, &o, m0, l0, &o0);
-        merge_row<1>(M, L, &o, m1, l1, &o1);
-    }
-    if (p <= p_last) {
-        const float* s0 = base + p * a.slot_floats;
-        const f32x4 o0 = *reinterpret_cast<const f32x4*>(s0 + (int64_t)row * 128 + d0);
-        merge_row<1>(M, L, &o, s0[(int64_t)rows_slot * 128 + row], s0[(int64_t)rows_slot * 129 + row], &o0);
+    // four pieces per step: their loads are independent and overlap
+    for (int64_t p0 = p_first; p0 <= p_last; p0 += 4) {
+        f32x4 ov[4];
+        float mv[4], lv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t p = p0 + u <= p_last ? p0 + u : p_last;
+            const float* sl = base + p * a.slot_floats;
+            ov[u] = *reinterpret_cast<const f32x4*>(sl + (int64_t)row * 128 + d0);
+            mv[u] = sl[(int64_t)rows_slot * 128 + row];
+            lv[u] = sl[(int64_t)rows_slot * 129 + row];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (p0 + u <= p_last) merge_row<1>(M, L, &o, mv[u], lv[u], &ov[u]);
     }
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;
     const int j = row / a.G;
@@ -652,6 +652,10 @@ int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
     int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
     if (P > kMaxSplitGroups) P = kMaxSplitGroups;
     if (P > tiles_max) P = tiles_max;
+    // at most about kMaxPieces pieces per segment when the segments are full: more split
+    // work-groups would only lengthen the merge of a few long streams
+    const int64_t cap = (int64_t)kMaxPieces * a.S * a.Hkv;
+    if (P > cap) P = cap;
     return (int)(P < 1 ? 1 : P);
 }
 

@@ -1,8 +1,351 @@
-// fa_prefill.hip -- causal prefill / large verify blocks on gfx950 MFMA.
+// fa_prefill.hip -- chunked causal prefill (and any block of more than 96 rows per GQA group)
+// on gfx950 f16 MFMA (head_dim 128, f16 KV).
+//
+// Work decomposition.  One work-group computes 128 consecutive rows (block rows j) of one
+// q-head of one stream, over every KV cell those rows see.  The grid is ordered heaviest
+// row block first (the last rows of a causal chunk see the most cells), so the long blocks
+// start first and the short ones fill in behind them.  Four waves own 32 rows each.
+//
+// Per 64-cell KV tile (double-buffered in LDS, one barrier per tile):
+//   K   [64 cells][16 chunks of 16 B], chunk q of cell c stored at slot q ^ (c & 15): filled by
+//       direct global->LDS loads (each lane fetches the global chunk that lands in its slot),
+//       read back conflict-free as MFMA A operands;
+//   V^T [128 dims][64 cells + pad], built once per work-group from registers: every thread
+//       loads two cells x 8 dims, pairs them with v_perm_b32 and writes 32-bit cell pairs,
+//       so each wave later reads its A operands as plain 16-byte rows.
+//   S^T = K Q^T on v_mfma_f32_32x32x16_f16: A = 32 cells x 16 dims from LDS, B = Q^T held in
+//       registers for the whole work-group (lane l: row l%32, dims 16ks + 8(l/32)..+7);
+//       lane l receives cells 8b + 4(l/32) + e (b, e < 4) of row l%32, so a row's 64 cells
+//       live in lanes l and l^32 and the row max needs one v_permlane32_swap.
+//   softmax: lazy exponent reference (moves only when the tile max exceeds it by 2^8),
+//       p = 2^(s*c - m*c) in one FMA.
+//   O^T += V^T P^T on v_mfma_f32_32x32x16_f16: for the 16-cell step kk the lane's eight
+//       values i = 8(kk%2) .. +7 of S^T block kk/2 are exactly its B operand; the V^T rows
+//       store each 16-cell group in the matching order (cells 4..7 and 8..11 swapped).
+// Only tiles that reach past the first row's causal boundary (or the stream's end) mask.
 #include "fa_device.hpp"
 
 namespace sixi {
+namespace {
 
-hipError_t launch_prefill(const FaArgs&, int, int, int, hipStream_t) { return hipErrorNotSupported; }
+constexpr int kBM = 128;           // rows per work-group
+constexpr int kBN = 64;            // cells per KV tile
+constexpr int kThreads = 256;      // 4 waves x 32 rows
+constexpr int kVtStride = 72;      // f16 per V^T row (64 cells + 8 pad): 144 B, conflict-free reads
+constexpr int kKBytes = kBN * 256;              // 16 KB
+constexpr int kVtBytes = 128 * kVtStride * 2;   // 18 KB
+constexpr float kLazyLog2 = 8.0f;
+
+enum { MODE_FAST = 0, MODE_GENERIC = 1 };
+
+struct PrefillLds {
+    u32x4 k[2][kKBytes / 16];
+    uint32_t vt[2][kVtBytes / 4];
+};
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// position of cell offset co (0..63) inside a V^T row: the middle quads of every 16-cell
+// group are swapped, so that the B-operand order of P^T is contiguous
+__device__ __forceinline__ int vt_pos(int co) {
+    const int q = (co >> 2) & 3;
+    const int qp = (q == 1) ? 2 : (q == 2 ? 1 : q);
+    return (co & ~15) | (qp << 2) | (co & 3);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int causal, int nrb) {
+    __shared__ PrefillLds sh;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int hl = lane >> 5;      // lane half
+    const int rl = lane & 31;      // row inside the wave / M index inside an MFMA block
+
+    // heaviest row block first
+    const int SH = a.S * a.H;
+    const int b = blockIdx.x;
+    const int rb = nrb - 1 - b / SH;
+    const int s = (b % SH) / a.H;
+    const int h = (b % SH) % a.H;
+    const int g = h / a.G;
+    const StreamDims sd = stream_dims(a, s);
+    const int j0 = rb * kBM;
+    if (j0 >= sd.ql) return;
+    const int j_last = min(j0 + kBM, sd.ql) - 1;
+    const int j = j0 + 32 * w + rl;  // this lane's row
+    const bool row_ok = j < sd.ql;
+
+    // cells each row sees; tiles below t_full are unmasked for every row of the group
+    const int vis = causal ? sd.kl + min(j, j_last) + 1 : sd.nc;
+    const int vis_max = causal ? sd.kl + j_last + 1 : sd.nc;
+    const int vis_min = causal ? sd.kl + j0 + 1 : sd.nc;
+    const int n_tiles = (vis_max + kBN - 1) / kBN;
+    const int t_full = (MODE == MODE_GENERIC) ? 0 : vis_min / kBN;
+
+    // ---- Q^T B operands in registers: lane l -> row j, dims 16ks + 8*hl .. +7 ----
+    f16x8 qop[8];
+    {
+        const char* src = a.q + (int64_t)j * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const int d0 = 16 * ks + 8 * hl;
+            if (!row_ok) {
+                qop[ks] = as_f16x8(u32x4{0u, 0u, 0u, 0u});
+            } else if (a.q_f16) {
+                qop[ks] = as_f16x8(ld16(src + d0 * 2));
+            } else {
+                const f32x4 lo = *reinterpret_cast<const f32x4*>(src + d0 * 4);
+                const f32x4 hi = *reinterpret_cast<const f32x4*>(src + d0 * 4 + 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qop[ks][e] = (_Float16)lo[e];
+                    qop[ks][4 + e] = (_Float16)hi[e];
+                }
+            }
+        }
+    }
+
+    // K/V of (stream, kv-head) through range-checked buffer resources (cells >= nc read 0)
+    const int64_t rowb = 128 * 2;
+    const i32x4 krs = make_rsrc_sgpr(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
+                                     (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + rowb));
+    const buf_rsrc vrs = make_rsrc(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
+                                   (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + rowb));
+    const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
+
+    // K: wave w stages cells 16w .. 16w+15 (4 loads of 4 cells x 256 B); lane l of load u
+    // lands in slot l%16 of cell 4u + l/16 and so fetches chunk (l%16) ^ (cell & 15)
+    auto issue_k = [&](int t, int buf) {
+        const uint32_t base = lds_addr(&sh.k[buf][0]);
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const int u = 4 * w + u4;
+            const int cell = 4 * u + (lane >> 4);
+            const uint32_t chunk = (uint32_t)((lane & 15) ^ (cell & 15));
+            dma16_to_lds(krs, (uint32_t)(t * kBN + cell) * knb + chunk * 16, base + u * 1024);
+        }
+    };
+    // V: thread item it = tid + 256k: cell pair p2 = it % 32, dim chunk q = it / 32
+    u32x4 vreg[2][2];
+    auto load_v = [&](int t) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int it = tid + 256 * k;
+            const int c = 2 * (it & 31);
+            const int q = it >> 5;
+            const uint32_t off = (uint32_t)(t * kBN + c) * vnb + q * 16;
+            vreg[k][0] = buf_ld16(vrs, off);
+            vreg[k][1] = buf_ld16(vrs, off + vnb);
+        }
+    };
+    auto store_vt = [&](int buf) {
+        uint32_t* vt = sh.vt[buf];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int it = tid + 256 * k;
+            const int c = 2 * (it & 31);
+            const int q = it >> 5;
+            const int pos = vt_pos(c);
+#pragma unroll
+            for (int t8 = 0; t8 < 8; ++t8) {
+                const int d2 = t8 >> 1;
+                const uint32_t sel = (t8 & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t pair = __builtin_amdgcn_perm(vreg[k][1][d2], vreg[k][0][d2], sel);
+                vt[((8 * q + t8) * kVtStride + pos) >> 1] = pair;
+            }
+        }
+    };
+
+    f32x16 acc[4];  // O^T blocks: dims 32db + 8(i/4) + 4hl + i%4 of row j
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[db][i] = 0.0f;
+    float m_ref = neg_inf();  // raw score (FAST) or log2 units (GENERIC)
+    float l_sum = 0.0f;
+    const float c2 = a.scale_log2;
+    const float thr = (MODE == MODE_FAST) ? kLazyLog2 / c2 : kLazyLog2;
+    const float slope = (MODE == MODE_GENERIC) ? alibi_slope(a, h) : 1.0f;
+    const char* mrow = nullptr;
+    if (MODE == MODE_GENERIC && a.mask)
+        mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3 + (int64_t)min(j, j_last) * a.m_nb1;
+
+    // prologue: tile 0
+    if (n_tiles > 0) {
+        load_v(0);
+        issue_k(0, 0);
+        wait_vmcnt<4>();  // the V loads (issued first) are back; the K DMA may still run
+        store_vt(0);
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+
+#pragma unroll 1
+    for (int t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        const bool more = t + 1 < n_tiles;
+        if (more) {
+            load_v(t + 1);
+            issue_k(t + 1, buf ^ 1);
+        }
+        const int c0 = t * kBN;
+        const bool masked = t >= t_full;
+
+        // ---- S^T = K Q^T: two 32-cell blocks ----
+        f32x16 st[2];
+        const u32x4* kt = sh.k[buf];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st[cb][i] = 0.0f;
+            const int cell = 32 * cb + rl;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const int chunk = (2 * ks + hl) ^ (cell & 15);
+                st[cb] = mfma32x32x16(as_f16x8(kt[cell * 16 + chunk]), qop[ks], st[cb]);
+            }
+        }
+
+        // ---- scores, row max (lanes l and l^32 hold the row's 64 cells) ----
+        float mx = neg_inf();
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int cell = c0 + 32 * cb + 8 * (i >> 2) + 4 * hl + (i & 3);
+                float x = st[cb][i];
+                if (MODE == MODE_GENERIC) {
+                    x *= a.scale;
+                    if (a.softcap != 0.0f) x = a.softcap * tanhf(x);
+                    if (a.mask) {
+                        float mv = neg_inf();
+                        if (cell < sd.nc)
+                            mv = slope * half_bits_to_float(*reinterpret_cast<const uint16_t*>(mrow + (int64_t)cell * 2));
+                        x = (mv == neg_inf()) ? neg_inf() : x + mv;
+                    } else if (cell >= vis) {
+                        x = neg_inf();
+                    }
+                    x *= kLog2e;
+                } else if (masked) {
+                    if (cell >= vis) x = neg_inf();
+                }
+                st[cb][i] = x;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) mx = fmaxf(mx, max3f(st[cb][i], st[cb][i + 1], fmaxf(st[cb][i + 2], st[cb][i + 3])));
+        }
+        {
+            auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+
+        // ---- lazy exponent reference ----
+        const bool need = mx > m_ref + thr;
+        if (__builtin_amdgcn_ballot_w64(need) != 0) {
+            float alpha = 1.0f;
+            if (need) {
+                alpha = fast_exp2((MODE == MODE_FAST) ? (m_ref - mx) * c2 : m_ref - mx);
+                m_ref = mx;
+            }
+            l_sum *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+        }
+
+        // ---- probabilities ----
+        const float mc = (m_ref == neg_inf()) ? 0.0f : ((MODE == MODE_FAST) ? m_ref * c2 : m_ref);
+        f16x8 pb[4];  // B operands of the four 16-cell steps
+        float psum = 0.0f;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = fast_exp2((MODE == MODE_FAST) ? fmaf(st[cb][i], c2, -mc) : st[cb][i] - mc);
+                psum += p;
+                pb[2 * cb + (i >> 3)][i & 7] = (_Float16)p;
+            }
+        }
+        l_sum += psum;
+
+        // Explicit masks: a cell that none of this wave's 32 rows sees may hold NaN bits, so
+        // its V^T entries are zeroed in this wave's operands (0 * NaN must not reach O).
+        uint32_t keep[4][4];
+        if (MODE == MODE_GENERIC && a.mask) {
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int m2 = 0; m2 < 4; ++m2) {
+                    const uint64_t b0 = __builtin_amdgcn_ballot_w64((float)pb[kk][2 * m2] != 0.0f);
+                    const uint64_t b1 = __builtin_amdgcn_ballot_w64((float)pb[kk][2 * m2 + 1] != 0.0f);
+                    keep[kk][m2] = ((((b0 >> (32 * hl)) & 0xffffffffull) != 0) ? 0x0000ffffu : 0u) |
+                                   ((((b1 >> (32 * hl)) & 0xffffffffull) != 0) ? 0xffff0000u : 0u);
+                }
+        }
+
+        // ---- O^T += V^T P^T ----
+        const uint32_t* vt = sh.vt[buf];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                u32x4 vop = *reinterpret_cast<const u32x4*>(&vt[((32 * db + rl) * kVtStride + 16 * kk + 8 * hl) >> 1]);
+                if (MODE == MODE_GENERIC && a.mask) {
+#pragma unroll
+                    for (int m2 = 0; m2 < 4; ++m2) vop[m2] &= keep[kk][m2];
+                }
+                acc[db] = mfma32x32x16(as_f16x8(vop), pb[kk], acc[db]);
+            }
+        }
+
+        if (more) {
+            wait_vmcnt<4>();  // V of tile t+1 (issued before its K DMA)
+            store_vt(buf ^ 1);
+            wait_vmcnt<0>();
+        }
+        __syncthreads();
+    }
+
+    // ---- normalise and write: lane holds dims 32db + 8b + 4hl .. +3 of row j ----
+    {
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_sum), __float_as_uint(l_sum), false, false);
+        l_sum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    if (row_ok) {
+        const float inv = l_sum == 0.0f ? 0.0f : 1.0f / l_sum;
+        char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int bq = 0; bq < 4; ++bq)
+                st16(dst + (32 * db + 8 * bq + 4 * hl) * 4,
+                     f32x4{acc[db][4 * bq], acc[db][4 * bq + 1], acc[db][4 * bq + 2], acc[db][4 * bq + 3]} * inv);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim, hipStream_t stream) {
+    if (kv_type != SIXI_TYPE_F16 || head_dim != 128) return hipErrorNotSupported;
+    const bool generic = mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f;
+    const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
+    const int nrb = (a.n_q + kBM - 1) / kBM;
+    const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
+    if (generic)
+        hipLaunchKernelGGL((prefill_f16_d128<MODE_GENERIC>), grid, block, 0, stream, a, causal, nrb);
+    else
+        hipLaunchKernelGGL((prefill_f16_d128<MODE_FAST>), grid, block, 0, stream, a, causal, nrb);
+    return hipGetLastError();
+}
 
 }  // namespace sixi

@@ -185,12 +185,16 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
-    if (!pl.splitk) return SIXI_E_UNSUPPORTED;  // prefill kernel not built yet
-
-    pl.row_tiles = sixi::decode_row_tiles(rows);
-    a.slot_floats = sixi::decode_slot_floats(pl.row_tiles);
-    const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
-    pl.ws_bytes = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
+    if (pl.splitk) {
+        pl.row_tiles = sixi::decode_row_tiles(rows);
+        a.slot_floats = sixi::decode_slot_floats(pl.row_tiles);
+        const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
+        pl.ws_bytes = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
+    } else {
+        // the prefill kernel keeps everything on chip; a token workspace keeps the contract uniform
+        if (S * H * ((n_q + 127) / 128) > (int64_t)INT32_MAX) return SIXI_E_UNSUPPORTED;
+        pl.ws_bytes = kWsAlign;
+    }
     *out = pl;
     return SIXI_OK;
 }

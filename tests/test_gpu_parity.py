@@ -145,7 +145,7 @@ def test_repeatable_bitwise_over_20_launches(fa):
     w, host, dev = _small()
     first = _run(fa, w, dev)
     for _ in range(19):
-        assert np.array_equal(first, _run(fa, w, dev))
+        assert np.array_equal(first, _run(fa, w, dev), equal_nan=True)
 
 
 def test_row_ignores_later_rows_and_cells(fa):
