@@ -36,22 +36,37 @@
 //                 dims 8r..8r+7), so output tile tt holds dims 8r + tt.
 // Only the tiles that reach past the first causal boundary (or the stream's end) apply a
 // mask; the rest run the unmasked body.
+//
+// q8_0 KV (ggml blocks {f16 d; int8 q[32]}, 136 B per 128-dim head row, only 4-byte aligned)
+// uses the same core: the raw rows of a tile are copied to LDS with dword LDS-DMA
+// (buffer_load_dword ... lds), each lane pulls the eight int8 values of its operand with
+// aligned dword reads and v_alignbyte_b32, and dequantises them in registers
+// (dequant_q8x8: one f16 rounding of q*d).  Q is quantised to q8_0 exactly as ggml's
+// flash_attn_ext does before the dot (per 32-dim block, d = amax/127) and enters the MFMA as
+// its dequantised f16 values.  (RS = 1 only: up to 48 rows per GQA group.)
 #include "fa_device.hpp"
 
 namespace sixi {
 namespace {
 
 constexpr int kTile = kDecodeTile;  // 16 cells
-constexpr int kSlotChunks = 8;      // 4 K chunks (ks) + 4 V chunks (e), 1 KB each
-constexpr int kDmaPerTile = 8;      // 16-byte LDS-DMA loads per lane per tile
+constexpr int kQ8Row = 136;         // bytes of one q8_0 head row (4 blocks of 34)
+constexpr int kQ8Dma = 9;           // dword LDS-DMA loads covering 16 q8_0 rows (2304 >= 2176 B)
 constexpr float kLazyLog2 = 8.0f;   // headroom (log2 units) before the exponent reference moves
 constexpr int kMaxPieces = 16;      // target bound on the pieces of one full-length segment
 
 enum { MODE_FAST = 0, MODE_GENERIC = 1 };
 
-template <int RS> struct Shape;
-template <> struct Shape<1> { static constexpr int waves = 4, lanes = 4, slots = 2, groups_per_cu = 2; };
-template <> struct Shape<2> { static constexpr int waves = 4, lanes = 2, slots = 3, groups_per_cu = 2; };
+// Per KV type: bytes of one ring slot (one 16-cell tile of K and V) and LDS-DMA loads
+// a tile takes (per wave when one wave stages it all).
+template <int KV> struct KvTile;
+template <> struct KvTile<SIXI_TYPE_F16> { static constexpr int slot_bytes = 8192, dma = 8; };
+template <> struct KvTile<SIXI_TYPE_Q8_0> { static constexpr int slot_bytes = 2 * kQ8Dma * 256, dma = 2 * kQ8Dma; };
+
+template <int RS, int KV> struct Shape;
+template <> struct Shape<1, SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 4, slots = 2, groups_per_cu = 2; };
+template <> struct Shape<2, SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 2, slots = 3, groups_per_cu = 2; };
+template <> struct Shape<1, SIXI_TYPE_Q8_0> { static constexpr int waves = 4, lanes = 4, slots = 3, groups_per_cu = 2; };
 
 template <int NT, int NS>
 struct MergeBuf {
@@ -61,14 +76,15 @@ struct MergeBuf {
 };
 
 // NTW = row tiles per wave, RS = row groups (waves that share a tile).
-template <int NTW, int RS>
+template <int NTW, int RS, int KV>
 struct DecodeLds {
+    using Sh = Shape<RS, KV>;
     union {
         struct {
-            u32x4 ring[Shape<RS>::lanes * Shape<RS>::slots * kSlotChunks * 64];
+            u32x4 ring[Sh::lanes * Sh::slots * KvTile<KV>::slot_bytes / 16];
             u32x4 q[NTW * RS * 4 * 64];  // Q^T B operands: [row tile][ks][lane], 8 f16 each
         } t;
-        MergeBuf<NTW, RS * Shape<RS>::lanes / 2> mg;  // reused after the tile loop
+        MergeBuf<NTW, RS * Sh::lanes / 2> mg;  // reused after the tile loop
     };
     int ps[kMaxStreams + 1];
 };
@@ -135,9 +151,8 @@ __device__ __forceinline__ void acc_merge_lds(const MergeBuf<NT, NS>& mg, int sl
 // Merges the tile lanes of each row group into tile lane 0: with four lanes (2,3) -> (0,1)
 // then 1 -> 0, with two lanes 1 -> 0.  Every wave must call it.  Returns whether this wave
 // owns its rows afterwards.
-template <int NTW, int RS, int NS>
+template <int NTW, int TL, int NS>
 __device__ __forceinline__ bool merge_lanes(MergeBuf<NTW, NS>& mg, Acc<NTW>& acc, int rg, int tl, int lane) {
-    constexpr int TL = Shape<RS>::lanes;
     constexpr int H = TL / 2;  // merge slots per row group
     if (TL == 4) {
         if (tl >= 2) acc_to_lds(mg, H * rg + tl - 2, acc, lane);
@@ -189,18 +204,41 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 // `after_reads` runs once the slot's LDS reads are consumed.  The phases run over all row
 // tiles at once (every QK^T, then every row max, one rare rescale branch, then every
 // exponential and PV), so each phase offers the scheduler NT independent chains.
-template <int NT, int MODE, bool MASKED, typename F>
+template <int NT, int KV, int MODE, bool MASKED, typename F>
 __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT>& acc, const u32x4* slot,
                                           const u32x4* qs, int c0, const RowInfo<NT>& ri,
                                           const char* mrow, int nc, int lane, F&& after_reads) {
     const int c = lane >> 4;
+    const int r = lane & 15;
 
+    // K operands (cell r, dims 32ks + 8c .. +7) and V rows (cells 4c + e, dims 8r .. 8r+7)
     f16x8 kop[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kop[ks] = as_f16x8(slot[ks * 64 + lane]);
     u32x4 vr[4];
+    if constexpr (KV == SIXI_TYPE_F16) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) vr[e] = slot[(4 + e) * 64 + lane];
+        for (int ks = 0; ks < 4; ++ks) kop[ks] = as_f16x8(slot[ks * 64 + lane]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vr[e] = slot[(4 + e) * 64 + lane];
+    } else {
+        // raw q8_0 rows packed at 136 B: block b of row x holds d at x*136 + 34b and the
+        // int8 values at x*136 + 34b + 2 (2 bytes past a dword boundary for even b)
+        const uint32_t* kraw = reinterpret_cast<const uint32_t*>(slot);
+        const uint32_t* vraw = kraw + kQ8Dma * 64;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            uint32_t w0, w1;
+            ld8_at(kraw, r * kQ8Row + 34 * ks + 2 + 8 * c, (ks & 1) == 0, w0, w1);
+            kop[ks] = as_f16x8(dequant_q8x8(w0, w1, ld_half_at(kraw, r * kQ8Row + 34 * ks)));
+        }
+        const int b = r >> 2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int x = 4 * c + e;
+            uint32_t w0, w1;
+            ld8_at(vraw, x * kQ8Row + 34 * b + 2 + 8 * (r & 3), (b & 1) == 0, w0, w1);
+            vr[e] = dequant_q8x8(w0, w1, ld_half_at(vraw, x * kQ8Row + 34 * b));
+        }
+    }
 
     // ---- S^T = K Q^T for every row tile ----
     f32x4 st[NT];
@@ -368,13 +406,15 @@ struct Piece {
 };
 
 // One piece: tiles [tb, te) of segment (s, g).
-template <int NTW, int RS, int MODE>
-__device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS>& sh, int causal, const Piece& pc) {
+template <int NTW, int RS, int KV, int MODE>
+__device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS, KV>& sh, int causal, const Piece& pc) {
     constexpr int NTOT = NTW * RS;
-    constexpr int TL = Shape<RS>::lanes;       // tile lanes
-    constexpr int NSLOT = Shape<RS>::slots;
-    constexpr int NTHREADS = Shape<RS>::waves * 64;
-    constexpr int DMA = kDmaPerTile / RS;      // LDS-DMA loads per tile per wave
+    constexpr int TL = Shape<RS, KV>::lanes;   // tile lanes
+    constexpr int NSLOT = Shape<RS, KV>::slots;
+    constexpr int NTHREADS = Shape<RS, KV>::waves * 64;
+    constexpr int SLOT16 = KvTile<KV>::slot_bytes / 16;
+    constexpr int DMA = KvTile<KV>::dma / RS;  // LDS-DMA loads per tile per wave
+    static_assert(KV == SIXI_TYPE_F16 || RS == 1, "q8_0 runs one row group");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -398,17 +438,40 @@ __device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS>& sh, int causal
             const int h = g * G + row % G;
             const char* src = a.q + (int64_t)j * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3 +
                               (int64_t)chunk * 8 * a.q_es;
-            f16x8 hv;
+            float xv[8];
             if (a.q_f16) {
-                hv = as_f16x8(ld16(src));
+                const f16x8 hq = as_f16x8(ld16(src));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] = (float)hq[e];
             } else {
                 const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
                 const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 16);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    hv[e] = (_Float16)lo[e];
-                    hv[4 + e] = (_Float16)hi[e];
+                    xv[e] = lo[e];
+                    xv[4 + e] = hi[e];
                 }
+            }
+            f16x8 hv;
+            if constexpr (KV == SIXI_TYPE_Q8_0) {
+                // ggml converts Q to the K dot type: q8_0 per 32-dim block, d = amax/127,
+                // q = round-half-away(x * 127/amax) clamped to +-127; the MFMA takes q*d
+                float am = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(xv[e]));
+                am = fmaxf(am, __shfl_xor(am, 1, 64));
+                am = fmaxf(am, __shfl_xor(am, 2, 64));
+                const float d = am / 127.0f;
+                const float id = d != 0.0f ? 127.0f / am : 0.0f;
+                const _Float16 dh = (_Float16)d;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float qv = fminf(fmaxf(roundf(xv[e] * id), -127.0f), 127.0f);
+                    hv[e] = (_Float16)(qv * (float)dh);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = (_Float16)xv[e];
             }
             val = as_u32x4(hv);
         }
@@ -438,7 +501,7 @@ __device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS>& sh, int causal
 
     // K/V of this (stream, kv-head) through range-checked buffer resources: cells >= nc read
     // as zeros (and are masked), so the tail tile needs no clamping and cannot fault.
-    const int64_t rowb = 128 * 2;
+    const int64_t rowb = (KV == SIXI_TYPE_F16) ? 128 * 2 : kQ8Row;
     const i32x4 krs = make_rsrc_sgpr(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
                                      (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + rowb));
     const i32x4 vrs = make_rsrc_sgpr(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
@@ -449,45 +512,71 @@ __device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS>& sh, int causal
     const int t0 = tb + tl;
     const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
     const int n_iter = (te - tb + TL - 1) / TL;
-    u32x4* ring = sh.t.ring + (size_t)tl * NSLOT * kSlotChunks * 64;
+    u32x4* ring = sh.t.ring + (size_t)tl * NSLOT * SLOT16;
     const uint32_t ring_base = lds_addr(ring);
 
-    // Stage tile i of this lane into slot i % NSLOT.  RS = 1: all 8 chunks; RS = 2: row
-    // group 0 stages the 4 K chunks and row group 1 the 4 V chunks.
+    // q8_0: dword t = 64u + lane of the packed 16-row tile is dword t % 34 of row t / 34
+    // (lanes past the 16 rows repeat the last dword into the slot's spare tail)
+    uint32_t q8_cell[kQ8Dma], q8_dw[kQ8Dma];
+    if constexpr (KV == SIXI_TYPE_Q8_0) {
+#pragma unroll
+        for (int u = 0; u < kQ8Dma; ++u) {
+            const int t = 64 * u + lane;
+            const bool in = t < 16 * (kQ8Row / 4);
+            q8_cell[u] = in ? t / (kQ8Row / 4) : 15;
+            q8_dw[u] = in ? t % (kQ8Row / 4) : kQ8Row / 4 - 1;
+        }
+    }
+
+    // Stage tile i of this lane into slot i % NSLOT.  RS = 1: all of it; RS = 2: row group
+    // 0 stages the 4 K chunks and row group 1 the 4 V chunks.
     auto issue = [&](int i) {
         const uint32_t c0 = (uint32_t)(t0 + i * TL) * kTile;
-        const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * (kSlotChunks * 1024);
-        if (RS == 1 || rg == 0) {
-            const uint32_t off = (c0 + r) * knb + c * 16;
+        const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * KvTile<KV>::slot_bytes;
+        if constexpr (KV == SIXI_TYPE_F16) {
+            if (RS == 1 || rg == 0) {
+                const uint32_t off = (c0 + r) * knb + c * 16;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) dma16_to_lds(krs, off + ks * 64, base + ks * 1024);
-        }
-        if (RS == 1 || rg == 1) {
-            const uint32_t vo = (c0 + 4 * c) * vnb + r * 16;
+                for (int ks = 0; ks < 4; ++ks) dma16_to_lds(krs, off + ks * 64, base + ks * 1024);
+            }
+            if (RS == 1 || rg == 1) {
+                const uint32_t vo = (c0 + 4 * c) * vnb + r * 16;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dma16_to_lds(vrs, vo + e * vnb, base + (4 + e) * 1024);
+                for (int e = 0; e < 4; ++e) dma16_to_lds(vrs, vo + e * vnb, base + (4 + e) * 1024);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kQ8Dma; ++u)
+                dma4_to_lds(krs, (c0 + q8_cell[u]) * knb + q8_dw[u] * 4, base + u * 256);
+#pragma unroll
+            for (int u = 0; u < kQ8Dma; ++u)
+                dma4_to_lds(vrs, (c0 + q8_cell[u]) * vnb + q8_dw[u] * 4, base + (kQ8Dma + u) * 256);
         }
     };
     auto step = [&](int i, auto&& after_reads) {
-        const u32x4* slot = ring + (i % NSLOT) * (kSlotChunks * 64);
+        const u32x4* slot = ring + (i % NSLOT) * SLOT16;
         const int t = t0 + i * TL;
         if (t < t_full)
-            tile_step<NTW, MODE, false>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
+            tile_step<NTW, KV, MODE, false>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
         else
-            tile_step<NTW, MODE, true>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
+            tile_step<NTW, KV, MODE, true>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
     };
 
     if constexpr (RS == 1) {
-        // private ring: the slot just read is refilled with tile i+2
-        if (n_my > 0) issue(0);
-        if (n_my > 1) issue(1);
+        // private ring: the slot just read is refilled with tile i+NSLOT
+        static_assert(NSLOT == 2 || NSLOT == 3, "ring depth");
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i)
+            if (i < n_my) issue(i);
 #pragma unroll 1
         for (int i = 0; i < n_my; ++i) {
-            if (i + 1 < n_my) wait_vmcnt<DMA>();
+            const int ahead = n_my - 1 - i;  // own tiles issued after tile i
+            if (NSLOT == 3 && ahead >= 2) wait_vmcnt<2 * DMA>();
+            else if (ahead >= 1) wait_vmcnt<DMA>();
             else wait_vmcnt<0>();
             step(i, [&] {
                 wait_lgkmcnt0();
-                if (i + 2 < n_my) issue(i + 2);
+                if (i + NSLOT < n_my) issue(i + NSLOT);
             });
         }
     } else {
@@ -517,7 +606,7 @@ __device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS>& sh, int causal
     }
 
     __syncthreads();  // every wave is past its ring (each drained its own loads)
-    if (merge_lanes<NTW, RS>(sh.mg, acc, rg, tl, lane)) {
+    if (merge_lanes<NTW, TL>(sh.mg, acc, rg, tl, lane)) {
         if (tb == 0 && te == pc.nt_seg)
             write_rows(a, acc, n0, s, g, R, lane);
         else
@@ -544,10 +633,10 @@ __device__ __forceinline__ bool partition(const FaArgs& a, const int* ps, int b,
     return true;
 }
 
-template <int NTW, int RS, int MODE>
-__global__ __launch_bounds__(Shape<RS>::waves * 64, Shape<RS>::groups_per_cu) void decode_f16_d128(FaArgs a,
-                                                                                                 int causal) {
-    __shared__ DecodeLds<NTW, RS> sh;
+template <int NTW, int RS, int KV, int MODE>
+__global__ __launch_bounds__((Shape<RS, KV>::waves * 64), (Shape<RS, KV>::groups_per_cu)) void decode_d128(
+    FaArgs a, int causal) {
+    __shared__ DecodeLds<NTW, RS, KV> sh;
     const int tid = threadIdx.x;
     if (tid < 64) build_tile_prefix(a, sh.ps);
     __syncthreads();
@@ -576,7 +665,7 @@ __global__ __launch_bounds__(Shape<RS>::waves * 64, Shape<RS>::groups_per_cu) vo
         pc.te = (int)(min(pt.x1, ck + nt) - ck);
         pc.nt_seg = nt;
         pc.slot = (int64_t)s * Hkv + g + pt.p_log;
-        decode_piece<NTW, RS, MODE>(a, sh, causal, pc);
+        decode_piece<NTW, RS, KV, MODE>(a, sh, causal, pc);
         x = ck + pc.te;
     }
 }
@@ -629,13 +718,13 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
 }
 
-template <int NTW, int RS>
+template <int NTW, int RS, int KV>
 hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
-    const dim3 grid(a.P), block(Shape<RS>::waves * 64);
+    const dim3 grid(a.P), block(Shape<RS, KV>::waves * 64);
     if (generic)
-        hipLaunchKernelGGL((decode_f16_d128<NTW, RS, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_d128<NTW, RS, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
     else
-        hipLaunchKernelGGL((decode_f16_d128<NTW, RS, MODE_FAST>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_d128<NTW, RS, KV, MODE_FAST>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int rows_slot = NTW * RS * 16;
@@ -648,7 +737,7 @@ hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stre
 
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
     const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + kTile - 1) / kTile);
-    const int per_cu = row_tiles <= 3 ? Shape<1>::groups_per_cu : Shape<2>::groups_per_cu;
+    const int per_cu = row_tiles <= 3 ? Shape<1, SIXI_TYPE_F16>::groups_per_cu : Shape<2, SIXI_TYPE_F16>::groups_per_cu;
     int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
     if (P > kMaxSplitGroups) P = kMaxSplitGroups;
     if (P > tiles_max) P = tiles_max;
@@ -661,17 +750,28 @@ int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
 
 hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream) {
-    if (kv_type != SIXI_TYPE_F16 || head_dim != 128) return hipErrorNotSupported;
+    if (head_dim != 128) return hipErrorNotSupported;
     const bool generic = mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f;
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
-    switch (row_tiles) {
-        case 1: return launch_nt<1, 1>(a, generic, causal, stream);
-        case 2: return launch_nt<2, 1>(a, generic, causal, stream);
-        case 3: return launch_nt<3, 1>(a, generic, causal, stream);
-        case 4: return launch_nt<2, 2>(a, generic, causal, stream);
-        case 6: return launch_nt<3, 2>(a, generic, causal, stream);
-        default: return hipErrorNotSupported;
+    if (kv_type == SIXI_TYPE_F16) {
+        switch (row_tiles) {
+            case 1: return launch_nt<1, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 2: return launch_nt<2, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 3: return launch_nt<3, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 4: return launch_nt<2, 2, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 6: return launch_nt<3, 2, SIXI_TYPE_F16>(a, generic, causal, stream);
+            default: return hipErrorNotSupported;
+        }
     }
+    if (kv_type == SIXI_TYPE_Q8_0) {
+        switch (row_tiles) {
+            case 1: return launch_nt<1, 1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
+            case 2: return launch_nt<2, 1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
+            case 3: return launch_nt<3, 1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
+    return hipErrorNotSupported;
 }
 
 }  // namespace sixi

@@ -79,6 +79,20 @@ __device__ __forceinline__ void dma16_to_lds(i32x4 rsrc, uint32_t voff, uint32_t
         : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc)
         : "memory");
 }
+// 4 bytes per lane from buffer offset `voff` into LDS at `lds_addr` + 4*lane
+// (buffer_load_dword ... lds); used for rows whose alignment is only 4 bytes (q8_0).
+__device__ __forceinline__ void dma4_to_lds(i32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+    int saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc)
+        : "memory");
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -149,6 +163,44 @@ __device__ __forceinline__ float alibi_slope(const FaArgs& a, int h) {
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
+}
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Eight int8 values (two dwords, little-endian) times the f16 block scale `dbits`, as eight
+// f16 (u32x4).  Each byte becomes the f16 1024 + (b ^ 0x80) = 1152 + b through v_perm_b32,
+// an exact f16 subtraction recovers b, and one f16 multiply rounds b * d once.
+__device__ __forceinline__ u32x4 dequant_q8x8(uint32_t w0, uint32_t w1, uint16_t dbits) {
+    const _Float16 d = __builtin_bit_cast(_Float16, dbits);
+    const f16x2 dd = {d, d};
+    const f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
+    u32x4 out;
+    out[0] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - off) * dd);
+    out[1] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - off) * dd);
+    out[2] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - off) * dd);
+    out[3] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - off) * dd);
+    return out;
+}
+
+// The 8 bytes at byte offset `a` of a dword array whose element `a` lies 2 bytes past a
+// dword boundary (odd2 = true) or on one.
+__device__ __forceinline__ void ld8_at(const uint32_t* base, int a, bool odd2, uint32_t& w0, uint32_t& w1) {
+    if (odd2) {
+        const int d0 = (a - 2) >> 2;
+        const uint32_t x0 = base[d0], x1 = base[d0 + 1], x2 = base[d0 + 2];
+        w0 = __builtin_amdgcn_alignbyte(x1, x0, 2);
+        w1 = __builtin_amdgcn_alignbyte(x2, x1, 2);
+    } else {
+        w0 = base[a >> 2];
+        w1 = base[(a >> 2) + 1];
+    }
+}
+
+// The f16 bits at an even byte offset `a` of a dword array.
+__device__ __forceinline__ uint16_t ld_half_at(const uint32_t* base, int a) {
+    const uint32_t w = base[a >> 2];
+    return (uint16_t)((a & 2) ? (w >> 16) : (w & 0xffffu));
 }
 
 }  // namespace sixi

@@ -100,18 +100,19 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     if (o.ne[0] != D || o.ne[1] != H || o.ne[2] != n_q || o.ne[3] != S) return SIXI_E_INVALID_ARGUMENT;
     if (S > sixi::kMaxStreams || H > 4096 || n_q > (1 << 20) || n_kv > (1 << 26)) return SIXI_E_UNSUPPORTED;
     if (D != kMaxHeadDim) return SIXI_E_UNSUPPORTED;
-    if (k.type == SIXI_TYPE_Q8_0) return SIXI_E_UNSUPPORTED;  // q8_0 kernels are not built yet
 
     // element strides and alignment
     const int qes = elem_bytes(q.type);
     if (q.nb[0] != qes || o.nb[0] != 4) return SIXI_E_INVALID_ARGUMENT;
     if (k.nb[0] != (k.type == SIXI_TYPE_Q8_0 ? 34 : 2) || v.nb[0] != k.nb[0]) return SIXI_E_INVALID_ARGUMENT;
+    // f16 rows are moved in 16-byte pieces, q8_0 rows (136 B) in dwords
+    const int kv_align = (k.type == SIXI_TYPE_Q8_0) ? 4 : 16;
     for (int d = 1; d < 4; ++d) {
         if (q.nb[d] <= 0 || k.nb[d] <= 0 || v.nb[d] <= 0 || o.nb[d] <= 0) return SIXI_E_INVALID_ARGUMENT;
         if (q.nb[d] % qes) return SIXI_E_ALIGNMENT;
-        if (k.nb[d] % 16 || v.nb[d] % 16 || o.nb[d] % 16) return SIXI_E_ALIGNMENT;
+        if (k.nb[d] % kv_align || v.nb[d] % kv_align || o.nb[d] % 16) return SIXI_E_ALIGNMENT;
     }
-    if (!aligned(q.data, qes) || !aligned(k.data, 16) || !aligned(v.data, 16) || !aligned(o.data, 16))
+    if (!aligned(q.data, qes) || !aligned(k.data, kv_align) || !aligned(v.data, kv_align) || !aligned(o.data, 16))
         return SIXI_E_ALIGNMENT;
     const int64_t kvrow = row_bytes(k.type, D);
     if (k.nb[1] < kvrow || v.nb[1] < kvrow) return SIXI_E_INVALID_ARGUMENT;  // rows must not overlap
@@ -185,6 +186,8 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
+    // q8_0 KV: the split-K kernel with one row group (up to 48 rows per kv-head group)
+    if (k.type == SIXI_TYPE_Q8_0 && rows > 48) return SIXI_E_UNSUPPORTED;
     if (pl.splitk) {
         pl.row_tiles = sixi::decode_row_tiles(rows);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles);

@@ -1,0 +1,108 @@
+"""GPU parity of q8_0 KV decode/verify against the oracle, through the C ABI.
+
+The oracle follows ggml: Q is quantised to q8_0 (per 32-dim block, d = amax/127, q rounded
+half away from zero), every block dot is an exact integer sum scaled by d_k * d_q, and V is
+dequantised to f32.  The GPU computes the same quantised values with one f16 rounding of
+q * d per operand.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sixi_attn as sa
+from sixi_attn import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-3
+REL_L2 = 1e-3
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", file=sys.stderr, flush=True)
+
+
+@pytest.fixture(scope="module")
+def fa():
+    assert torch.cuda.is_available(), "the gpu tests need a GPU"
+    sa.load_library()
+    return sa.FlashAttnExt()
+
+
+def _run(fa, w, dev, mask_mode=sa.MASK_BLOCK_CAUSAL, mask=None, k=None, v=None):
+    out = torch.full((w.S, w.n_q, w.H, w.D), float("nan"), dtype=torch.float32, device="cuda")
+    fa(dev["q"], dev["k"] if k is None else k, dev["v"] if v is None else v, out, kv_len=dev["kv_len"],
+       q_len=dev["q_len"], mask_mode=mask_mode, mask=mask)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _check(w, host, got, streams, label):
+    want = oracle.attention_for_workload(host, w.kv_type, streams)
+    ql = host["q_len"]
+    rows_g = np.concatenate([got[s, :ql[s]].ravel() for s in streams])
+    rows_w = np.concatenate([want[i, :ql[s]].ravel() for i, s in enumerate(streams)])
+    m = oracle.diff_metrics(rows_w, rows_g)
+    _say(f"{label} max_abs={m['max_abs']:.3e} rel_l2={m['rel_l2']:.3e}")
+    assert np.all(np.isfinite(rows_g))
+    assert m["max_abs"] <= MAX_ABS and m["rel_l2"] <= REL_L2, m
+
+
+@pytest.mark.parametrize("name", ["long_q8_decode", "long_q8_verify"])
+def test_long_q8_configs(fa, name):
+    _say(f"config {name} (oracle on streams 0 and 5)")
+    w = wl.config(name)
+    host = wl.make_host(w, poison=True)
+    dev = wl.to_device(host)
+    got = _run(fa, w, dev)
+    _check(w, host, got, [0, 5], name)
+    assert np.all(np.isfinite(np.concatenate([got[s, :w.q_len[s]].ravel() for s in range(w.S)])))
+
+
+@pytest.mark.parametrize("kv_len,q_len,H,Hkv", [
+    ([0, 5, 100, 1531], [1, 3, 8, 7], 24, 4),   # empty cache, ragged rows up to 48 per group
+    ([300, 33], [2, 2], 8, 8),                  # no GQA
+    ([4000], [3], 32, 2),                       # 16 q-heads per kv-head, 48 rows
+])
+def test_q8_ragged(fa, kv_len, q_len, H, Hkv):
+    _say(f"q8 ragged kv_len={kv_len} q_len={q_len} H={H} Hkv={Hkv}")
+    w = wl.Workload("q8_ragged", 0x51A7_5000 + sum(kv_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv,
+                    kv_type=sa.TYPE_Q8_0)
+    host = wl.make_host(w, poison=True)
+    dev = wl.to_device(host)
+    _check(w, host, _run(fa, w, dev), list(range(w.S)), "q8 ragged")
+
+
+def test_q8_explicit_mask_and_invariance(fa):
+    _say("q8 explicit mask, and rows ignore cells past their position")
+    w = wl.Workload("q8_small", 0x51A7_6000, 3, [130, 700, 41], [8, 8, 8], kv_type=sa.TYPE_Q8_0)
+    host = wl.make_host(w, poison=True)
+    dev = wl.to_device(host)
+    base = _run(fa, w, dev)
+    _check(w, host, base, list(range(w.S)), "q8 block-causal")
+    n_kv = dev["k"].shape[1]
+    mask = torch.from_numpy(oracle.build_kq_mask(n_kv, w.n_q, w.kv_len, w.q_len, True)).view(torch.float16).cuda()
+    ex = _run(fa, w, dev, mask_mode=sa.MASK_EXPLICIT, mask=mask)
+    _check(w, host, ex, list(range(w.S)), "q8 explicit mask")
+    j = 3
+    k2 = dev["k"].clone()
+    v2 = dev["v"].clone()
+    for s in range(w.S):
+        k2[s, w.kv_len[s] + j + 1:] = 0x55
+        v2[s, w.kv_len[s] + j + 1:] = 0x33
+    alt = _run(fa, w, dev, k=k2, v=v2)
+    assert np.array_equal(base[:, :j + 1], alt[:, :j + 1])
+    for _ in range(5):
+        assert np.array_equal(base, _run(fa, w, dev), equal_nan=True)
+
+
+def test_q8_more_than_48_rows_is_unsupported(fa):
+    w = wl.Workload("q8_wide", 0x51A7_7000, 1, [100], [16], kv_type=sa.TYPE_Q8_0)
+    host = wl.make_host(w)
+    dev = wl.to_device(host)
+    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    rc = fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], check=False)
+    assert rc == sa.E_UNSUPPORTED
