@@ -502,9 +502,9 @@ __device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS, KV>& sh, int ca
     // K/V of this (stream, kv-head) through range-checked buffer resources: cells >= nc read
     // as zeros (and are masked), so the tail tile needs no clamping and cannot fault.
     const int64_t rowb = (KV == SIXI_TYPE_F16) ? 128 * 2 : kQ8Row;
-    const i32x4 krs = make_rsrc_sgpr(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
+    const buf_rsrc krs = make_rsrc(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
                                      (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + rowb));
-    const i32x4 vrs = make_rsrc_sgpr(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
+    const buf_rsrc vrs = make_rsrc(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
                                      (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + rowb));
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
 

@@ -52,22 +52,11 @@ __device__ __forceinline__ uint32_t buf_ld4(buf_rsrc r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
-// Raw buffer resource as four SGPRs, for inline-asm loads.
-__device__ __forceinline__ i32x4 make_rsrc_sgpr(const void* base, uint32_t bytes) {
-    const uint64_t addr = reinterpret_cast<uint64_t>(base);
-    i32x4 r;
-    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
-    r[1] = __builtin_amdgcn_readfirstlane((int)((addr >> 32) & 0xffffu));  // stride 0
-    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
-    r[3] = 0x00020000;
-    return r;
-}
-
 // 16 bytes per lane from buffer offset `voff` straight into LDS at `lds_addr` + 16*lane
 // (gfx950 buffer_load_dwordx4 ... lds).  Issued from asm so that the compiler does not
 // drain every LDS-DMA load before each LDS read; the caller waits with wait_vmcnt<N>.
 // m0 is saved and restored; the s_nop covers the m0-write -> LDS-DMA hazard.
-__device__ __forceinline__ void dma16_to_lds(i32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+__device__ __forceinline__ void dma16_to_lds(buf_rsrc rsrc, uint32_t voff, uint32_t lds_addr) {
     int saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
@@ -81,7 +70,7 @@ __device__ __forceinline__ void dma16_to_lds(i32x4 rsrc, uint32_t voff, uint32_t
 }
 // 4 bytes per lane from buffer offset `voff` into LDS at `lds_addr` + 4*lane
 // (buffer_load_dword ... lds); used for rows whose alignment is only 4 bytes (q8_0).
-__device__ __forceinline__ void dma4_to_lds(i32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+__device__ __forceinline__ void dma4_to_lds(buf_rsrc rsrc, uint32_t voff, uint32_t lds_addr) {
     int saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"

@@ -23,6 +23,8 @@
 //       values i = 8(kk%2) .. +7 of S^T block kk/2 are exactly its B operand; the V^T rows
 //       store each 16-cell group in the matching order (cells 4..7 and 8..11 swapped).
 // Only tiles that reach past the first row's causal boundary (or the stream's end) mask.
+#include <type_traits>
+
 #include "fa_device.hpp"
 
 namespace sixi {
@@ -116,55 +118,71 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         }
     }
 
-    // K/V of (stream, kv-head) through range-checked buffer resources (cells >= nc read 0)
+    // K/V of (stream, kv-head): every tile gets its own range-checked buffer resource whose
+    // base is the tile's first cell, so cells >= nc read as zero and no load can fault
     const int64_t rowb = 128 * 2;
-    const i32x4 krs = make_rsrc_sgpr(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
-                                     (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + rowb));
-    const buf_rsrc vrs = make_rsrc(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
-                                   (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + rowb));
+    const char* kbase = a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2;
+    const char* vbase = a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2;
+    const int64_t kbytes = (int64_t)(sd.nc - 1) * a.k_nb1 + rowb;
+    const int64_t vbytes = (int64_t)(sd.nc - 1) * a.v_nb1 + rowb;
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
 
-    // K: wave w stages cells 16w .. 16w+15 (4 loads of 4 cells x 256 B); lane l of load u
-    // lands in slot l%16 of cell 4u + l/16 and so fetches chunk (l%16) ^ (cell & 15)
-    auto issue_k = [&](int t, int buf) {
-        const uint32_t base = lds_addr(&sh.k[buf][0]);
+    // ---- per-lane LDS byte offsets, fixed for the whole loop ----
+    char* lds = reinterpret_cast<char*>(&sh);
+    const uint32_t lds0 = lds_addr(&sh);
+    constexpr int kVtBase = 2 * kKBytes;  // V^T buffers follow the two K buffers
+    // K A operand of (cb, ks): cell 32cb + rl, chunk (2ks + hl) stored at slot chunk ^ (rl & 15)
+    uint32_t koff[8];
 #pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-            const int u = 4 * w + u4;
-            const int cell = 4 * u + (lane >> 4);
-            const uint32_t chunk = (uint32_t)((lane & 15) ^ (cell & 15));
-            dma16_to_lds(krs, (uint32_t)(t * kBN + cell) * knb + chunk * 16, base + u * 1024);
-        }
+    for (int ks = 0; ks < 8; ++ks) koff[ks] = rl * 256 + ((((2 * ks + hl) ^ (rl & 15)) & 15) << 4);
+    // V^T A operand of (db, kk): row 32db + rl, positions 16kk + 8hl .. +7
+    const uint32_t vrd = rl * (kVtStride * 2) + 16 * hl;
+    // K staging: wave w's load u4 fills cells 4(4w + u4) + l/16; lane fetches chunk (l%16)^cell
+    uint32_t kdo[4];
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+        const int cell = 4 * (4 * w + u4) + (lane >> 4);
+        kdo[u4] = (uint32_t)cell * knb + (uint32_t)(((lane & 15) ^ (cell & 15)) * 16);
+    }
+    // V staging: item k = tid + 256k -> cell pair 2*(it%32), dim chunk it/32
+    uint32_t vdo[2], vst[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int it = tid + 256 * k;
+        const int c = 2 * (it & 31);
+        const int q = it >> 5;
+        vdo[k] = (uint32_t)c * vnb + (uint32_t)q * 16;
+        vst[k] = (uint32_t)(8 * q) * (kVtStride * 2) + (uint32_t)vt_pos(c) * 2;
+    }
+
+    auto issue_k = [&](int t, int buf) {
+        const int64_t o = (int64_t)t * kBN * knb;
+        const buf_rsrc rs = make_rsrc(kbase + o, (uint32_t)(kbytes > o ? kbytes - o : 0));
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4)
+            dma16_to_lds(rs, kdo[u4], lds0 + buf * kKBytes + (4 * w + u4) * 1024);
     };
-    // V: thread item it = tid + 256k: cell pair p2 = it % 32, dim chunk q = it / 32
     u32x4 vreg[2][2];
     auto load_v = [&](int t) {
+        const int64_t o = (int64_t)t * kBN * vnb;
+        const buf_rsrc rs = make_rsrc(vbase + o, (uint32_t)(vbytes > o ? vbytes - o : 0));
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int it = tid + 256 * k;
-            const int c = 2 * (it & 31);
-            const int q = it >> 5;
-            const uint32_t off = (uint32_t)(t * kBN + c) * vnb + q * 16;
-            vreg[k][0] = buf_ld16(vrs, off);
-            vreg[k][1] = buf_ld16(vrs, off + vnb);
+            vreg[k][0] = buf_ld16(rs, vdo[k]);
+            vreg[k][1] = buf_ld16(rs, vdo[k] + vnb);
         }
     };
     auto store_vt = [&](int buf) {
-        uint32_t* vt = sh.vt[buf];
+        char* vt = lds + kVtBase + buf * kVtBytes;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int it = tid + 256 * k;
-            const int c = 2 * (it & 31);
-            const int q = it >> 5;
-            const int pos = vt_pos(c);
+        for (int k = 0; k < 2; ++k)
 #pragma unroll
             for (int t8 = 0; t8 < 8; ++t8) {
                 const int d2 = t8 >> 1;
                 const uint32_t sel = (t8 & 1) ? 0x07060302u : 0x05040100u;
-                const uint32_t pair = __builtin_amdgcn_perm(vreg[k][1][d2], vreg[k][0][d2], sel);
-                vt[((8 * q + t8) * kVtStride + pos) >> 1] = pair;
+                *reinterpret_cast<uint32_t*>(vt + vst[k] + t8 * (kVtStride * 2)) =
+                    __builtin_amdgcn_perm(vreg[k][1][d2], vreg[k][0][d2], sel);
             }
-        }
     };
 
     f32x16 acc[4];  // O^T blocks: dims 32db + 8(i/4) + 4hl + i%4 of row j
@@ -180,42 +198,30 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     const char* mrow = nullptr;
     if (MODE == MODE_GENERIC && a.mask)
         mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3 + (int64_t)min(j, j_last) * a.m_nb1;
+    const f32x16 zero16 = {};
 
-    // prologue: tile 0
-    if (n_tiles > 0) {
-        load_v(0);
-        issue_k(0, 0);
-        wait_vmcnt<4>();  // the V loads (issued first) are back; the K DMA may still run
-        store_vt(0);
-        wait_vmcnt<0>();
-    }
-    __syncthreads();
-
-#pragma unroll 1
-    for (int t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
+    // One tile from LDS buffer BUF (compile-time, so every LDS offset is an immediate).
+    auto tile = [&](int t, auto BUF, auto MASKED) {
+        constexpr int buf = decltype(BUF)::value;
+        constexpr bool masked = decltype(MASKED)::value;
         const bool more = t + 1 < n_tiles;
-        if (more) {
-            load_v(t + 1);
-            issue_k(t + 1, buf ^ 1);
-        }
+        if (more) issue_k(t + 1, buf ^ 1);
         const int c0 = t * kBN;
-        const bool masked = t >= t_full;
+        const char* kt = lds + buf * kKBytes;
 
         // ---- S^T = K Q^T: two 32-cell blocks ----
         f32x16 st[2];
-        const u32x4* kt = sh.k[buf];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
+            st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 8192 + koff[0])), qop[0], zero16);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) st[cb][i] = 0.0f;
-            const int cell = 32 * cb + rl;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const int chunk = (2 * ks + hl) ^ (cell & 15);
-                st[cb] = mfma32x32x16(as_f16x8(kt[cell * 16 + chunk]), qop[ks], st[cb]);
-            }
+            for (int ks = 1; ks < 8; ++ks)
+                st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 8192 + koff[ks])), qop[ks],
+                                      st[cb]);
         }
+
+        // V of tile t+1 into registers while the scores are formed (stored as V^T below)
+        if (more) load_v(t + 1);
 
         // ---- scores, row max (lanes l and l^32 hold the row's 64 cells) ----
         float mx = neg_inf();
@@ -243,7 +249,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
                 st[cb][i] = x;
             }
 #pragma unroll
-            for (int i = 0; i < 16; i += 4) mx = fmaxf(mx, max3f(st[cb][i], st[cb][i + 1], fmaxf(st[cb][i + 2], st[cb][i + 3])));
+            for (int i = 0; i < 16; i += 8)
+                mx = max3f(mx, max3f(st[cb][i], st[cb][i + 1], st[cb][i + 2]),
+                           max3f(max3f(st[cb][i + 3], st[cb][i + 4], st[cb][i + 5]), st[cb][i + 6], st[cb][i + 7]));
         }
         {
             auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
@@ -266,17 +274,16 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         // ---- probabilities ----
         const float mc = (m_ref == neg_inf()) ? 0.0f : ((MODE == MODE_FAST) ? m_ref * c2 : m_ref);
         f16x8 pb[4];  // B operands of the four 16-cell steps
-        float psum = 0.0f;
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
+        for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float p = fast_exp2((MODE == MODE_FAST) ? fmaf(st[cb][i], c2, -mc) : st[cb][i] - mc);
-                psum += p;
+                part[i & 3] += p;
                 pb[2 * cb + (i >> 3)][i & 7] = (_Float16)p;
             }
-        }
-        l_sum += psum;
+        l_sum += (part[0] + part[1]) + (part[2] + part[3]);
 
         // Explicit masks: a cell that none of this wave's 32 rows sees may hold NaN bits, so
         // its V^T entries are zeroed in this wave's operands (0 * NaN must not reach O).
@@ -294,12 +301,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         }
 
         // ---- O^T += V^T P^T ----
-        const uint32_t* vt = sh.vt[buf];
+        const char* vt = lds + kVtBase + buf * kVtBytes + vrd;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                u32x4 vop = *reinterpret_cast<const u32x4*>(&vt[((32 * db + rl) * kVtStride + 16 * kk + 8 * hl) >> 1]);
+                u32x4 vop = *reinterpret_cast<const u32x4*>(vt + db * 32 * (kVtStride * 2) + kk * 32);
                 if (MODE == MODE_GENERIC && a.mask) {
 #pragma unroll
                     for (int m2 = 0; m2 < 4; ++m2) vop[m2] &= keep[kk][m2];
@@ -309,11 +316,32 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         }
 
         if (more) {
-            wait_vmcnt<4>();  // V of tile t+1 (issued before its K DMA)
-            store_vt(buf ^ 1);
-            wait_vmcnt<0>();
+            store_vt(buf ^ 1);  // the compiler waits for the V loads
+            wait_vmcnt<0>();    // and the K loads of tile t+1 are in LDS
         }
         __syncthreads();
+    };
+    auto run_tile = [&](int t, auto BUF) {
+        if (MODE == MODE_FAST && t < t_full)
+            tile(t, BUF, std::integral_constant<bool, false>{});
+        else
+            tile(t, BUF, std::integral_constant<bool, true>{});
+    };
+
+    // prologue: tile 0 into buffer 0
+    if (n_tiles > 0) {
+        load_v(0);
+        issue_k(0, 0);
+        wait_vmcnt<4>();  // the V loads (issued first) are back; the K loads may still run
+        store_vt(0);
+        wait_vmcnt<0>();
+    }
+    __syncthreads();
+
+#pragma unroll 1
+    for (int t = 0; t < n_tiles; t += 2) {
+        run_tile(t, std::integral_constant<int, 0>{});
+        if (t + 1 < n_tiles) run_tile(t + 1, std::integral_constant<int, 1>{});
     }
 
     // ---- normalise and write: lane holds dims 32db + 8b + 4hl .. +3 of row j ----
