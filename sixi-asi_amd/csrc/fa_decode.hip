@@ -44,6 +44,8 @@
 // (dequant_q8x8: one f16 rounding of q*d).  Q is quantised to q8_0 exactly as ggml's
 // flash_attn_ext does before the dot (per 32-dim block, d = amax/127) and enters the MFMA as
 // its dequantised f16 values.  (RS = 1 only: up to 48 rows per GQA group.)
+#include <type_traits>
+
 #include "fa_device.hpp"
 
 namespace sixi {
@@ -149,11 +151,13 @@ __device__ __forceinline__ void acc_merge_lds(const MergeBuf<NT, NS>& mg, int sl
 }
 
 // Merges the tile lanes of each row group into tile lane 0: with four lanes (2,3) -> (0,1)
-// then 1 -> 0, with two lanes 1 -> 0.  Every wave must call it.  Returns whether this wave
-// owns its rows afterwards.
+// then 1 -> 0, with two lanes 1 -> 0, with one lane nothing.  Every wave must call it.
+// Returns whether this wave owns its rows afterwards.
 template <int NTW, int TL, int NS>
 __device__ __forceinline__ bool merge_lanes(MergeBuf<NTW, NS>& mg, Acc<NTW>& acc, int rg, int tl, int lane) {
     constexpr int H = TL / 2;  // merge slots per row group
+    static_assert(TL == 1 || TL == 2 || TL == 4, "tile lanes");
+    if (TL == 1) return true;
     if (TL == 4) {
         if (tl >= 2) acc_to_lds(mg, H * rg + tl - 2, acc, lane);
         __syncthreads();
@@ -167,14 +171,14 @@ __device__ __forceinline__ bool merge_lanes(MergeBuf<NTW, NS>& mg, Acc<NTW>& acc
 }
 
 // Inclusive tile prefix over streams into ps[0..S] (run by one wave).
-__device__ void build_tile_prefix(const FaArgs& a, int* ps) {
+__device__ __forceinline__ void build_tile_prefix(const FaArgs& a, int* ps) {
     const int lane = threadIdx.x & 63;
     if (lane == 0) ps[0] = 0;
     int carry = 0;
     for (int base = 0; base < a.S; base += 64) {
         const int s = base + lane;
         int x = 0;
-        if (s < a.S) x = (stream_dims(a, s).nc + kTile - 1) / kTile;
+        if (s < a.S) x = (stream_dims(a, s).nc + a.tile_cells - 1) / a.tile_cells;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const int y = __shfl_up(x, off, 64);
@@ -192,13 +196,6 @@ struct RowInfo {
     int j[NT];       // block row of the lane's row of tile n
     float slope[NT]; // ALiBi slope (explicit masks)
 };
-
-// max over three floats in one instruction (no NaN canonicalisation around it)
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
 
 // One 16-cell tile from a staged ring slot.  MASKED applies the visibility of each row;
 // `after_reads` runs once the slot's LDS reads are consumed.  The phases run over all row
@@ -407,7 +404,7 @@ struct Piece {
 
 // One piece: tiles [tb, te) of segment (s, g).
 template <int NTW, int RS, int KV, int MODE>
-__device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS, KV>& sh, int causal, const Piece& pc) {
+__device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS, KV>& sh, int causal, const Piece& pc) {
     constexpr int NTOT = NTW * RS;
     constexpr int TL = Shape<RS, KV>::lanes;   // tile lanes
     constexpr int NSLOT = Shape<RS, KV>::slots;
@@ -536,21 +533,28 @@ __device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS, KV>& sh, int ca
         if constexpr (KV == SIXI_TYPE_F16) {
             if (RS == 1 || rg == 0) {
                 const uint32_t off = (c0 + r) * knb + c * 16;
+                uint32_t vo4[4];
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) dma16_to_lds(krs, off + ks * 64, base + ks * 1024);
+                for (int ks = 0; ks < 4; ++ks) vo4[ks] = off + ks * 64;
+                dma16x4_to_lds(krs, vo4, base);
             }
             if (RS == 1 || rg == 1) {
                 const uint32_t vo = (c0 + 4 * c) * vnb + r * 16;
+                uint32_t vo4[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dma16_to_lds(vrs, vo + e * vnb, base + (4 + e) * 1024);
+                for (int e = 0; e < 4; ++e) vo4[e] = vo + e * vnb;
+                dma16x4_to_lds(vrs, vo4, base + 4 * 1024);
             }
         } else {
+            static_assert(kQ8Dma == 9, "dword LDS-DMA batch of nine loads");
+            uint32_t ko[kQ8Dma], vo[kQ8Dma];
 #pragma unroll
-            for (int u = 0; u < kQ8Dma; ++u)
-                dma4_to_lds(krs, (c0 + q8_cell[u]) * knb + q8_dw[u] * 4, base + u * 256);
-#pragma unroll
-            for (int u = 0; u < kQ8Dma; ++u)
-                dma4_to_lds(vrs, (c0 + q8_cell[u]) * vnb + q8_dw[u] * 4, base + (kQ8Dma + u) * 256);
+            for (int u = 0; u < kQ8Dma; ++u) {
+                ko[u] = (c0 + q8_cell[u]) * knb + q8_dw[u] * 4;
+                vo[u] = (c0 + q8_cell[u]) * vnb + q8_dw[u] * 4;
+            }
+            dma4x9_to_lds(krs, ko, base);
+            dma4x9_to_lds(vrs, vo, base + kQ8Dma * 256);
         }
     };
     auto step = [&](int i, auto&& after_reads) {
@@ -615,6 +619,350 @@ __device__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS, KV>& sh, int ca
     __syncthreads();  // LDS (q, merge buffers, rings) is reused by the next piece
 }
 
+// ---------------------------------------------------------------------------------------
+// f16 KV, 49..96 rows per GQA group: 32-cell steps.
+//
+// Same split as the kernel above.  A work-group holds WideShape::lanes piece lanes of two
+// waves each: the two waves of a lane are its two row groups (NTW row tiles each), read the
+// same staged steps and each stage half of every step (row group 0 the K rows, row group 1
+// the V rows); the lanes take the piece's steps round robin, and the whole group meets at
+// one barrier per step.  The lanes' (m, l, O) are merged in LDS at the end of the piece.
+// A step covers 32 cells:
+//   * O^T += V^T P^T runs on v_mfma_f32_16x16x32_f16 (the 16x16x16 form issues at half
+//     that rate on gfx950), and each row maximum and Q^T operand covers twice the cells;
+//   * P^T needs no shuffle: the two S^T halves (cells 0-15, 16-31) give lane (r, c) row r
+//     at cells 4c+i and 16+4c+i, and the PV reduction index k = 8c + e is taken to mean
+//     cell 16(e/4) + 4c + e%4; V^T uses the same order;
+//   * V^T comes from LDS with ds_read_b64_tr_b16: the V rows of a step sit in LDS as
+//     [cell][dim] with the 32-byte dim chunks XOR-swizzled by cell%8 (bank-conflict-free
+//     transposed reads); lane (g, j) of a read addresses cell 16h + 4g + j/4 at dims
+//     16db + 4(j%4), so lane (g, i) receives dim 16db + i of cells 16h + 4g .. +3;
+//   * Q^T stays in registers for the whole piece.
+// O layout: lane (r, c) holds row 16n + r, dims 16t + 4c + i at o[t][n][i].
+constexpr int kWide = kDecodeTileWide;  // 32 cells
+constexpr int kWideSlot = 16384;        // K [half][ks][lane] x 16 B, then V: 32 swizzled 256-B rows
+struct WideShape { static constexpr int lanes = 2, waves = 2 * lanes, slots = 2, groups_per_cu = 2; };
+
+template <int NTW>
+struct alignas(256) WideLds {
+    union {
+        u32x4 ring[WideShape::lanes * WideShape::slots * kWideSlot / 16];
+        MergeBuf<NTW, WideShape::lanes> mg;  // reused after the step loop
+    };
+    int ps[kMaxStreams + 1];
+};
+
+template <int NT, int MODE, bool MASKED>
+__device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u32x4* kslot, uint32_t vlane,
+                                          const f16x8 (&qv)[NT][4], int c0,
+                                          const RowInfo<NT>& ri, const char* mrow, int nc, int lane) {
+    const int c = lane >> 4;
+
+    // ---- S^T halves: lane (r, c) receives cells 16h + 4c + i of row r ----
+    f32x4 st[2][NT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const f16x8 kop = as_f16x8(kslot[(h * 4 + ks) * 64 + lane]);
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                st[h][n] = mfma16x16x32(kop, qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
+        }
+    }
+
+    // ---- scores (FAST: raw dot products; GENERIC: log2-domain logits) and row maxima ----
+    const float c2 = a.scale_log2;
+    float sv[NT][8];
+    float mx[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int cell = c0 + 16 * (e >> 2) + 4 * c + (e & 3);
+            float x = st[e >> 2][n][e & 3];
+            if (MODE == MODE_GENERIC) {
+                x *= a.scale;
+                if (a.softcap != 0.0f) x = a.softcap * tanhf(x);
+                if (a.mask) {
+                    float mv = neg_inf();
+                    if (cell < nc) {
+                        const uint16_t bits = *reinterpret_cast<const uint16_t*>(
+                            mrow + (int64_t)ri.j[n] * a.m_nb1 + (int64_t)cell * 2);
+                        mv = ri.slope[n] * half_bits_to_float(bits);
+                    }
+                    x = (mv == neg_inf()) ? neg_inf() : x + mv;
+                } else if (cell >= ri.vis[n]) {
+                    x = neg_inf();
+                }
+                x *= kLog2e;
+            } else if (MASKED) {
+                if (cell >= ri.vis[n]) x = neg_inf();
+            }
+            sv[n][e] = x;
+        }
+        mx[n] = max4_rowgroups(max3f(max3f(sv[n][0], sv[n][1], sv[n][2]), max3f(sv[n][3], sv[n][4], sv[n][5]),
+                                     max2f(sv[n][6], sv[n][7])));
+    }
+
+    // ---- lazy exponent reference (as in tile_step) ----
+    const float thr = (MODE == MODE_FAST) ? kLazyLog2 / c2 : kLazyLog2;
+    bool need[NT];
+    bool need_any = false;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        need[n] = mx[n] > acc.m[n] + thr;
+        need_any |= need[n];
+    }
+    if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            float alpha = 1.0f;
+            if (need[n]) {
+                alpha = fast_exp2((MODE == MODE_FAST) ? (acc.m[n] - mx[n]) * c2 : acc.m[n] - mx[n]);
+                acc.m[n] = mx[n];
+            }
+            acc.l[n] *= alpha;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc.o[t][n] *= alpha;
+        }
+    }
+
+    // ---- probabilities: P^T operand in the lane's own cell order, f32 row sums ----
+    f16x8 pt[NT];
+    u32x4 keep[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const float ref = acc.m[n];
+        const float mc = (ref == neg_inf()) ? 0.0f : ((MODE == MODE_FAST) ? ref * c2 : ref);
+        float ps[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            ps[e] = fast_exp2((MODE == MODE_FAST) ? fmaf(sv[n][e], c2, -mc) : sv[n][e] - mc);
+            pt[n][e] = (_Float16)ps[e];
+        }
+        acc.l[n] += ((ps[0] + ps[1]) + (ps[2] + ps[3])) + ((ps[4] + ps[5]) + (ps[6] + ps[7]));
+        if (MODE == MODE_GENERIC && a.mask) {
+            // explicit masks: a cell that none of these 16 rows sees may hold NaN bits, so
+            // its V^T column is zeroed for them (0 * NaN must not reach the accumulator)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint64_t b0 = __builtin_amdgcn_ballot_w64((float)pt[n][2 * w] != 0.0f);
+                const uint64_t b1 = __builtin_amdgcn_ballot_w64((float)pt[n][2 * w + 1] != 0.0f);
+                keep[n][w] = ((((b0 >> (16 * c)) & 0xffffull) != 0) ? 0x0000ffffu : 0u) |
+                             ((((b1 >> (16 * c)) & 0xffffull) != 0) ? 0xffff0000u : 0u);
+            }
+        }
+    }
+
+    // ---- O^T += V^T P^T, V^T from transposed LDS reads (vlane ^ 32t: chunk t of the lane's row) ----
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const lds_char* vp = lds_ptr(vlane ^ (32u * t));
+        const u32x2 lo = ld_tr16(vp);
+        const u32x2 hi = ld_tr16(vp + 4096);
+        const u32x4 vt = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+            if (MODE == MODE_GENERIC && a.mask)
+                acc.o[t][n] = mfma16x16x32(as_f16x8(vt & keep[n]), pt[n], acc.o[t][n]);
+            else
+                acc.o[t][n] = mfma16x16x32(as_f16x8(vt), pt[n], acc.o[t][n]);
+        }
+    }
+}
+
+// Normalised rows (O layout of the 32-cell kernel).
+template <int NT>
+__device__ __forceinline__ void write_rows_wide(const FaArgs& a, const Acc<NT>& acc, int n0, int s, int g, int R,
+                                                int lane) {
+    const int r = lane & 15, c = lane >> 4;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        if (row >= R) continue;
+        const int j = row / a.G;
+        const int h = g * a.G + row % a.G;
+        const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
+        char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + c * 16;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) st16(dst + t * 64, acc.o[t][n] * inv);
+    }
+}
+
+// Partial slot (same format as write_partial) from the 32-cell kernel's O layout.
+template <int NT>
+__device__ __forceinline__ void write_partial_wide(float* slot, int rows_slot, int n0, int R, const Acc<NT>& acc,
+                                                   int lane) {
+    const int r = lane & 15, c = lane >> 4;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        if (row >= R) continue;
+        char* dst = reinterpret_cast<char*>(slot + (int64_t)row * 128) + c * 16;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) st16(dst + t * 64, acc.o[t][n]);
+        if (c == 0) {
+            slot[(int64_t)rows_slot * 128 + row] = acc.m[n];
+            slot[(int64_t)rows_slot * 129 + row] = acc.l[n];
+        }
+    }
+}
+
+// One piece of the 32-cell kernel: steps [tb, te) of segment (s, g).
+template <int NTW, int MODE>
+__device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW>& sh, int causal, const Piece& pc) {
+    constexpr int TL = WideShape::lanes;
+    constexpr int NS = WideShape::slots;
+    constexpr int SLOT16 = kWideSlot / 16;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int rg = w / TL;
+    const int tl = w % TL;
+    const int r = lane & 15;
+    const int c = lane >> 4;
+    const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
+    const StreamDims sd = stream_dims(a, s);
+    const int G = a.G;
+    const int R = G * sd.ql;
+    const int n0 = rg * NTW;
+
+    // ---- Q^T operands in registers: row 16(n0+n) + r, dims 32ks + 8c .. +7 ----
+    f16x8 qv[NTW][4];
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        const bool valid = row < R;
+        const int j = valid ? row / G : 0;
+        const int h = g * G + (valid ? row % G : 0);
+        const char* src = a.q + (int64_t)j * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3 +
+                          (int64_t)(8 * c) * a.q_es;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            f16x8 hv = {};
+            if (valid) {
+                const char* p = src + (int64_t)(32 * ks) * a.q_es;
+                if (a.q_f16) {
+                    hv = as_f16x8(ld16(p));
+                } else {
+                    const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+                    const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 16);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        hv[e] = (_Float16)lo[e];
+                        hv[4 + e] = (_Float16)hi[e];
+                    }
+                }
+            }
+            qv[n][ks] = hv;
+        }
+    }
+
+    RowInfo<NTW> ri;
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        const bool valid = row < R;
+        const int j = valid ? row / G : 0;
+        ri.j[n] = j;
+        ri.vis[n] = (valid && causal) ? sd.kl + j + 1 : sd.nc;
+        ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, g * G + (valid ? row % G : 0)) : 1.0f;
+    }
+    // steps below t_full see no masked cell for any row
+    const int t_full = (MODE == MODE_GENERIC) ? 0 : (causal ? (sd.kl + 1) / kWide : sd.nc / kWide);
+    const char* mrow = nullptr;
+    if (MODE == MODE_GENERIC && a.mask) mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3;
+
+    Acc<NTW> acc;
+    acc_clear(acc);
+
+    // cells >= nc read as zeros through the range-checked resources (and are masked)
+    const buf_rsrc krs = make_rsrc_uniform(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
+                                           (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + 256));
+    const buf_rsrc vrs = make_rsrc_uniform(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
+                                           (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + 256));
+    const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
+    // LDS-DMA source offsets from a step's first cell.  K (row group 0), load (h, ks): lane
+    // (r, c) copies cell 16h + r, dims 32ks + 8c .. +7 to [h][ks][lane].  V (row group 1),
+    // load u: lane t fills LDS row 4u + t/16 at 16-byte position t%16, i.e. 32-byte chunk
+    // (t%16)/2 of that row, which holds dims 16 * (chunk ^ (row % 8)).
+    const uint32_t koff = (uint32_t)r * knb + 16u * c;
+    uint32_t voff[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        voff[u] = (uint32_t)(lane >> 4) * vnb + 32u * (((lane & 15) >> 1) ^ (4 * u + (lane >> 4))) + 16u * (lane & 1);
+    // transposed reads of a slot's V rows: lane (c, r) reads cell 4c + r/4 (+16h), dims
+    // 16t + 4(r%4) .. +3, found in 32-byte chunk t ^ (cell % 8) of the row.  The row offset
+    // has bits 5..7 clear, so chunk t lies at (row + 32*(cell % 8) + 8(r%4)) ^ 32t.
+    const uint32_t vrow = (uint32_t)(4 * c + (r >> 2)) * 256u + 32u * (4 * (c & 1) + (r >> 2)) + 8u * (r & 3);
+
+    // steps of this lane: tb + tl + TL*i, i < n_my; n_iter is the same for the whole group
+    const int t0 = tb + tl;
+    const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
+    const int n_iter = (te - tb + TL - 1) / TL;
+    u32x4* ring = sh.ring + (size_t)tl * NS * SLOT16;
+    const uint32_t ring_base = lds_addr(ring);
+
+    auto issue = [&](int i, int slot) {
+        const uint32_t c0 = (uint32_t)(t0 + i * TL) * kWide;
+        const uint32_t base = ring_base + (uint32_t)slot * kWideSlot;
+        uint32_t o8[8];
+        if (rg == 0) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) o8[h * 4 + ks] = (c0 + 16 * h) * knb + koff + ks * 64;
+            dma16x8_to_lds(krs, o8, base);
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o8[u] = (c0 + 4 * u) * vnb + voff[u & 1];
+            dma16x8_to_lds(vrs, o8, base + 8192);
+        }
+    };
+    // step i reads slot i % NS.  After the barrier of step i every wave has left step i-1,
+    // so step i+NS-1 goes into its slot; NS-2 steps stay in flight behind step i.
+    static_assert(NS >= 2 && NS <= 4, "ring depth");
+#pragma unroll
+    for (int k = 0; k < NS - 1; ++k)
+        if (k < n_my) issue(k, k);
+#pragma unroll 1
+    for (int i = 0; i < n_iter; ++i) {
+        const int ahead = n_my - 1 - i;  // own steps issued after step i
+        if (NS >= 4 && ahead >= 2) wait_vmcnt<16>();
+        else if (NS >= 3 && ahead >= 1) wait_vmcnt<8>();
+        else wait_vmcnt<0>();
+        __syncthreads();
+        if (i + NS - 1 < n_my) issue(i + NS - 1, (i + NS - 1) % NS);
+        if (i < n_my) {
+            const int t = t0 + i * TL;
+            const int sl = i % NS;
+            const u32x4* kslot = ring + sl * SLOT16;
+            // the V area is 256-byte aligned, so ^ 32t only moves bits 5..7 of vrow
+            const uint32_t vlane = ring_base + sl * kWideSlot + 8192 + vrow;
+            if (t < t_full)
+                wide_step<NTW, MODE, false>(a, acc, kslot, vlane, qv, t * kWide, ri, mrow, sd.nc, lane);
+            else
+                wide_step<NTW, MODE, true>(a, acc, kslot, vlane, qv, t * kWide, ri, mrow, sd.nc, lane);
+        }
+    }
+
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) {
+        acc.l[n] = sum4_rowgroups(acc.l[n]);
+        if (MODE == MODE_FAST && acc.m[n] != neg_inf()) acc.m[n] *= a.scale_log2;
+    }
+
+    __syncthreads();  // every wave is past its ring (each drained its own loads)
+    if (merge_lanes<NTW, TL>(sh.mg, acc, rg, tl, lane)) {
+        if (tb == 0 && te == pc.nt_seg)
+            write_rows_wide(a, acc, n0, s, g, R, lane);
+        else
+            write_partial_wide(a.part + pc.slot * a.slot_floats, NTW * 2 * 16, n0, R, acc, lane);
+    }
+    __syncthreads();  // LDS (merge buffers, rings) is reused by the next piece
+}
+
 // Work-group -> tile range.  Returns false for a work-group without tiles.
 struct Partition {
     int64_t T, P, x0, x1;
@@ -633,29 +981,25 @@ __device__ __forceinline__ bool partition(const FaArgs& a, const int* ps, int b,
     return true;
 }
 
-template <int NTW, int RS, int KV, int MODE>
-__global__ __launch_bounds__((Shape<RS, KV>::waves * 64), (Shape<RS, KV>::groups_per_cu)) void decode_d128(
-    FaArgs a, int causal) {
-    __shared__ DecodeLds<NTW, RS, KV> sh;
-    const int tid = threadIdx.x;
-    if (tid < 64) build_tile_prefix(a, sh.ps);
-    __syncthreads();
+// Runs fn(piece) for every piece of this work-group's tile range, in order.
+template <typename F>
+__device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F&& fn) {
     Partition pt;
-    if (!partition(a, sh.ps, blockIdx.x, pt)) return;
+    if (!partition(a, ps, blockIdx.x, pt)) return;
     const int64_t Hkv = a.Hkv;
 
     // stream holding tile x0: the largest s with Hkv*ps[s] <= x0
     int lo = 0, hi = a.S;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (Hkv * sh.ps[mid] <= pt.x0) lo = mid; else hi = mid - 1;
+        if (Hkv * ps[mid] <= pt.x0) lo = mid; else hi = mid - 1;
     }
     int s = lo;
     int64_t x = pt.x0;
     while (x < pt.x1) {
-        while (Hkv * sh.ps[s + 1] <= x) ++s;
-        const int nt = sh.ps[s + 1] - sh.ps[s];
-        const int64_t cs = Hkv * sh.ps[s];
+        while (Hkv * ps[s + 1] <= x) ++s;
+        const int nt = ps[s + 1] - ps[s];
+        const int64_t cs = Hkv * ps[s];
         const int g = (int)((x - cs) / nt);
         const int64_t ck = cs + (int64_t)g * nt;
         Piece pc;
@@ -665,9 +1009,27 @@ __global__ __launch_bounds__((Shape<RS, KV>::waves * 64), (Shape<RS, KV>::groups
         pc.te = (int)(min(pt.x1, ck + nt) - ck);
         pc.nt_seg = nt;
         pc.slot = (int64_t)s * Hkv + g + pt.p_log;
-        decode_piece<NTW, RS, KV, MODE>(a, sh, causal, pc);
+        fn(pc);
         x = ck + pc.te;
     }
+}
+
+template <int NTW, int RS, int KV, int MODE>
+__global__ __launch_bounds__((Shape<RS, KV>::waves * 64), (Shape<RS, KV>::groups_per_cu)) void decode_d128(
+    FaArgs a, int causal) {
+    __shared__ DecodeLds<NTW, RS, KV> sh;
+    if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
+    __syncthreads();
+    for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, RS, KV, MODE>(a, sh, causal, pc); });
+}
+
+template <int NTW, int MODE>
+__global__ __launch_bounds__((WideShape::waves * 64), (WideShape::waves * WideShape::groups_per_cu / 4)) void
+decode_wide_d128(FaArgs a, int causal) {
+    __shared__ WideLds<NTW> sh;
+    if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
+    __syncthreads();
+    for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece_wide<NTW, MODE>(a, sh, causal, pc); });
 }
 
 // Combines the pieces of every segment that more than one work-group touched, in the order
@@ -718,6 +1080,21 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
 }
 
+template <int NTW>
+hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
+    const dim3 grid(a.P), block(WideShape::waves * 64);
+    if (generic)
+        hipLaunchKernelGGL((decode_wide_d128<NTW, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+    else
+        hipLaunchKernelGGL((decode_wide_d128<NTW, MODE_FAST>), grid, block, 0, stream, a, causal);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int rows_slot = NTW * 2 * 16;
+    hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
+                       a, rows_slot);
+    return hipGetLastError();
+}
+
 template <int NTW, int RS, int KV>
 hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
     const dim3 grid(a.P), block(Shape<RS, KV>::waves * 64);
@@ -736,8 +1113,8 @@ hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stre
 }  // namespace
 
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
-    const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + kTile - 1) / kTile);
-    const int per_cu = row_tiles <= 3 ? Shape<1, SIXI_TYPE_F16>::groups_per_cu : Shape<2, SIXI_TYPE_F16>::groups_per_cu;
+    const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + a.tile_cells - 1) / a.tile_cells);
+    const int per_cu = row_tiles <= 3 ? Shape<1, SIXI_TYPE_F16>::groups_per_cu : WideShape::groups_per_cu;
     int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
     if (P > kMaxSplitGroups) P = kMaxSplitGroups;
     if (P > tiles_max) P = tiles_max;
@@ -758,8 +1135,8 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
             case 1: return launch_nt<1, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
             case 2: return launch_nt<2, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
             case 3: return launch_nt<3, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 4: return launch_nt<2, 2, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 6: return launch_nt<3, 2, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 4: return launch_wide<2>(a, generic, causal, stream);
+            case 6: return launch_wide<3>(a, generic, causal, stream);
             default: return hipErrorNotSupported;
         }
     }

@@ -42,6 +42,14 @@ typedef __amdgpu_buffer_rsrc_t buf_rsrc;
 __device__ __forceinline__ buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+// The same for a base and size that are uniform but that the compiler cannot prove so
+// (the inline-asm LDS-DMA loads need the resource in SGPRs).
+__device__ __forceinline__ buf_rsrc make_rsrc_uniform(const void* base, uint32_t bytes) {
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+    return make_rsrc(reinterpret_cast<const void*>((hi << 32) | lo), (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes));
+}
 __device__ __forceinline__ u32x4 buf_ld16(buf_rsrc r, uint32_t off) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
@@ -52,41 +60,126 @@ __device__ __forceinline__ uint32_t buf_ld4(buf_rsrc r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
-// 16 bytes per lane from buffer offset `voff` straight into LDS at `lds_addr` + 16*lane
-// (gfx950 buffer_load_dwordx4 ... lds).  Issued from asm so that the compiler does not
-// drain every LDS-DMA load before each LDS read; the caller waits with wait_vmcnt<N>.
-// m0 is saved and restored; the s_nop covers the m0-write -> LDS-DMA hazard.
-__device__ __forceinline__ void dma16_to_lds(buf_rsrc rsrc, uint32_t voff, uint32_t lds_addr) {
+// Batches of direct global->LDS loads (gfx950 buffer_load_dword{,x4} ... lds).  Load u of a
+// batch reads buffer offset v[u] into LDS at lds + stride*u + (bytes per lane)*lane.  They are
+// issued from asm so that the compiler does not drain every LDS-DMA load before each LDS
+// read; the caller waits with wait_vmcnt<N>.  One asm block per batch, so nothing is
+// scheduled between its loads: the block opens with the five wait states a VMEM read of an
+// SGPR written by a VALU instruction needs (v_readfirstlane, SGPR-spill restores: the
+// compiler does not see the resource read inside the asm), and the s_nop after each M0
+// write covers the M0 -> LDS-DMA hazard.  M0 is restored at the end.
+__device__ __forceinline__ void dma16x4_to_lds(buf_rsrc rs, const uint32_t (&v)[4], uint32_t lds) {
     int saved;
     asm volatile(
+        "s_nop 4\n\t"
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "buffer_load_dwordx4 %2, %6, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %3, %6, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %4, %6, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %5, %6, 0 offen lds\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc)
-        : "memory");
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "s"(rs)
+        : "memory", "scc");
 }
-// 4 bytes per lane from buffer offset `voff` into LDS at `lds_addr` + 4*lane
-// (buffer_load_dword ... lds); used for rows whose alignment is only 4 bytes (q8_0).
-__device__ __forceinline__ void dma4_to_lds(buf_rsrc rsrc, uint32_t voff, uint32_t lds_addr) {
+__device__ __forceinline__ void dma16x8_to_lds(buf_rsrc rs, const uint32_t (&v)[8], uint32_t lds) {
     int saved;
     asm volatile(
+        "s_nop 4\n\t"
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dword %2, %3, 0 offen lds\n\t"
+        "buffer_load_dwordx4 %2, %10, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %3, %10, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %4, %10, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %5, %10, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %6, %10, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %7, %10, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %8, %10, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %9, %10, 0 offen lds\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc)
-        : "memory");
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "s"(rs)
+        : "memory", "scc");
+}
+// 4 bytes per lane, LDS stride 256: q8_0 rows, whose alignment is only 4 bytes.
+__device__ __forceinline__ void dma4x9_to_lds(buf_rsrc rs, const uint32_t (&v)[9], uint32_t lds) {
+    int saved;
+    asm volatile(
+        "s_nop 4\n\t"
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %2, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %3, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %4, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %5, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %6, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %7, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %8, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %9, %11, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 256\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %10, %11, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "v"(v[8]), "s"(rs)
+        : "memory", "scc");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Transposed LDS read (gfx950 ds_read_b64_tr_b16).  Within each group of 16 lanes, lane i
+// receives as element e the 16-bit value i%4 of the 8 bytes addressed by lane 4e + i/4 of
+// the group; `p` must be 8-byte aligned.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ u32x2 ld_tr16(const lds_char* p) {
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)const_cast<lds_char*>(p)));
+}
+
+// LDS pointer from an LDS byte address.
+__device__ __forceinline__ const lds_char* lds_ptr(uint32_t addr) { return (const lds_char*)(size_t)addr; }
 
 // LDS byte address of a __shared__ object.
 template <typename T>
@@ -110,11 +203,19 @@ __device__ __forceinline__ void st16(char* p, f32x4 v) { *reinterpret_cast<f32x4
 // Reductions over the four lanes l, l^16, l^32, l^48 (the lane groups of one MFMA column)
 // with the gfx950 row-swap permutes (VALU only, no LDS round trip).  Each swap returns both
 // halves, so max/sum of the pair is the reduction over {l, l^32} (resp. {l, l^16}).
+// Maxima with IEEE-754 2019 `maximum` semantics (NaN propagates), which gfx950 issues as one
+// v_maximum3_f32 with no operand canonicalisation (fmaxf would first canonicalise every
+// MFMA result).  These are compiler builtins, not inline asm, so the hazard recognizer adds
+// the wait states a read of a fresh MFMA result needs.
+__device__ __forceinline__ float max2f(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
 __device__ __forceinline__ float max4_rowgroups(float x) {
     auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    x = max2f(__uint_as_float(a[0]), __uint_as_float(a[1]));
     auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    return max2f(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum4_rowgroups(float x) {
     auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);

@@ -43,6 +43,7 @@ struct FaArgs {
     float* part;           // partial slots of slot_floats floats: O rows [rows][128], then m, l
     int32_t P;             // work-groups of the split-K launch
     int32_t xcd_remap;     // 1: consecutive tile ranges go to work-groups of one XCD
+    int32_t tile_cells;    // KV cells per split tile (decode_tile_cells)
     int64_t slot_floats;   // floats per partial slot
 };
 
@@ -53,12 +54,17 @@ hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_
                           hipStream_t stream);
 
 // Sizing rules shared by the dispatcher and the launchers.
-constexpr int kDecodeTile = 16;        // KV cells per wave step of the decode kernel
+constexpr int kDecodeTile = 16;        // KV cells per wave step of the decode kernel (<= 48 rows, q8_0)
+constexpr int kDecodeTileWide = 32;    // KV cells per step of the f16 kernel for 49..96 rows
 constexpr int kDecodeMaxRowTiles = 6;  // 16-row MFMA tiles per (stream, kv-head): G*q_len <= 96
 constexpr int kMaxStreams = 512;       // LDS prefix table bound
 constexpr int kMaxSplitGroups = 2048;  // work-groups of a split-K launch (workspace bound)
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles);
+// Cells per split tile of the decode launch for this KV type and row-tile count.
+inline int decode_tile_cells(int kv_type, int row_tiles) {
+    return (kv_type == SIXI_TYPE_F16 && row_tiles > 3) ? kDecodeTileWide : kDecodeTile;
+}
 // Row tiles the decode kernel runs for `rows` = G * n_q rows: up to 3 per wave; beyond
 // that two row groups of equal size (so 5 tiles run as 6).
 inline int decode_row_tiles(int64_t rows) {

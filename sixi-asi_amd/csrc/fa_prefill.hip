@@ -51,12 +51,6 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float max3f(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-
 // position of cell offset co (0..63) inside a V^T row: the middle quads of every 16-cell
 // group are swapped, so that the B-operand order of P^T is contiguous
 __device__ __forceinline__ int vt_pos(int co) {
@@ -158,9 +152,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     auto issue_k = [&](int t, int buf) {
         const int64_t o = (int64_t)t * kBN * knb;
         const buf_rsrc rs = make_rsrc(kbase + o, (uint32_t)(kbytes > o ? kbytes - o : 0));
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4)
-            dma16_to_lds(rs, kdo[u4], lds0 + buf * kKBytes + (4 * w + u4) * 1024);
+        dma16x4_to_lds(rs, kdo, lds0 + buf * kKBytes + 4 * w * 1024);
     };
     u32x4 vreg[2][2];
     auto load_v = [&](int t) {

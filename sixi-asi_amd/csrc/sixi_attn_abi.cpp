@@ -119,7 +119,7 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     if (o.nb[1] < D * 4 || q.nb[1] < D * qes) return SIXI_E_INVALID_ARGUMENT;
     // one stream's cells (plus one tile of read-ahead) are addressed with 32-bit offsets
     int64_t kspan = 0, vspan = 0;
-    if (!mul_ok(n_kv + sixi::kDecodeTile, k.nb[1], &kspan) || !mul_ok(n_kv + sixi::kDecodeTile, v.nb[1], &vspan) ||
+    if (!mul_ok(n_kv + sixi::kDecodeTileWide, k.nb[1], &kspan) || !mul_ok(n_kv + sixi::kDecodeTileWide, v.nb[1], &vspan) ||
         kspan >= (int64_t)UINT32_MAX || vspan >= (int64_t)UINT32_MAX)
         return SIXI_E_UNSUPPORTED;
     if (view_span(q, D * qes) < 0 || view_span(k, kvrow) < 0 || view_span(v, kvrow) < 0 ||
@@ -232,6 +232,7 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     hipStream_t stream = static_cast<hipStream_t>(p->stream);
     hipError_t e;
     if (pl.splitk) {
+        a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles);
         a.P = sixi::decode_num_groups(a, cu_count_cached(), pl.row_tiles);
         a.xcd_remap = 0;
         e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D, pl.row_tiles, stream);

@@ -80,6 +80,8 @@ def test_batched_verify_parity(fa):
 @pytest.mark.parametrize("kv_len,q_len,H,Hkv", [
     ([0, 5, 100, 31], [1, 3, 16, 7], 24, 4),     # empty cache, ragged rows, 96 rows max
     ([64, 1000, 2], [7, 7, 7], 24, 4),           # 42 rows: 3 row tiles
+    ([3000, 45, 0, 511], [16, 13, 4, 16], 32, 8),  # GQA 4:1, 64 rows: 4 row tiles
+    ([129, 2048], [16, 11], 40, 8),              # GQA 5:1, 80 rows: 5 row tiles run as 6
     ([300, 33], [2, 2], 8, 8),                   # no GQA
     ([4096, 77], [5, 9], 32, 2),                 # GQA 16:1, 144 > 96 rows -> not split-K
 ])
