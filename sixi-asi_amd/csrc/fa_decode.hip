@@ -59,6 +59,20 @@ constexpr int kMaxPieces = 16;      // target bound on the pieces of one full-le
 
 enum { MODE_FAST = 0, MODE_GENERIC = 1 };
 
+// Per-stream (rows, cached cells), kept in LDS so that a piece reads its extents there.
+struct StreamTable {
+    int ps[kMaxStreams + 1];  // inclusive tile prefix over streams
+    int2 dims[kMaxStreams];   // (ql, kl) of every stream
+};
+// (every lane reads the same entry; readfirstlane tells the compiler the values are uniform)
+__device__ __forceinline__ StreamDims table_dims(const StreamTable& t, int s) {
+    StreamDims d;
+    d.ql = __builtin_amdgcn_readfirstlane(t.dims[s].x);
+    d.kl = __builtin_amdgcn_readfirstlane(t.dims[s].y);
+    d.nc = d.ql > 0 ? d.kl + d.ql : 0;
+    return d;
+}
+
 // Per KV type: bytes of one ring slot (one 16-cell tile of K and V) and LDS-DMA loads
 // a tile takes (per wave when one wave stages it all).
 template <int KV> struct KvTile;
@@ -88,7 +102,7 @@ struct DecodeLds {
         } t;
         MergeBuf<NTW, RS * Sh::lanes / 2> mg;  // reused after the tile loop
     };
-    int ps[kMaxStreams + 1];
+    int ps[kMaxStreams + 1];  // (no extents table: it would not leave room for two groups per CU)
 };
 
 template <int NT>
@@ -170,15 +184,20 @@ __device__ __forceinline__ bool merge_lanes(MergeBuf<NTW, NS>& mg, Acc<NTW>& acc
     return tl == 0;
 }
 
-// Inclusive tile prefix over streams into ps[0..S] (run by one wave).
-__device__ __forceinline__ void build_tile_prefix(const FaArgs& a, int* ps) {
+// Inclusive prefix of segment costs over streams into ps[0..S] (a stream with rows weighs
+// tiles + seg_cost per kv-head) and, if given, the stream extents (run by one wave).
+__device__ __forceinline__ void build_tile_prefix(const FaArgs& a, int* ps, int2* dims = nullptr) {
     const int lane = threadIdx.x & 63;
     if (lane == 0) ps[0] = 0;
     int carry = 0;
     for (int base = 0; base < a.S; base += 64) {
         const int s = base + lane;
         int x = 0;
-        if (s < a.S) x = (stream_dims(a, s).nc + a.tile_cells - 1) / a.tile_cells;
+        if (s < a.S) {
+            const StreamDims d = stream_dims(a, s < a.S ? s : 0);
+            x = d.nc > 0 ? (d.nc + a.tile_cells - 1) / a.tile_cells + a.seg_cost : 0;
+            if (dims) dims[s] = int2{d.ql, d.kl};
+        }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const int y = __shfl_up(x, off, 64);
@@ -426,54 +445,74 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS,
     const int n0 = rg * NTW;  // first row tile of this wave
 
     // ---- Q rows of the group -> f16 B operands in LDS (row 16n+r, dims 32ks+8c..+7) ----
-    for (int idx = tid; idx < NTOT * 16 * 16; idx += NTHREADS) {
+    // Item idx = tid + k*NTHREADS is row idx/16, 8-dim chunk idx%16.  Every load is issued
+    // before any is used (padding rows read row 0, which every piece has), so the staging
+    // costs one memory latency.
+    constexpr int QIT = NTOT * 16 * 16 / NTHREADS;
+    static_assert(QIT * NTHREADS == NTOT * 16 * 16, "Q items per thread");
+    const char* qsrc[QIT];
+    bool qok[QIT];
+#pragma unroll
+    for (int k = 0; k < QIT; ++k) {
+        const int idx = tid + k * NTHREADS;
         const int row = idx >> 4;
-        const int chunk = idx & 15;  // 8-dim chunk: ks = chunk/4, c = chunk%4
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (row < R) {
-            const int j = row / G;
-            const int h = g * G + row % G;
-            const char* src = a.q + (int64_t)j * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3 +
-                              (int64_t)chunk * 8 * a.q_es;
-            float xv[8];
-            if (a.q_f16) {
-                const f16x8 hq = as_f16x8(ld16(src));
+        qok[k] = row < R;
+        const int rr = qok[k] ? row : 0;
+        qsrc[k] = a.q + (int64_t)(rr / G) * a.q_nb1 + (int64_t)(g * G + rr % G) * a.q_nb2 + (int64_t)s * a.q_nb3 +
+                  (int64_t)(idx & 15) * 8 * a.q_es;
+    }
+    float xv[QIT][8];
+    if (a.q_f16) {
+        u32x4 raw[QIT];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xv[e] = (float)hq[e];
-            } else {
-                const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
-                const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 16);
+        for (int k = 0; k < QIT; ++k) raw[k] = ld16(qsrc[k]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    xv[e] = lo[e];
-                    xv[4 + e] = hi[e];
-                }
-            }
-            f16x8 hv;
-            if constexpr (KV == SIXI_TYPE_Q8_0) {
-                // ggml converts Q to the K dot type: q8_0 per 32-dim block, d = amax/127,
-                // q = round-half-away(x * 127/amax) clamped to +-127; the MFMA takes q*d
-                float am = 0.0f;
+        for (int k = 0; k < QIT; ++k)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(xv[e]));
-                am = fmaxf(am, __shfl_xor(am, 1, 64));
-                am = fmaxf(am, __shfl_xor(am, 2, 64));
-                const float d = am / 127.0f;
-                const float id = d != 0.0f ? 127.0f / am : 0.0f;
-                const _Float16 dh = (_Float16)d;
+            for (int e = 0; e < 8; ++e) xv[k][e] = (float)as_f16x8(raw[k])[e];
+    } else {
+        f32x4 lo[QIT], hi[QIT];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float qv = fminf(fmaxf(roundf(xv[e] * id), -127.0f), 127.0f);
-                    hv[e] = (_Float16)(qv * (float)dh);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) hv[e] = (_Float16)xv[e];
-            }
-            val = as_u32x4(hv);
+        for (int k = 0; k < QIT; ++k) {
+            lo[k] = *reinterpret_cast<const f32x4*>(qsrc[k]);
+            hi[k] = *reinterpret_cast<const f32x4*>(qsrc[k] + 16);
         }
+#pragma unroll
+        for (int k = 0; k < QIT; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xv[k][e] = lo[k][e];
+                xv[k][4 + e] = hi[k][e];
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < QIT; ++k) {
+        f16x8 hv;
+        if constexpr (KV == SIXI_TYPE_Q8_0) {
+            // ggml converts Q to the K dot type: q8_0 per 32-dim block, d = amax/127,
+            // q = round-half-away(x * 127/amax) clamped to +-127; the MFMA takes q*d
+            float am = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(xv[k][e]));
+            am = fmaxf(am, __shfl_xor(am, 1, 64));
+            am = fmaxf(am, __shfl_xor(am, 2, 64));
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 127.0f / am : 0.0f;
+            const _Float16 dh = (_Float16)d;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float qv = fminf(fmaxf(roundf(xv[k][e] * id), -127.0f), 127.0f);
+                hv[e] = (_Float16)(qv * (float)dh);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = (_Float16)xv[k][e];
+        }
+        const int idx = tid + k * NTHREADS;
+        const int row = idx >> 4;
+        const int chunk = idx & 15;  // ks = chunk/4, c = chunk%4
         const int n = row >> 4, rr = row & 15, ks = chunk >> 2, cc = chunk & 3;
-        sh.t.q[(n * 4 + ks) * 64 + cc * 16 + rr] = val;
+        sh.t.q[(n * 4 + ks) * 64 + cc * 16 + rr] = qok[k] ? as_u32x4(hv) : u32x4{0u, 0u, 0u, 0u};
     }
     __syncthreads();
 
@@ -641,16 +680,72 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS,
 // O layout: lane (r, c) holds row 16n + r, dims 16t + 4c + i at o[t][n][i].
 constexpr int kWide = kDecodeTileWide;  // 32 cells
 constexpr int kWideSlot = 16384;        // K [half][ks][lane] x 16 B, then V: 32 swizzled 256-B rows
-struct WideShape { static constexpr int lanes = 2, waves = 2 * lanes, slots = 2, groups_per_cu = 2; };
+struct WideShape { static constexpr int lanes = 2, slots = 2, groups_per_cu = 2; };
+struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
+constexpr WideSplit kWide64 = {2, 2};         // 64 rows
+constexpr WideSplit kWide96 = {3, 2};         // 96 rows
 
-template <int NTW>
+// RS row groups (waves per lane) of NTW row tiles each.
+template <int NTW, int RS>
 struct alignas(256) WideLds {
     union {
         u32x4 ring[WideShape::lanes * WideShape::slots * kWideSlot / 16];
-        MergeBuf<NTW, WideShape::lanes> mg;  // reused after the step loop
+        MergeBuf<NTW, RS * WideShape::lanes / 2> mg;  // reused after the step loop
     };
-    int ps[kMaxStreams + 1];
+    StreamTable st;
 };
+
+// Q^T B operands of row tiles n0 .. n0+NT-1 in registers: lane (r, c) gets row 16(n0+n) + r
+// at dims 32ks + 8c .. +7 as f16 (rows >= R are zero).  All loads are issued before any is
+// used -- padding rows read row 0, which every piece has -- so the piece start pays one
+// memory latency, not one per operand.
+template <int NT>
+__device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, int R, int n0, int lane,
+                                                f16x8 (&qv)[NT][4]) {
+    const int r = lane & 15, c = lane >> 4;
+    const char* src[NT];
+    bool valid[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        valid[n] = row < R;
+        const int rr = valid[n] ? row : 0;
+        src[n] = a.q + (int64_t)(rr / a.G) * a.q_nb1 + (int64_t)(g * a.G + rr % a.G) * a.q_nb2 +
+                 (int64_t)s * a.q_nb3 + (int64_t)(8 * c) * a.q_es;
+    }
+    if (a.q_f16) {
+        u32x4 raw[NT][4];
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) raw[n][ks] = ld16(src[n] + 64 * ks);
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qv[n][ks] = valid[n] ? as_f16x8(raw[n][ks]) : f16x8{};
+    } else {
+        f32x4 raw[NT][4][2];
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                raw[n][ks][0] = *reinterpret_cast<const f32x4*>(src[n] + 128 * ks);
+                raw[n][ks][1] = *reinterpret_cast<const f32x4*>(src[n] + 128 * ks + 16);
+            }
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                f16x8 hv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hv[e] = (_Float16)raw[n][ks][0][e];
+                    hv[4 + e] = (_Float16)raw[n][ks][1][e];
+                }
+                qv[n][ks] = valid[n] ? hv : f16x8{};
+            }
+    }
+}
 
 template <int NT, int MODE, bool MASKED>
 __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u32x4* kslot, uint32_t vlane,
@@ -810,8 +905,8 @@ __device__ __forceinline__ void write_partial_wide(float* slot, int rows_slot, i
 }
 
 // One piece of the 32-cell kernel: steps [tb, te) of segment (s, g).
-template <int NTW, int MODE>
-__device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW>& sh, int causal, const Piece& pc) {
+template <int NTW, int RS, int MODE>
+__device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, RS>& sh, int causal, const Piece& pc) {
     constexpr int TL = WideShape::lanes;
     constexpr int NS = WideShape::slots;
     constexpr int SLOT16 = kWideSlot / 16;
@@ -823,41 +918,14 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW>&
     const int r = lane & 15;
     const int c = lane >> 4;
     const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
-    const StreamDims sd = stream_dims(a, s);
+    const StreamDims sd = table_dims(sh.st, s);
     const int G = a.G;
     const int R = G * sd.ql;
     const int n0 = rg * NTW;
 
     // ---- Q^T operands in registers: row 16(n0+n) + r, dims 32ks + 8c .. +7 ----
     f16x8 qv[NTW][4];
-#pragma unroll
-    for (int n = 0; n < NTW; ++n) {
-        const int row = 16 * (n0 + n) + r;
-        const bool valid = row < R;
-        const int j = valid ? row / G : 0;
-        const int h = g * G + (valid ? row % G : 0);
-        const char* src = a.q + (int64_t)j * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3 +
-                          (int64_t)(8 * c) * a.q_es;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            f16x8 hv = {};
-            if (valid) {
-                const char* p = src + (int64_t)(32 * ks) * a.q_es;
-                if (a.q_f16) {
-                    hv = as_f16x8(ld16(p));
-                } else {
-                    const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
-                    const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 16);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        hv[e] = (_Float16)lo[e];
-                        hv[4 + e] = (_Float16)hi[e];
-                    }
-                }
-            }
-            qv[n][ks] = hv;
-        }
-    }
+    load_q_operands<NTW>(a, s, g, R, n0, lane, qv);
 
     RowInfo<NTW> ri;
 #pragma unroll
@@ -914,7 +982,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW>&
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) o8[h * 4 + ks] = (c0 + 16 * h) * knb + koff + ks * 64;
             dma16x8_to_lds(krs, o8, base);
-        } else {
+        } else if (rg == 1) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) o8[u] = (c0 + 4 * u) * vnb + voff[u & 1];
             dma16x8_to_lds(vrs, o8, base + 8192);
@@ -928,7 +996,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW>&
         if (k < n_my) issue(k, k);
 #pragma unroll 1
     for (int i = 0; i < n_iter; ++i) {
-        const int ahead = n_my - 1 - i;  // own steps issued after step i
+        const int ahead = n_my - 1 - i;  // own steps issued after step i (row groups 0 and 1)
         if (NS >= 4 && ahead >= 2) wait_vmcnt<16>();
         else if (NS >= 3 && ahead >= 1) wait_vmcnt<8>();
         else wait_vmcnt<0>();
@@ -958,12 +1026,13 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW>&
         if (tb == 0 && te == pc.nt_seg)
             write_rows_wide(a, acc, n0, s, g, R, lane);
         else
-            write_partial_wide(a.part + pc.slot * a.slot_floats, NTW * 2 * 16, n0, R, acc, lane);
+            write_partial_wide(a.part + pc.slot * a.slot_floats, NTW * RS * 16, n0, R, acc, lane);
     }
     __syncthreads();  // LDS (merge buffers, rings) is reused by the next piece
 }
 
-// Work-group -> tile range.  Returns false for a work-group without tiles.
+// Work-group -> range of the cost line (segments laid end to end, each seg_cost units of
+// start-up followed by its tiles).  Returns false for a work-group without a range.
 struct Partition {
     int64_t T, P, x0, x1;
     int p_log;
@@ -971,7 +1040,7 @@ struct Partition {
 
 __device__ __forceinline__ bool partition(const FaArgs& a, const int* ps, int b, Partition& pt) {
     pt.T = (int64_t)a.Hkv * ps[a.S];
-    pt.P = pt.T < a.P ? pt.T : a.P;  // active work-groups: every one owns >= 1 tile
+    pt.P = pt.T < a.P ? pt.T : a.P;  // active work-groups: every one owns >= 1 unit
     // logical index: with the remap, consecutive tile ranges land on one XCD (work-groups
     // are dealt round-robin over the XCDs)
     pt.p_log = a.xcd_remap ? (b % kXcds) * (a.P / kXcds) + b / kXcds : b;
@@ -988,7 +1057,7 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
     if (!partition(a, ps, blockIdx.x, pt)) return;
     const int64_t Hkv = a.Hkv;
 
-    // stream holding tile x0: the largest s with Hkv*ps[s] <= x0
+    // stream holding unit x0: the largest s with Hkv*ps[s] <= x0
     int lo = 0, hi = a.S;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -998,19 +1067,24 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
     int64_t x = pt.x0;
     while (x < pt.x1) {
         while (Hkv * ps[s + 1] <= x) ++s;
-        const int nt = ps[s + 1] - ps[s];
+        const int ct = ps[s + 1] - ps[s];  // segment cost: seg_cost + tiles
         const int64_t cs = Hkv * ps[s];
-        const int g = (int)((x - cs) / nt);
-        const int64_t ck = cs + (int64_t)g * nt;
-        Piece pc;
-        pc.s = s;
-        pc.g = g;
-        pc.tb = (int)(x - ck);
-        pc.te = (int)(min(pt.x1, ck + nt) - ck);
-        pc.nt_seg = nt;
-        pc.slot = (int64_t)s * Hkv + g + pt.p_log;
-        fn(pc);
-        x = ck + pc.te;
+        const int g = (int)((x - cs) / ct);
+        const int64_t ck = cs + (int64_t)g * ct;
+        const int64_t t0 = ck + a.seg_cost;  // unit of the segment's first tile
+        const int64_t xb = x > t0 ? x : t0;
+        const int64_t xe = pt.x1 < ck + ct ? pt.x1 : ck + ct;
+        if (xb < xe) {
+            Piece pc;
+            pc.s = s;
+            pc.g = g;
+            pc.tb = (int)(xb - t0);
+            pc.te = (int)(xe - t0);
+            pc.nt_seg = ct - a.seg_cost;
+            pc.slot = (int64_t)s * Hkv + g + pt.p_log;
+            fn(pc);
+        }
+        x = ck + ct;
     }
 }
 
@@ -1023,13 +1097,13 @@ __global__ __launch_bounds__((Shape<RS, KV>::waves * 64), (Shape<RS, KV>::groups
     for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, RS, KV, MODE>(a, sh, causal, pc); });
 }
 
-template <int NTW, int MODE>
-__global__ __launch_bounds__((WideShape::waves * 64), (WideShape::waves * WideShape::groups_per_cu / 4)) void
+template <int NTW, int RS, int MODE>
+__global__ __launch_bounds__((RS * WideShape::lanes * 64), (RS * WideShape::lanes * WideShape::groups_per_cu / 4)) void
 decode_wide_d128(FaArgs a, int causal) {
-    __shared__ WideLds<NTW> sh;
-    if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
+    __shared__ WideLds<NTW, RS> sh;
+    if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
-    for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece_wide<NTW, MODE>(a, sh, causal, pc); });
+    for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE>(a, sh, causal, pc); });
 }
 
 // Combines the pieces of every segment that more than one work-group touched, in the order
@@ -1042,13 +1116,15 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     const int64_t k = blockIdx.x;
     const int s = (int)(k / a.Hkv);
     const int g = (int)(k % a.Hkv);
-    const int nt = ps[s + 1] - ps[s];
-    if (nt == 0) return;
+    const int ct = ps[s + 1] - ps[s];
+    if (ct == 0) return;
     const int64_t T = (int64_t)a.Hkv * ps[a.S];
     const int64_t P = T < a.P ? T : a.P;
-    const int64_t ck = (int64_t)a.Hkv * ps[s] + (int64_t)g * nt;
-    const int64_t p_first = ((ck + 1) * P - 1) / T;
-    const int64_t p_last = ((ck + nt) * P - 1) / T;
+    const int64_t ck = (int64_t)a.Hkv * ps[s] + (int64_t)g * ct;
+    // work-groups holding the segment's first and last tile (unit x lies in group
+    // floor(((x+1)P - 1) / T))
+    const int64_t p_first = ((ck + a.seg_cost + 1) * P - 1) / T;
+    const int64_t p_last = ((ck + ct) * P - 1) / T;
     if (p_first == p_last) return;  // written whole by its only work-group
 
     const StreamDims sd = stream_dims(a, s);
@@ -1080,16 +1156,16 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
 }
 
-template <int NTW>
+template <int NTW, int RS>
 hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
-    const dim3 grid(a.P), block(WideShape::waves * 64);
+    const dim3 grid(a.P), block(RS * WideShape::lanes * 64);
     if (generic)
-        hipLaunchKernelGGL((decode_wide_d128<NTW, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_wide_d128<NTW, RS, MODE_GENERIC>), grid, block, 0, stream, a, causal);
     else
-        hipLaunchKernelGGL((decode_wide_d128<NTW, MODE_FAST>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_wide_d128<NTW, RS, MODE_FAST>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int rows_slot = NTW * 2 * 16;
+    const int rows_slot = NTW * RS * 16;
     hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
                        a, rows_slot);
     return hipGetLastError();
@@ -1113,7 +1189,7 @@ hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stre
 }  // namespace
 
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
-    const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + a.tile_cells - 1) / a.tile_cells);
+    const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + a.tile_cells - 1) / a.tile_cells + a.seg_cost);
     const int per_cu = row_tiles <= 3 ? Shape<1, SIXI_TYPE_F16>::groups_per_cu : WideShape::groups_per_cu;
     int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
     if (P > kMaxSplitGroups) P = kMaxSplitGroups;
@@ -1135,8 +1211,8 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
             case 1: return launch_nt<1, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
             case 2: return launch_nt<2, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
             case 3: return launch_nt<3, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 4: return launch_wide<2>(a, generic, causal, stream);
-            case 6: return launch_wide<3>(a, generic, causal, stream);
+            case 4: return launch_wide<kWide64.ntw, kWide64.rs>(a, generic, causal, stream);
+            case 6: return launch_wide<kWide96.ntw, kWide96.rs>(a, generic, causal, stream);
             default: return hipErrorNotSupported;
         }
     }

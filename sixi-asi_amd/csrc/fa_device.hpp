@@ -231,17 +231,26 @@ struct StreamDims {
     int nc;     // cells scanned: kl + ql (0 when the stream has no rows)
 };
 
-__device__ __forceinline__ StreamDims stream_dims(const FaArgs& a, int s) {
+__device__ __forceinline__ StreamDims stream_dims_from(const FaArgs& a, int q_raw, int kv_raw) {
     StreamDims d;
-    d.ql = a.q_len ? min(max(a.q_len[s], 0), a.n_q) : a.n_q;
+    d.ql = a.q_len ? min(max(q_raw, 0), a.n_q) : a.n_q;
     if (a.kv_len) {
-        d.kl = min(max(a.kv_len[s], 0), a.n_kv - d.ql);
+        d.kl = min(max(kv_raw, 0), a.n_kv - d.ql);
         d.nc = d.ql > 0 ? d.kl + d.ql : 0;
     } else {
         d.kl = a.n_kv - d.ql;
         d.nc = d.ql > 0 ? a.n_kv : 0;
     }
     return d;
+}
+// Both length loads go through buffer resources that are empty when an array is absent
+// (such a load returns 0 and touches no memory), so they issue together, without a branch.
+__device__ __forceinline__ StreamDims stream_dims(const FaArgs& a, int s) {
+    const buf_rsrc qr = make_rsrc(a.q_len, a.q_len ? (uint32_t)a.S * 4u : 0u);
+    const buf_rsrc kr = make_rsrc(a.kv_len, a.kv_len ? (uint32_t)a.S * 4u : 0u);
+    const int q_raw = (int)buf_ld4(qr, (uint32_t)s * 4u);
+    const int kv_raw = (int)buf_ld4(kr, (uint32_t)s * 4u);
+    return stream_dims_from(a, q_raw, kv_raw);
 }
 
 // ALiBi slope of q-head h (ggml's rule); 1 when ALiBi is off.

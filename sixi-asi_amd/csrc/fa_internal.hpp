@@ -44,6 +44,7 @@ struct FaArgs {
     int32_t P;             // work-groups of the split-K launch
     int32_t xcd_remap;     // 1: consecutive tile ranges go to work-groups of one XCD
     int32_t tile_cells;    // KV cells per split tile (decode_tile_cells)
+    int32_t seg_cost;      // tiles' worth of work charged to each segment in the split
     int64_t slot_floats;   // floats per partial slot
 };
 
@@ -64,6 +65,13 @@ int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles);
 // Cells per split tile of the decode launch for this KV type and row-tile count.
 inline int decode_tile_cells(int kv_type, int row_tiles) {
     return (kv_type == SIXI_TYPE_F16 && row_tiles > 3) ? kDecodeTileWide : kDecodeTile;
+}
+// Fixed cost of starting a piece (loading Q, filling the ring, merging and writing the
+// rows), in tiles of the split: each segment weighs tiles + seg_cost, so a work-group whose
+// range enters a segment gets that many tiles less.
+constexpr int kWideSegCost = 12;
+inline int decode_seg_cost(int kv_type, int row_tiles) {
+    return (kv_type == SIXI_TYPE_F16 && row_tiles > 3) ? kWideSegCost : 0;
 }
 // Row tiles the decode kernel runs for `rows` = G * n_q rows: up to 3 per wave; beyond
 // that two row groups of equal size (so 5 tiles run as 6).

@@ -233,6 +233,7 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     hipError_t e;
     if (pl.splitk) {
         a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles);
+        a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles);
         a.P = sixi::decode_num_groups(a, cu_count_cached(), pl.row_tiles);
         a.xcd_remap = 0;
         e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D, pl.row_tiles, stream);
