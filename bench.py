@@ -3,8 +3,9 @@
 Headline workload: batched speculative verify -- 32 streams x 16 drafted rows, block-causal,
 per-stream cached lengths drawn from [512, 16384], 24 q-heads / 4 kv-heads x 128, f16 KV in
 per-stream 256-cell pages, f32 Q -- one attention layer per step.  A step is one call of
-the C ABI (sixi_attn_forward), i.e. the split-K kernel plus its merge kernel, timed with
-HIP events on the stream the library launches on, inputs resident in HBM.
+the C ABI (sixi_attn_forward), i.e. the split-K kernel (decode_wide_d128, 32-cell steps)
+plus its merge kernel, timed with HIP events on the stream the library launches on, inputs
+resident in HBM.
 
 Prints one JSON line: value = algorithmic HBM GB/s of the verify call (K/V of every attended
 cell + Q + O, counted once); roofline = that rate against the 8 TB/s HBM peak; the other
@@ -14,7 +15,8 @@ restatement of ggml's CPU flash_attn_ext, f16 V accumulator as upstream) on the 
 same inputs.
 
 `--workload copy` instead times a plain 1 GiB device copy: the calibration run for the HBM
-byte counters (FETCH_SIZE / WRITE_SIZE) used in the traffic figures.
+byte counters (FETCH_SIZE / WRITE_SIZE) used in the traffic figures.  `--workload prefill`
+times only the chunked causal prefill (two 2048-row chunks), for profiling that kernel.
 """
 from __future__ import annotations
 
@@ -140,12 +142,38 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
+def time_prefill(fa, steps: int, warmup: int):
+    """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks)."""
+    from sixi_attn import workloads as wl
+
+    pre = []
+    for name in ("prefill_chunk0", "prefill_chunk1"):
+        wp = wl.config(name)
+        dp = wl.to_device(wl.make_host(wp))
+        msp, _ = time_calls(fa, wp, dp, steps, warmup)
+        pre.append((wp, msp))
+        del dp
+    flops = sum(wp.flops() for wp, _ in pre)
+    t = sum(msp for _, msp in pre)
+    return flops / (t * 1e-3) / 1e12, t * 1e3
+
+
+def prefill_only(steps: int, warmup: int) -> int:
+    import sixi_attn as sa
+
+    fa = sa.FlashAttnExt()
+    tf, us = time_prefill(fa, max(1, steps), warmup)
+    print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks", "us_two_chunks": round(us, 2),
+                      "TFLOPs": round(tf, 2)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "copy"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -160,6 +188,8 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.workload == "copy":
         return copy_calibration(max(1, args.steps))
+    if args.workload == "prefill":
+        return prefill_only(args.steps, args.warmup)
 
     import sixi_attn as sa
     from sixi_attn import workloads as wl
@@ -203,7 +233,8 @@ def main() -> int:
         "verify_tflops": head["TFLOPs"],
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_f16_d128<3,2,0> + decode_merge (one sixi_attn_forward call)",
+            "kernel": "decode_wide_d128<3,2,0> + decode_merge (one sixi_attn_forward call; "
+                      "achieved = algorithmic bytes / call time)",
             "achieved": gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -229,21 +260,12 @@ def main() -> int:
 
         # chunked causal prefill (2 chunks of 2048 rows on a 2048-cell cache)
         try:
-            pre = []
-            for name in ("prefill_chunk0", "prefill_chunk1"):
-                wp = wl.config(name)
-                hp = wl.make_host(wp)
-                dp = wl.to_device(hp)
-                msp, _ = time_calls(fa, wp, dp, max(10, args.steps // 4), max(3, args.warmup // 4))
-                pre.append((wp, msp))
-            flops = sum(wp.flops() for wp, _ in pre)
-            t = sum(msp for _, msp in pre)
-            tf = flops / (t * 1e-3) / 1e12
+            tf, us = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4))
             result["prefill_tflops"] = round(tf, 2)
-            result["prefill_us_two_chunks"] = round(t * 1e3, 2)
+            result["prefill_us_two_chunks"] = round(us, 2)
             result["prefill_roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": F16_PEAK_TFLOPS,
                                           "unit": "TFLOP/s", "frac": round(tf / F16_PEAK_TFLOPS, 4)}
-            _log(f"prefill: {t * 1e3:.1f} us for 2 chunks, {tf:.1f} TFLOP/s")
+            _log(f"prefill: {us:.1f} us for 2 chunks, {tf:.1f} TFLOP/s")
         except sa.SixiAttnError as e:
             result["prefill_tflops"] = None
             result["prefill_note"] = f"prefill kernel unavailable: {e}"

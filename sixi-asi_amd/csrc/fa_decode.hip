@@ -1,29 +1,27 @@
 // fa_decode.hip -- split-K flash-decoding for single-token decode and speculative verify
-// on gfx950 (head_dim 128, f16 KV).
+// on gfx950 (head_dim 128, f16 or q8_0 KV, up to 96 rows per GQA group).
 //
-// Work decomposition.  A segment is one (stream s, kv-head g): nt_s = ceil(cells_s / 16)
-// tiles of 16 KV cells, and all R = G*q_len_s query rows of the GQA group ride along with
-// every tile, so each K/V byte leaves HBM once for the whole group.  Segments are laid end
-// to end (stream-major, then kv-head) and the P work-groups take equal shares
-// [p*T/P, (p+1)*T/P) of the T tiles ("stream-K"), so any mix of lengths balances over the
-// CUs.  The share of work-group p inside a segment is a piece.  A work-group that owns a
-// whole segment writes the rows directly; every other piece leaves (m, l, O) in a
-// workspace slot, and a second launch (decode_merge) combines the pieces of each split
-// segment in a fixed order.  The kernel boundary orders the two launches, so neither
-// needs device-scope fences or atomics.
+// Work decomposition.  A segment is one (stream s, kv-head g): nt_s tiles of KV cells, and
+// all R = G*q_len_s query rows of the GQA group ride along with every tile, so each K/V
+// byte leaves HBM once for the whole group.  Segments are laid end to end (stream-major,
+// then kv-head) on a cost line where each weighs seg_cost + nt_s units, and the P
+// work-groups take equal shares [p*T/P, (p+1)*T/P) of it ("stream-K"), so any mix of
+// lengths balances over the CUs and a work-group that has to start an extra segment gets
+// correspondingly fewer tiles.  The share of work-group p inside a segment is a piece.  A
+// work-group that owns a whole segment writes the rows directly; every other piece leaves
+// (m, l, O) in a workspace slot, and a second launch (decode_merge) combines the pieces of
+// each split segment in a fixed order.  The kernel boundary orders the two launches, so
+// neither needs device-scope fences or atomics.
 //
-// Every SIMD holds two waves (<= 256 registers each), so one wave's MFMA and memory stalls
-// hide behind the other's VALU work:
-//   RS = 1 (<= 48 rows): two work-groups of four waves per CU (<= 80 KB LDS each); the
-//          waves are independent tile lanes, each with a private two-slot LDS ring, so the
-//          tile loop has no barrier;
-//   RS = 2 (49..96 rows): two work-groups of four waves per CU, each = two tile lanes x two
-//          row groups; the two waves of a lane share a three-slot ring (each stages half of
-//          every tile, two tiles in flight) and the group meets at one barrier a tile.
-// K/V tiles reach LDS by direct global->LDS loads (buffer_load_dwordx4 ... lds), so bytes
-// in flight cost no VGPRs.
+// Two kernels share this split:
+//   decode_d128 (<= 48 rows, and q8_0 KV): tiles of 16 cells; two work-groups of four
+//     waves per CU, the waves independent tile lanes with private LDS rings (no barrier
+//     in the tile loop).  Described next.
+//   decode_wide_d128 (f16 KV, 49..96 rows): steps of 32 cells; described further down.
+// K/V reach LDS by direct global->LDS loads (buffer_load_dword{,x4} ... lds), so bytes in
+// flight cost no VGPRs.
 //
-// Per 16-cell tile and wave:
+// decode_d128, per 16-cell tile and wave:
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 cells x 32 dims straight from the ring
 //                 (lane (r, c) holds cell r, dims 32ks+8c..+7), B = Q^T from LDS;
 //                 lane (r, c) receives cells 4c..4c+3 of row r;
@@ -43,7 +41,7 @@
 // aligned dword reads and v_alignbyte_b32, and dequantises them in registers
 // (dequant_q8x8: one f16 rounding of q*d).  Q is quantised to q8_0 exactly as ggml's
 // flash_attn_ext does before the dot (per 32-dim block, d = amax/127) and enters the MFMA as
-// its dequantised f16 values.  (RS = 1 only: up to 48 rows per GQA group.)
+// its dequantised f16 values.
 #include <type_traits>
 
 #include "fa_device.hpp"
@@ -79,10 +77,10 @@ template <int KV> struct KvTile;
 template <> struct KvTile<SIXI_TYPE_F16> { static constexpr int slot_bytes = 8192, dma = 8; };
 template <> struct KvTile<SIXI_TYPE_Q8_0> { static constexpr int slot_bytes = 2 * kQ8Dma * 256, dma = 2 * kQ8Dma; };
 
-template <int RS, int KV> struct Shape;
-template <> struct Shape<1, SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 4, slots = 2, groups_per_cu = 2; };
-template <> struct Shape<2, SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 2, slots = 3, groups_per_cu = 2; };
-template <> struct Shape<1, SIXI_TYPE_Q8_0> { static constexpr int waves = 4, lanes = 4, slots = 3, groups_per_cu = 2; };
+// Four independent tile lanes (one wave each) per work-group, two work-groups per CU.
+template <int KV> struct Shape;
+template <> struct Shape<SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 4, slots = 2, groups_per_cu = 2; };
+template <> struct Shape<SIXI_TYPE_Q8_0> { static constexpr int waves = 4, lanes = 4, slots = 3, groups_per_cu = 2; };
 
 template <int NT, int NS>
 struct MergeBuf {
@@ -91,16 +89,16 @@ struct MergeBuf {
     float l[NS][NT * 64];
 };
 
-// NTW = row tiles per wave, RS = row groups (waves that share a tile).
-template <int NTW, int RS, int KV>
+// NTW = row tiles per wave.
+template <int NTW, int KV>
 struct DecodeLds {
-    using Sh = Shape<RS, KV>;
+    using Sh = Shape<KV>;
     union {
         struct {
             u32x4 ring[Sh::lanes * Sh::slots * KvTile<KV>::slot_bytes / 16];
-            u32x4 q[NTW * RS * 4 * 64];  // Q^T B operands: [row tile][ks][lane], 8 f16 each
+            u32x4 q[NTW * 4 * 64];  // Q^T B operands: [row tile][ks][lane], 8 f16 each
         } t;
-        MergeBuf<NTW, RS * Sh::lanes / 2> mg;  // reused after the tile loop
+        MergeBuf<NTW, Sh::lanes / 2> mg;  // reused after the tile loop
     };
     int ps[kMaxStreams + 1];  // (no extents table: it would not leave room for two groups per CU)
 };
@@ -422,20 +420,20 @@ struct Piece {
 };
 
 // One piece: tiles [tb, te) of segment (s, g).
-template <int NTW, int RS, int KV, int MODE>
-__device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS, KV>& sh, int causal, const Piece& pc) {
-    constexpr int NTOT = NTW * RS;
-    constexpr int TL = Shape<RS, KV>::lanes;   // tile lanes
-    constexpr int NSLOT = Shape<RS, KV>::slots;
-    constexpr int NTHREADS = Shape<RS, KV>::waves * 64;
+template <int NTW, int KV, int MODE>
+__device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>& sh, int causal, const Piece& pc) {
+    constexpr int NTOT = NTW;
+    constexpr int TL = Shape<KV>::lanes;   // tile lanes (one wave each)
+    constexpr int NSLOT = Shape<KV>::slots;
+    constexpr int NTHREADS = Shape<KV>::waves * 64;
     constexpr int SLOT16 = KvTile<KV>::slot_bytes / 16;
-    constexpr int DMA = KvTile<KV>::dma / RS;  // LDS-DMA loads per tile per wave
-    static_assert(KV == SIXI_TYPE_F16 || RS == 1, "q8_0 runs one row group");
+    constexpr int DMA = KvTile<KV>::dma;  // LDS-DMA loads per tile per wave
+    static_assert(Shape<KV>::waves == TL, "one row group");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
-    const int rg = w / TL;
-    const int tl = w % TL;
+    const int rg = 0;
+    const int tl = w;
     const int r = lane & 15;
     const int c = lane >> 4;
     const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
@@ -544,10 +542,9 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS,
                                      (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + rowb));
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
 
-    // tiles of this lane: tb + tl + TL*i, i < n_my; n_iter is the same for the whole group
+    // tiles of this lane: tb + tl + TL*i, i < n_my
     const int t0 = tb + tl;
     const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
-    const int n_iter = (te - tb + TL - 1) / TL;
     u32x4* ring = sh.t.ring + (size_t)tl * NSLOT * SLOT16;
     const uint32_t ring_base = lds_addr(ring);
 
@@ -564,26 +561,21 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS,
         }
     }
 
-    // Stage tile i of this lane into slot i % NSLOT.  RS = 1: all of it; RS = 2: row group
-    // 0 stages the 4 K chunks and row group 1 the 4 V chunks.
+    // Stage tile i of this lane into slot i % NSLOT.
     auto issue = [&](int i) {
         const uint32_t c0 = (uint32_t)(t0 + i * TL) * kTile;
         const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * KvTile<KV>::slot_bytes;
         if constexpr (KV == SIXI_TYPE_F16) {
-            if (RS == 1 || rg == 0) {
-                const uint32_t off = (c0 + r) * knb + c * 16;
-                uint32_t vo4[4];
+            const uint32_t off = (c0 + r) * knb + c * 16;
+            const uint32_t vo = (c0 + 4 * c) * vnb + r * 16;
+            uint32_t ko4[4], vo4[4];
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) vo4[ks] = off + ks * 64;
-                dma16x4_to_lds(krs, vo4, base);
+            for (int e = 0; e < 4; ++e) {
+                ko4[e] = off + e * 64;
+                vo4[e] = vo + e * vnb;
             }
-            if (RS == 1 || rg == 1) {
-                const uint32_t vo = (c0 + 4 * c) * vnb + r * 16;
-                uint32_t vo4[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) vo4[e] = vo + e * vnb;
-                dma16x4_to_lds(vrs, vo4, base + 4 * 1024);
-            }
+            dma16x4_to_lds(krs, ko4, base);
+            dma16x4_to_lds(vrs, vo4, base + 4 * 1024);
         } else {
             static_assert(kQ8Dma == 9, "dword LDS-DMA batch of nine loads");
             uint32_t ko[kQ8Dma], vo[kQ8Dma];
@@ -605,40 +597,21 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, RS,
             tile_step<NTW, KV, MODE, true>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
     };
 
-    if constexpr (RS == 1) {
-        // private ring: the slot just read is refilled with tile i+NSLOT
-        static_assert(NSLOT == 2 || NSLOT == 3, "ring depth");
+    // private ring: the slot just read is refilled with tile i+NSLOT
+    static_assert(NSLOT == 2 || NSLOT == 3, "ring depth");
 #pragma unroll
-        for (int i = 0; i < NSLOT; ++i)
-            if (i < n_my) issue(i);
+    for (int i = 0; i < NSLOT; ++i)
+        if (i < n_my) issue(i);
 #pragma unroll 1
-        for (int i = 0; i < n_my; ++i) {
-            const int ahead = n_my - 1 - i;  // own tiles issued after tile i
-            if (NSLOT == 3 && ahead >= 2) wait_vmcnt<2 * DMA>();
-            else if (ahead >= 1) wait_vmcnt<DMA>();
-            else wait_vmcnt<0>();
-            step(i, [&] {
-                wait_lgkmcnt0();
-                if (i + NSLOT < n_my) issue(i + NSLOT);
-            });
-        }
-    } else {
-        // shared ring: tile i+NSLOT-1 goes into the slot of tile i-1, which both readers
-        // left before the barrier of iteration i
-        static_assert(NSLOT == 3 || NSLOT == 4, "ring depth");
-#pragma unroll
-        for (int i = 0; i < NSLOT - 1; ++i)
-            if (i < n_my) issue(i);
-#pragma unroll 1
-        for (int i = 0; i < n_iter; ++i) {
-            const int ahead = n_my - 1 - i;  // own tiles issued after tile i
-            if (NSLOT == 4 && ahead >= 2) wait_vmcnt<2 * DMA>();
-            else if (ahead >= 1) wait_vmcnt<DMA>();
-            else wait_vmcnt<0>();
-            __syncthreads();
-            if (i + NSLOT - 1 < n_my) issue(i + NSLOT - 1);
-            if (i < n_my) step(i, [] {});
-        }
+    for (int i = 0; i < n_my; ++i) {
+        const int ahead = n_my - 1 - i;  // own tiles issued after tile i
+        if (NSLOT == 3 && ahead >= 2) wait_vmcnt<2 * DMA>();
+        else if (ahead >= 1) wait_vmcnt<DMA>();
+        else wait_vmcnt<0>();
+        step(i, [&] {
+            wait_lgkmcnt0();
+            if (i + NSLOT < n_my) issue(i + NSLOT);
+        });
     }
 
     // row sums over the lane groups; FAST references to log2 units for merging
@@ -1088,13 +1061,13 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
     }
 }
 
-template <int NTW, int RS, int KV, int MODE>
-__global__ __launch_bounds__((Shape<RS, KV>::waves * 64), (Shape<RS, KV>::groups_per_cu)) void decode_d128(
-    FaArgs a, int causal) {
-    __shared__ DecodeLds<NTW, RS, KV> sh;
+template <int NTW, int KV, int MODE>
+__global__ __launch_bounds__((Shape<KV>::waves * 64), (Shape<KV>::waves * Shape<KV>::groups_per_cu / 4)) void
+decode_d128(FaArgs a, int causal) {
+    __shared__ DecodeLds<NTW, KV> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
     __syncthreads();
-    for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, RS, KV, MODE>(a, sh, causal, pc); });
+    for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, KV, MODE>(a, sh, causal, pc); });
 }
 
 template <int NTW, int RS, int MODE>
@@ -1171,16 +1144,16 @@ hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t st
     return hipGetLastError();
 }
 
-template <int NTW, int RS, int KV>
+template <int NTW, int KV>
 hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
-    const dim3 grid(a.P), block(Shape<RS, KV>::waves * 64);
+    const dim3 grid(a.P), block(Shape<KV>::waves * 64);
     if (generic)
-        hipLaunchKernelGGL((decode_d128<NTW, RS, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
     else
-        hipLaunchKernelGGL((decode_d128<NTW, RS, KV, MODE_FAST>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_FAST>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int rows_slot = NTW * RS * 16;
+    const int rows_slot = NTW * 16;
     hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
                        a, rows_slot);
     return hipGetLastError();
@@ -1190,7 +1163,7 @@ hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stre
 
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
     const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + a.tile_cells - 1) / a.tile_cells + a.seg_cost);
-    const int per_cu = row_tiles <= 3 ? Shape<1, SIXI_TYPE_F16>::groups_per_cu : WideShape::groups_per_cu;
+    const int per_cu = row_tiles <= 3 ? Shape<SIXI_TYPE_F16>::groups_per_cu : WideShape::groups_per_cu;
     int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
     if (P > kMaxSplitGroups) P = kMaxSplitGroups;
     if (P > tiles_max) P = tiles_max;
@@ -1208,9 +1181,9 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
     if (kv_type == SIXI_TYPE_F16) {
         switch (row_tiles) {
-            case 1: return launch_nt<1, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 2: return launch_nt<2, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 3: return launch_nt<3, 1, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 1: return launch_nt<1, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 2: return launch_nt<2, SIXI_TYPE_F16>(a, generic, causal, stream);
+            case 3: return launch_nt<3, SIXI_TYPE_F16>(a, generic, causal, stream);
             case 4: return launch_wide<kWide64.ntw, kWide64.rs>(a, generic, causal, stream);
             case 6: return launch_wide<kWide96.ntw, kWide96.rs>(a, generic, causal, stream);
             default: return hipErrorNotSupported;
@@ -1218,9 +1191,9 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
     }
     if (kv_type == SIXI_TYPE_Q8_0) {
         switch (row_tiles) {
-            case 1: return launch_nt<1, 1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
-            case 2: return launch_nt<2, 1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
-            case 3: return launch_nt<3, 1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
+            case 1: return launch_nt<1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
+            case 2: return launch_nt<2, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
+            case 3: return launch_nt<3, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
             default: return hipErrorNotSupported;
         }
     }
