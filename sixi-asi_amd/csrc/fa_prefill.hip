@@ -6,13 +6,15 @@
 // row block first (the last rows of a causal chunk see the most cells), so the long blocks
 // start first and the short ones fill in behind them.  Four waves own 32 rows each.
 //
-// Per 64-cell KV tile (double-buffered in LDS, one barrier per tile):
-//   K   [64 cells][16 chunks of 16 B], chunk q of cell c stored at slot q ^ (c & 15): filled by
-//       direct global->LDS loads (each lane fetches the global chunk that lands in its slot),
-//       read back conflict-free as MFMA A operands;
-//   V^T [128 dims][64 cells + pad], built once per work-group from registers: every thread
-//       loads two cells x 8 dims, pairs them with v_perm_b32 and writes 32-bit cell pairs,
-//       so each wave later reads its A operands as plain 16-byte rows.
+// Per 64-cell KV tile (double-buffered in LDS, one barrier per tile), both K and V arrive by
+// direct global->LDS loads issued one tile ahead:
+//   K   [64 cells][16 chunks of 16 B], chunk q of cell c stored at slot q ^ (c & 15) (each
+//       lane fetches the global chunk that lands in its slot), read back conflict-free as
+//       MFMA A operands;
+//   V   [64 cells][8 chunks of 32 B], chunk q of cell c stored at position q ^ (c & 7); the
+//       V^T A operands come out of it with ds_read_b64_tr_b16 (within each 16-lane group,
+//       lane i receives element i%4 of the 8 bytes addressed by lane 4e + i/4), so no
+//       transpose runs through registers.
 //   S^T = K Q^T on v_mfma_f32_32x32x16_f16: A = 32 cells x 16 dims from LDS, B = Q^T held in
 //       registers for the whole work-group (lane l: row l%32, dims 16ks + 8(l/32)..+7);
 //       lane l receives cells 8b + 4(l/32) + e (b, e < 4) of row l%32, so a row's 64 cells
@@ -20,8 +22,9 @@
 //   softmax: lazy exponent reference (moves only when the tile max exceeds it by 2^8),
 //       p = 2^(s*c - m*c) in one FMA.
 //   O^T += V^T P^T on v_mfma_f32_32x32x16_f16: for the 16-cell step kk the lane's eight
-//       values i = 8(kk%2) .. +7 of S^T block kk/2 are exactly its B operand; the V^T rows
-//       store each 16-cell group in the matching order (cells 4..7 and 8..11 swapped).
+//       values i = 8(kk%2) .. +7 of S^T block kk/2 are exactly its B operand, so the
+//       reduction index k = 8(l/32) + e stands for cell 8(e/4) + 4(l/32) + e%4 of the step;
+//       the transposed V reads follow the same order.
 // Only tiles that reach past the first row's causal boundary (or the stream's end) mask.
 #include <type_traits>
 
@@ -33,30 +36,21 @@ namespace {
 constexpr int kBM = 128;           // rows per work-group
 constexpr int kBN = 64;            // cells per KV tile
 constexpr int kThreads = 256;      // 4 waves x 32 rows
-constexpr int kVtStride = 72;      // f16 per V^T row (64 cells + 8 pad): 144 B, conflict-free reads
 constexpr int kKBytes = kBN * 256;              // 16 KB
-constexpr int kVtBytes = 128 * kVtStride * 2;   // 18 KB
+constexpr int kVBytes = kBN * 256;              // 16 KB
 constexpr float kLazyLog2 = 8.0f;
 
 enum { MODE_FAST = 0, MODE_GENERIC = 1 };
 
 struct PrefillLds {
     u32x4 k[2][kKBytes / 16];
-    uint32_t vt[2][kVtBytes / 4];
+    u32x4 v[2][kVBytes / 16];
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-// position of cell offset co (0..63) inside a V^T row: the middle quads of every 16-cell
-// group are swapped, so that the B-operand order of P^T is contiguous
-__device__ __forceinline__ int vt_pos(int co) {
-    const int q = (co >> 2) & 3;
-    const int qp = (q == 1) ? 2 : (q == 2 ? 1 : q);
-    return (co & ~15) | (qp << 2) | (co & 3);
 }
 
 template <int MODE>
@@ -90,24 +84,32 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     const int t_full = (MODE == MODE_GENERIC) ? 0 : vis_min / kBN;
 
     // ---- Q^T B operands in registers: lane l -> row j, dims 16ks + 8*hl .. +7 ----
+    // (every load issued before any is used; rows past the block read its first row)
     f16x8 qop[8];
     {
-        const char* src = a.q + (int64_t)j * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3;
+        const char* src = a.q + (int64_t)(row_ok ? j : j0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3;
+        if (a.q_f16) {
+            u32x4 raw[8];
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const int d0 = 16 * ks + 8 * hl;
-            if (!row_ok) {
-                qop[ks] = as_f16x8(u32x4{0u, 0u, 0u, 0u});
-            } else if (a.q_f16) {
-                qop[ks] = as_f16x8(ld16(src + d0 * 2));
-            } else {
-                const f32x4 lo = *reinterpret_cast<const f32x4*>(src + d0 * 4);
-                const f32x4 hi = *reinterpret_cast<const f32x4*>(src + d0 * 4 + 16);
+            for (int ks = 0; ks < 8; ++ks) raw[ks] = ld16(src + (16 * ks + 8 * hl) * 2);
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) qop[ks] = row_ok ? as_f16x8(raw[ks]) : f16x8{};
+        } else {
+            f32x4 lo[8], hi[8];
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                lo[ks] = *reinterpret_cast<const f32x4*>(src + (16 * ks + 8 * hl) * 4);
+                hi[ks] = *reinterpret_cast<const f32x4*>(src + (16 * ks + 8 * hl) * 4 + 16);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                f16x8 hv;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    qop[ks][e] = (_Float16)lo[e];
-                    qop[ks][4 + e] = (_Float16)hi[e];
+                    hv[e] = (_Float16)lo[ks][e];
+                    hv[4 + e] = (_Float16)hi[ks][e];
                 }
+                qop[ks] = row_ok ? hv : f16x8{};
             }
         }
     }
@@ -124,13 +126,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     // ---- per-lane LDS byte offsets, fixed for the whole loop ----
     char* lds = reinterpret_cast<char*>(&sh);
     const uint32_t lds0 = lds_addr(&sh);
-    constexpr int kVtBase = 2 * kKBytes;  // V^T buffers follow the two K buffers
+    constexpr int kVBase = 2 * kKBytes;  // the V buffers follow the two K buffers
     // K A operand of (cb, ks): cell 32cb + rl, chunk (2ks + hl) stored at slot chunk ^ (rl & 15)
     uint32_t koff[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) koff[ks] = rl * 256 + ((((2 * ks + hl) ^ (rl & 15)) & 15) << 4);
-    // V^T A operand of (db, kk): row 32db + rl, positions 16kk + 8hl .. +7
-    const uint32_t vrd = rl * (kVtStride * 2) + 16 * hl;
     // K staging: wave w's load u4 fills cells 4(4w + u4) + l/16; lane fetches chunk (l%16)^cell
     uint32_t kdo[4];
 #pragma unroll
@@ -138,43 +138,36 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         const int cell = 4 * (4 * w + u4) + (lane >> 4);
         kdo[u4] = (uint32_t)cell * knb + (uint32_t)(((lane & 15) ^ (cell & 15)) * 16);
     }
-    // V staging: item k = tid + 256k -> cell pair 2*(it%32), dim chunk it/32
-    uint32_t vdo[2], vst[2];
+    // V staging: wave w's load u4 fills LDS rows 4u + t/16 (u = 4w + u4) at 16-byte position
+    // t%16, i.e. 32-byte chunk position (t%16)/2 of the row, which holds dims
+    // 16 * (position ^ (row % 8)); row % 8 = 4(u % 2) + t/16
+    uint32_t vdo[4];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int it = tid + 256 * k;
-        const int c = 2 * (it & 31);
-        const int q = it >> 5;
-        vdo[k] = (uint32_t)c * vnb + (uint32_t)q * 16;
-        vst[k] = (uint32_t)(8 * q) * (kVtStride * 2) + (uint32_t)vt_pos(c) * 2;
+    for (int u4 = 0; u4 < 4; ++u4) {
+        const int u = 4 * w + u4;
+        vdo[u4] = (uint32_t)(4 * u + (lane >> 4)) * vnb +
+                  32u * (((lane & 15) >> 1) ^ (4 * (u & 1) + (lane >> 4))) + 16u * (lane & 1);
+    }
+    // V^T A operand of (db, kk), half h: lane (G = l/16, q = l%16) addresses cell
+    // 16kk + 8h + 4(G/2) + q/4, dims 32db + 16(G%2) + 4(q%4) .. +3, which sits in chunk
+    // position (2db + G%2) ^ (4(G/2) + q/4).  The row offset has bits 5..7 clear, so the
+    // address is (row + 32*((G%2) ^ (4(G/2) + q/4)) + 8(q%4)) ^ 64db + (16kk + 8h)*256.
+    uint32_t vtr[4];
+    {
+        const int G = lane >> 4, q = lane & 15;
+        const int x = 4 * (G >> 1) + (q >> 2);
+        const uint32_t base = (uint32_t)x * 256u + 32u * (uint32_t)((G & 1) ^ x) + 8u * (uint32_t)(q & 3);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) vtr[db] = lds0 + kVBase + (base ^ (64u * db));
     }
 
-    auto issue_k = [&](int t, int buf) {
-        const int64_t o = (int64_t)t * kBN * knb;
-        const buf_rsrc rs = make_rsrc(kbase + o, (uint32_t)(kbytes > o ? kbytes - o : 0));
-        dma16x4_to_lds(rs, kdo, lds0 + buf * kKBytes + 4 * w * 1024);
-    };
-    u32x4 vreg[2][2];
-    auto load_v = [&](int t) {
-        const int64_t o = (int64_t)t * kBN * vnb;
-        const buf_rsrc rs = make_rsrc(vbase + o, (uint32_t)(vbytes > o ? vbytes - o : 0));
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            vreg[k][0] = buf_ld16(rs, vdo[k]);
-            vreg[k][1] = buf_ld16(rs, vdo[k] + vnb);
-        }
-    };
-    auto store_vt = [&](int buf) {
-        char* vt = lds + kVtBase + buf * kVtBytes;
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-#pragma unroll
-            for (int t8 = 0; t8 < 8; ++t8) {
-                const int d2 = t8 >> 1;
-                const uint32_t sel = (t8 & 1) ? 0x07060302u : 0x05040100u;
-                *reinterpret_cast<uint32_t*>(vt + vst[k] + t8 * (kVtStride * 2)) =
-                    __builtin_amdgcn_perm(vreg[k][1][d2], vreg[k][0][d2], sel);
-            }
+    auto issue_kv = [&](int t, int buf) {
+        const int64_t ko = (int64_t)t * kBN * knb;
+        const buf_rsrc krs = make_rsrc(kbase + ko, (uint32_t)(kbytes > ko ? kbytes - ko : 0));
+        dma16x4_to_lds(krs, kdo, lds0 + buf * kKBytes + 4 * w * 1024);
+        const int64_t vo = (int64_t)t * kBN * vnb;
+        const buf_rsrc vrs = make_rsrc(vbase + vo, (uint32_t)(vbytes > vo ? vbytes - vo : 0));
+        dma16x4_to_lds(vrs, vdo, lds0 + kVBase + buf * kVBytes + 4 * w * 1024);
     };
 
     f32x16 acc[4];  // O^T blocks: dims 32db + 8(i/4) + 4hl + i%4 of row j
@@ -197,7 +190,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         constexpr int buf = decltype(BUF)::value;
         constexpr bool masked = decltype(MASKED)::value;
         const bool more = t + 1 < n_tiles;
-        if (more) issue_k(t + 1, buf ^ 1);
+        if (more) issue_kv(t + 1, buf ^ 1);
         const int c0 = t * kBN;
         const char* kt = lds + buf * kKBytes;
 
@@ -211,9 +204,6 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
                 st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 8192 + koff[ks])), qop[ks],
                                       st[cb]);
         }
-
-        // V of tile t+1 into registers while the scores are formed (stored as V^T below)
-        if (more) load_v(t + 1);
 
         // ---- scores, row max (lanes l and l^32 hold the row's 64 cells) ----
         float mx = neg_inf();
@@ -292,13 +282,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
                 }
         }
 
-        // ---- O^T += V^T P^T ----
-        const char* vt = lds + kVtBase + buf * kVtBytes + vrd;
+        // ---- O^T += V^T P^T, V^T by transposed reads of the V rows ----
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                u32x4 vop = *reinterpret_cast<const u32x4*>(vt + db * 32 * (kVtStride * 2) + kk * 32);
+                const lds_char* vp = lds_ptr(vtr[db] + buf * kVBytes + kk * 16 * 256);
+                const u32x2 lo = ld_tr16(vp);
+                const u32x2 hi = ld_tr16(vp + 8 * 256);
+                u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
                 if (MODE == MODE_GENERIC && a.mask) {
 #pragma unroll
                     for (int m2 = 0; m2 < 4; ++m2) vop[m2] &= keep[kk][m2];
@@ -307,10 +299,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
             }
         }
 
-        if (more) {
-            store_vt(buf ^ 1);  // the compiler waits for the V loads
-            wait_vmcnt<0>();    // and the K loads of tile t+1 are in LDS
-        }
+        if (more) wait_vmcnt<0>();  // this wave's share of tile t+1 is in LDS
         __syncthreads();
     };
     auto run_tile = [&](int t, auto BUF) {
@@ -322,10 +311,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
 
     // prologue: tile 0 into buffer 0
     if (n_tiles > 0) {
-        load_v(0);
-        issue_k(0, 0);
-        wait_vmcnt<4>();  // the V loads (issued first) are back; the K loads may still run
-        store_vt(0);
+        issue_kv(0, 0);
         wait_vmcnt<0>();
     }
     __syncthreads();
