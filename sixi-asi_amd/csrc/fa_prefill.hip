@@ -48,6 +48,7 @@ struct PrefillLds {
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -255,15 +256,23 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
 
         // ---- probabilities ----
         const float mc = (m_ref == neg_inf()) ? 0.0f : ((MODE == MODE_FAST) ? m_ref * c2 : m_ref);
-        f16x8 pb[4];  // B operands of the four 16-cell steps
+        // B operands of the four 16-cell steps (f16 pairs by packed RNE conversion) and the
+        // row sum of exactly those f16 probabilities, two per v_dot2_f32_f16
+        f16x8 pb[4];
         float part[4] = {0.f, 0.f, 0.f, 0.f};
+        const f16x2 one2 = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float p = fast_exp2((MODE == MODE_FAST) ? fmaf(st[cb][i], c2, -mc) : st[cb][i] - mc);
-                part[i & 3] += p;
-                pb[2 * cb + (i >> 3)][i & 7] = (_Float16)p;
+            for (int i = 0; i < 16; i += 2) {
+                f32x2 pp;
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    pp[e] = fast_exp2((MODE == MODE_FAST) ? fmaf(st[cb][i + e], c2, -mc) : st[cb][i + e] - mc);
+                const f16x2 ph = __builtin_convertvector(pp, f16x2);
+                pb[2 * cb + (i >> 3)][i & 7] = ph[0];
+                pb[2 * cb + (i >> 3)][(i & 7) + 1] = ph[1];
+                part[(i >> 1) & 3] = __builtin_amdgcn_fdot2(ph, one2, part[(i >> 1) & 3], false);
             }
         l_sum += (part[0] + part[1]) + (part[2] + part[3]);
 
@@ -316,8 +325,17 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     }
     __syncthreads();
 
+    // the unmasked tiles in pairs (buffers 0, 1), then the tail with the masked tiles, so
+    // each loop holds one copy of the tile body per buffer
+    const int t_fast = (MODE == MODE_FAST) ? min(t_full, n_tiles) : 0;
+    int t = 0;
 #pragma unroll 1
-    for (int t = 0; t < n_tiles; t += 2) {
+    for (; t + 2 <= t_fast; t += 2) {
+        tile(t, std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
+        tile(t + 1, std::integral_constant<int, 1>{}, std::integral_constant<bool, false>{});
+    }
+#pragma unroll 1
+    for (; t < n_tiles; t += 2) {
         run_tile(t, std::integral_constant<int, 0>{});
         if (t + 1 < n_tiles) run_tile(t + 1, std::integral_constant<int, 1>{});
     }
