@@ -41,7 +41,7 @@ struct FaArgs {
 
     // split-K bookkeeping (workspace)
     float* part;           // partial slots of slot_floats floats: O rows [rows][128], then m, l
-    int32_t P;             // work-groups of the split-K launch
+    int32_t P;             // work-groups of the split-K launch (prefill: CUs of the device)
     int32_t xcd_remap;     // 1: consecutive tile ranges go to work-groups of one XCD
     int32_t tile_cells;    // KV cells per split tile (decode_tile_cells)
     int32_t seg_cost;      // tiles' worth of work charged to each segment in the split

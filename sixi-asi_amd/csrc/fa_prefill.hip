@@ -55,7 +55,7 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
 }
 
 template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int causal, int nrb) {
+__global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int causal, int nrb, int n_cu) {
     __shared__ PrefillLds sh;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -63,12 +63,24 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     const int hl = lane >> 5;      // lane half
     const int rl = lane & 31;      // row inside the wave / M index inside an MFMA block
 
-    // heaviest row block first
+    // Work-group order.  (row block, head) items are ranked heaviest first (the last rows of
+    // a causal chunk see the most cells).  The first n_cu work-groups take a CU each and the
+    // next ones (up to n_cu more) join the earliest of them, where both run slower than a
+    // work-group alone on its CU; so the heaviest ranks go to the positions that keep a CU to
+    // themselves, the next ranks to the positions that will be joined, the lightest last.
     const int SH = a.S * a.H;
     const int b = blockIdx.x;
-    const int rb = nrb - 1 - b / SH;
-    const int s = (b % SH) / a.H;
-    const int h = (b % SH) % a.H;
+    const int N = gridDim.x;
+    int rank = b;
+    if (N > n_cu && N <= 2 * n_cu) {
+        const int npair = N - n_cu;
+        const int alone = n_cu - npair;
+        if (b < npair) rank = alone + b;
+        else if (b < n_cu) rank = b - npair;
+    }
+    const int rb = nrb - 1 - rank / SH;
+    const int s = (rank % SH) / a.H;
+    const int h = (rank % SH) % a.H;
     const int g = h / a.G;
     const StreamDims sd = stream_dims(a, s);
     const int j0 = rb * kBM;
@@ -366,9 +378,9 @@ hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_
     const int nrb = (a.n_q + kBM - 1) / kBM;
     const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
     if (generic)
-        hipLaunchKernelGGL((prefill_f16_d128<MODE_GENERIC>), grid, block, 0, stream, a, causal, nrb);
+        hipLaunchKernelGGL((prefill_f16_d128<MODE_GENERIC>), grid, block, 0, stream, a, causal, nrb, a.P);
     else
-        hipLaunchKernelGGL((prefill_f16_d128<MODE_FAST>), grid, block, 0, stream, a, causal, nrb);
+        hipLaunchKernelGGL((prefill_f16_d128<MODE_FAST>), grid, block, 0, stream, a, causal, nrb, a.P);
     return hipGetLastError();
 }
 

@@ -238,6 +238,7 @@ int sixi_attn_forward(const sixi_attn_params* p) {
         a.xcd_remap = 0;
         e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D, pl.row_tiles, stream);
     } else {
+        a.P = cu_count_cached();  // the prefill grid order depends on the CU count
         e = sixi::launch_prefill(a, pl.kv_type, pl.mask_mode, pl.D, stream);
     }
     if (e == hipErrorNotSupported) return SIXI_E_UNSUPPORTED;
