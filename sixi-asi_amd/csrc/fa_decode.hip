@@ -378,8 +378,8 @@ __device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT>& acc, 
     for (int n = 0; n < NT; ++n) {
         const int row = 16 * (n0 + n) + r;
         if (row >= R) continue;
-        const int j = row / a.G;
-        const int h = g * a.G + row % a.G;
+        const int j = row / a.Gr;
+        const int h = g * a.G + a.hoff + row % a.Gr;
         const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
         char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + c * 32 * 4;
 #pragma unroll
@@ -438,7 +438,8 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
     const int c = lane >> 4;
     const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
     const StreamDims sd = stream_dims(a, s);
-    const int G = a.G;
+    const int G = a.Gr;                 // rows of one block row (heads of this launch)
+    const int hb = g * a.G + a.hoff;    // first of those heads
     const int R = G * sd.ql;
     const int n0 = rg * NTW;  // first row tile of this wave
 
@@ -456,7 +457,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
         const int row = idx >> 4;
         qok[k] = row < R;
         const int rr = qok[k] ? row : 0;
-        qsrc[k] = a.q + (int64_t)(rr / G) * a.q_nb1 + (int64_t)(g * G + rr % G) * a.q_nb2 + (int64_t)s * a.q_nb3 +
+        qsrc[k] = a.q + (int64_t)(rr / G) * a.q_nb1 + (int64_t)(hb + rr % G) * a.q_nb2 + (int64_t)s * a.q_nb3 +
                   (int64_t)(idx & 15) * 8 * a.q_es;
     }
     float xv[QIT][8];
@@ -522,7 +523,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
         const int j = valid ? row / G : 0;
         ri.j[n] = j;
         ri.vis[n] = (valid && causal) ? sd.kl + j + 1 : sd.nc;
-        ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, g * G + (valid ? row % G : 0)) : 1.0f;
+        ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, hb + (valid ? row % G : 0)) : 1.0f;
     }
     // tiles below t_full see no masked cell for any row
     const int t_full = (MODE == MODE_GENERIC) ? 0 : (causal ? (sd.kl + 1) / kTile : sd.nc / kTile);
@@ -683,7 +684,7 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
         const int row = 16 * (n0 + n) + r;
         valid[n] = row < R;
         const int rr = valid[n] ? row : 0;
-        src[n] = a.q + (int64_t)(rr / a.G) * a.q_nb1 + (int64_t)(g * a.G + rr % a.G) * a.q_nb2 +
+        src[n] = a.q + (int64_t)(rr / a.Gr) * a.q_nb1 + (int64_t)(g * a.G + a.hoff + rr % a.Gr) * a.q_nb2 +
                  (int64_t)s * a.q_nb3 + (int64_t)(8 * c) * a.q_es;
     }
     if (a.q_f16) {
@@ -849,8 +850,8 @@ __device__ __forceinline__ void write_rows_wide(const FaArgs& a, const Acc<NT>& 
     for (int n = 0; n < NT; ++n) {
         const int row = 16 * (n0 + n) + r;
         if (row >= R) continue;
-        const int j = row / a.G;
-        const int h = g * a.G + row % a.G;
+        const int j = row / a.Gr;
+        const int h = g * a.G + a.hoff + row % a.Gr;
         const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
         char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + c * 16;
 #pragma unroll
@@ -892,7 +893,8 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     const int c = lane >> 4;
     const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
     const StreamDims sd = table_dims(sh.st, s);
-    const int G = a.G;
+    const int G = a.Gr;                 // rows of one block row (heads of this launch)
+    const int hb = g * a.G + a.hoff;    // first of those heads
     const int R = G * sd.ql;
     const int n0 = rg * NTW;
 
@@ -908,7 +910,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
         const int j = valid ? row / G : 0;
         ri.j[n] = j;
         ri.vis[n] = (valid && causal) ? sd.kl + j + 1 : sd.nc;
-        ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, g * G + (valid ? row % G : 0)) : 1.0f;
+        ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, hb + (valid ? row % G : 0)) : 1.0f;
     }
     // steps below t_full see no masked cell for any row
     const int t_full = (MODE == MODE_GENERIC) ? 0 : (causal ? (sd.kl + 1) / kWide : sd.nc / kWide);
@@ -1083,9 +1085,10 @@ decode_wide_d128(FaArgs a, int causal) {
 // of the work-groups.  grid = (S*Hkv segments, row blocks of 8); 256 threads = 8 rows x 32
 // four-dim chunks, so every (row, chunk) is one thread.
 __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
-    __shared__ int ps[kMaxStreams + 1];
-    if (threadIdx.x < 64) build_tile_prefix(a, ps);
+    __shared__ StreamTable st;
+    if (threadIdx.x < 64) build_tile_prefix(a, st.ps, st.dims);
     __syncthreads();
+    const int* ps = st.ps;
     const int64_t k = blockIdx.x;
     const int s = (int)(k / a.Hkv);
     const int g = (int)(k % a.Hkv);
@@ -1100,19 +1103,20 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     const int64_t p_last = ((ck + ct) * P - 1) / T;
     if (p_first == p_last) return;  // written whole by its only work-group
 
-    const StreamDims sd = stream_dims(a, s);
+    const StreamDims sd = table_dims(st, s);
     const int row = blockIdx.y * 8 + (threadIdx.x >> 5);
-    if (row >= a.G * sd.ql) return;
+    if (row >= a.Gr * sd.ql) return;
     const int d0 = (threadIdx.x & 31) * 4;
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    // four pieces per step: their loads are independent and overlap
-    for (int64_t p0 = p_first; p0 <= p_last; p0 += 4) {
-        f32x4 ov[4];
-        float mv[4], lv[4];
+    // eight pieces per step (a segment rarely has more): their loads are independent, so
+    // the merge costs one memory latency
+    for (int64_t p0 = p_first; p0 <= p_last; p0 += 8) {
+        f32x4 ov[8];
+        float mv[8], lv[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 8; ++u) {
             const int64_t p = p0 + u <= p_last ? p0 + u : p_last;
             const float* sl = base + p * a.slot_floats;
             ov[u] = *reinterpret_cast<const f32x4*>(sl + (int64_t)row * 128 + d0);
@@ -1120,12 +1124,12 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
             lv[u] = sl[(int64_t)rows_slot * 129 + row];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 8; ++u)
             if (p0 + u <= p_last) merge_row<1>(M, L, &o, mv[u], lv[u], &ov[u]);
     }
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;
-    const int j = row / a.G;
-    const int h = g * a.G + row % a.G;
+    const int j = row / a.Gr;
+    const int h = g * a.G + a.hoff + row % a.Gr;
     st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
 }
 

@@ -32,6 +32,8 @@ struct FaArgs {
     int32_t m_ne3;
 
     int32_t S, H, Hkv, G;  // streams, q heads, kv heads, H / Hkv
+    int32_t Gr, hoff;      // heads of each GQA group this launch covers: hoff .. hoff+Gr-1
+                           // (rows of a group = Gr * q_len, row r -> head g*G + hoff + r % Gr)
     int32_t n_q, n_kv;     // view extents (max rows per stream, cells per stream)
     float scale;           // softmax scale (already divided by the softcap when it is on)
     float scale_log2;      // scale * log2(e)

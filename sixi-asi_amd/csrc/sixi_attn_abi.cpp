@@ -7,6 +7,7 @@
 // GGML_ASSERT.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -21,6 +22,7 @@ using sixi::FaArgs;
 constexpr size_t kWsAlign = 256;
 constexpr int kMaxHeadDim = 128;       // head dims built for gfx950 in this library
 constexpr int kSplitMaxRows = 16 * sixi::kDecodeMaxRowTiles;  // G * n_q of the split-K kernel
+constexpr int64_t kQ8MaxRows = 48;  // rows per kv-head group of one q8_0 split-K launch
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -60,6 +62,7 @@ struct Plan {
     int D = 0;
     bool splitk = true;
     int row_tiles = 0;
+    int heads_per_launch = 0;  // split-K: heads of each GQA group per launch (the group in parts)
     size_t ws_bytes = 0;
 };
 
@@ -168,6 +171,7 @@ int resolve(const sixi_attn_params* p, Plan* out) {
         a.m_ne3 = 1;
     }
     a.S = (int32_t)S; a.H = (int32_t)H; a.Hkv = (int32_t)Hkv; a.G = (int32_t)(H / Hkv);
+    a.Gr = a.G; a.hoff = 0;
     a.n_q = (int32_t)n_q; a.n_kv = (int32_t)n_kv;
     const float softcap = p->logit_softcap;
     a.scale = softcap != 0.0f ? p->scale / softcap : p->scale;
@@ -186,10 +190,15 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
-    // q8_0 KV: the split-K kernel with one row group (up to 48 rows per kv-head group)
-    if (k.type == SIXI_TYPE_Q8_0 && rows > 48) return SIXI_E_UNSUPPORTED;
+    // q8_0 KV runs the 16-cell split-K kernel, which holds up to 48 rows per kv-head group:
+    // a larger group is covered in launches over disjoint head subsets (each reads the KV).
+    pl.heads_per_launch = a.G;
+    if (k.type == SIXI_TYPE_Q8_0 && rows > kQ8MaxRows) {
+        if (!pl.splitk || n_q > kQ8MaxRows) return SIXI_E_UNSUPPORTED;
+        pl.heads_per_launch = (int)(kQ8MaxRows / n_q);
+    }
     if (pl.splitk) {
-        pl.row_tiles = sixi::decode_row_tiles(rows);
+        pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles);
         const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
         pl.ws_bytes = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
@@ -236,7 +245,14 @@ int sixi_attn_forward(const sixi_attn_params* p) {
         a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles);
         a.P = sixi::decode_num_groups(a, cu_count_cached(), pl.row_tiles);
         a.xcd_remap = 0;
-        e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D, pl.row_tiles, stream);
+        e = hipSuccess;
+        // one launch pair per head subset, ordered on the stream (they share the workspace)
+        for (int h0 = 0; h0 < a.G && e == hipSuccess; h0 += pl.heads_per_launch) {
+            a.hoff = h0;
+            a.Gr = std::min(pl.heads_per_launch, a.G - h0);
+            e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D,
+                                    sixi::decode_row_tiles((int64_t)a.Gr * a.n_q), stream);
+        }
     } else {
         a.P = cu_count_cached();  // the prefill grid order depends on the CU count
         e = sixi::launch_prefill(a, pl.kv_type, pl.mask_mode, pl.D, stream);

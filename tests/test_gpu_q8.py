@@ -99,8 +99,22 @@ def test_q8_explicit_mask_and_invariance(fa):
         assert np.array_equal(base, _run(fa, w, dev), equal_nan=True)
 
 
-def test_q8_more_than_48_rows_is_unsupported(fa):
-    w = wl.Workload("q8_wide", 0x51A7_7000, 1, [100], [16], kv_type=sa.TYPE_Q8_0)
+@pytest.mark.parametrize("kv_len,q_len,H,Hkv", [
+    ([2000, 0, 513], [16, 16, 9], 24, 4),        # 16-token verify at GQA 6:1: 96 rows, two launches of 3 heads
+    ([700, 4100], [12, 5], 20, 4),               # GQA 5:1, 60 rows: launches of 4 and 1 heads
+])
+def test_q8_group_in_head_parts(fa, kv_len, q_len, H, Hkv):
+    """More than 48 rows per kv-head group: covered by launches over disjoint head subsets."""
+    _say(f"q8 head parts kv_len={kv_len} q_len={q_len} H={H} Hkv={Hkv}")
+    w = wl.Workload("q8_parts", 0x51A7_7000 + sum(kv_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv,
+                    kv_type=sa.TYPE_Q8_0)
+    host = wl.make_host(w, poison=True)
+    dev = wl.to_device(host)
+    _check(w, host, _run(fa, w, dev), list(range(w.S)), "q8 head parts")
+
+
+def test_q8_prefill_sized_block_is_unsupported(fa):
+    w = wl.Workload("q8_wide", 0x51A7_7100, 1, [100], [64], kv_type=sa.TYPE_Q8_0)
     host = wl.make_host(w)
     dev = wl.to_device(host)
     out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
