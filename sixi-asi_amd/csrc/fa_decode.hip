@@ -963,32 +963,33 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             dma16x8_to_lds(vrs, o8, base + 8192);
         }
     };
-    // step i reads slot i % NS.  After the barrier of step i every wave has left step i-1,
-    // so step i+NS-1 goes into its slot; NS-2 steps stay in flight behind step i.
-    static_assert(NS >= 2 && NS <= 4, "ring depth");
-#pragma unroll
-    for (int k = 0; k < NS - 1; ++k)
-        if (k < n_my) issue(k, k);
-#pragma unroll 1
-    for (int i = 0; i < n_iter; ++i) {
-        const int ahead = n_my - 1 - i;  // own steps issued after step i (row groups 0 and 1)
-        if (NS >= 4 && ahead >= 2) wait_vmcnt<16>();
-        else if (NS >= 3 && ahead >= 1) wait_vmcnt<8>();
-        else wait_vmcnt<0>();
+    // step i reads slot i % 2.  After the barrier of step i every wave has left step i-1, so
+    // step i+1 goes into its slot while step i is computed.
+    static_assert(NS == 2, "one step in flight per lane");
+    if (n_my > 0) issue(0, 0);
+    auto step = [&](int i, auto masked) {
+        wait_vmcnt<0>();  // this wave's share of step i (the only loads it has in flight)
         __syncthreads();
-        if (i + NS - 1 < n_my) issue(i + NS - 1, (i + NS - 1) % NS);
-        if (i < n_my) {
+        if (i + 1 < n_my) issue(i + 1, (i + 1) % NS);
+        if (!decltype(masked)::value || i < n_my) {
             const int t = t0 + i * TL;
             const int sl = i % NS;
             const u32x4* kslot = ring + sl * SLOT16;
             // the V area is 256-byte aligned, so ^ 32t only moves bits 5..7 of vrow
             const uint32_t vlane = ring_base + sl * kWideSlot + 8192 + vrow;
-            if (t < t_full)
-                wide_step<NTW, MODE, false>(a, acc, kslot, vlane, qv, t * kWide, ri, mrow, sd.nc, lane);
-            else
-                wide_step<NTW, MODE, true>(a, acc, kslot, vlane, qv, t * kWide, ri, mrow, sd.nc, lane);
+            wide_step<NTW, MODE, decltype(masked)::value>(a, acc, kslot, vlane, qv, t * kWide, ri, mrow, sd.nc, lane);
         }
-    }
+    };
+    // Steps that every lane has and that lie below t_full for every lane run unmasked in a
+    // loop of their own, the rest masked in a second loop.  (One loop choosing the body per
+    // step makes the compiler merge two accumulator sets every step: 96 register copies per
+    // step, and spills.)
+    const int n_plain = min(max((t_full - tb) / TL, 0), (te - tb) / TL);
+    int i = 0;
+#pragma unroll 1
+    for (; i < n_plain; ++i) step(i, std::false_type{});
+#pragma unroll 1
+    for (; i < n_iter; ++i) step(i, std::true_type{});
 
 #pragma unroll
     for (int n = 0; n < NTW; ++n) {
@@ -1050,13 +1051,15 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
         const int64_t xb = x > t0 ? x : t0;
         const int64_t xe = pt.x1 < ck + ct ? pt.x1 : ck + ct;
         if (xb < xe) {
+            // the walk reads the LDS table, so the compiler cannot see that these values are
+            // uniform; readfirstlane keeps them, and the addresses built on them, in SGPRs
             Piece pc;
-            pc.s = s;
-            pc.g = g;
-            pc.tb = (int)(xb - t0);
-            pc.te = (int)(xe - t0);
-            pc.nt_seg = ct - a.seg_cost;
-            pc.slot = (int64_t)s * Hkv + g + pt.p_log;
+            pc.s = __builtin_amdgcn_readfirstlane(s);
+            pc.g = __builtin_amdgcn_readfirstlane(g);
+            pc.tb = __builtin_amdgcn_readfirstlane((int)(xb - t0));
+            pc.te = __builtin_amdgcn_readfirstlane((int)(xe - t0));
+            pc.nt_seg = __builtin_amdgcn_readfirstlane(ct - a.seg_cost);
+            pc.slot = __builtin_amdgcn_readfirstlane((int)((int64_t)s * Hkv + g + pt.p_log));
             fn(pc);
         }
         x = ck + ct;

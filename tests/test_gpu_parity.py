@@ -82,6 +82,9 @@ def test_batched_verify_parity(fa):
     ([64, 1000, 2], [7, 7, 7], 24, 4),           # 42 rows: 3 row tiles
     ([3000, 45, 0, 511], [16, 13, 4, 16], 32, 8),  # GQA 4:1, 64 rows: 4 row tiles
     ([129, 2048], [16, 11], 40, 8),              # GQA 5:1, 80 rows: 5 row tiles run as 6
+    ([700, 3000], [16, 10], 12, 2),              # 96 rows, two kv-heads: head groups of 2
+    ([2000, 50, 900], [10, 16, 1], 6, 1),        # 96 rows, one kv-head: head groups of 1
+    ([1500, 400], [16, 3], 36, 6),               # 96 rows, six kv-heads: three groups of 2
     ([300, 33], [2, 2], 8, 8),                   # no GQA
     ([4096, 77], [5, 9], 32, 2),                 # GQA 16:1, 144 > 96 rows -> not split-K
 ])
