@@ -390,8 +390,9 @@ __device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT>& acc, 
     }
 }
 
-// Partial slot of `rows_slot` rows: unnormalised O rows [row][128] f32, then m[row], l[row]
-// (log2-domain references).
+// Partial slot of `rows_slot` rows: normalised O rows [row][128] f16 (O/l, a convex
+// combination of f16 V rows, so it fits f16 and rounds by at most 2^-11 relative), then
+// m[row] and l[row] in f32 (log2-domain references).
 template <int NT>
 __device__ __forceinline__ void write_partial(float* slot, int rows_slot, int n0, int R, const Acc<NT>& acc,
                                               int lane) {
@@ -400,15 +401,18 @@ __device__ __forceinline__ void write_partial(float* slot, int rows_slot, int n0
     for (int n = 0; n < NT; ++n) {
         const int row = 16 * (n0 + n) + r;
         if (row >= R) continue;
-        char* dst = reinterpret_cast<char*>(slot + (int64_t)row * 128) + c * 32 * 4;
+        const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
+        char* dst = reinterpret_cast<char*>(slot) + (int64_t)row * 256 + c * 64;  // dims 32c .. 32c+31
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            st16(dst + i * 32, f32x4{acc.o[0][n][i], acc.o[1][n][i], acc.o[2][n][i], acc.o[3][n][i]});
-            st16(dst + i * 32 + 16, f32x4{acc.o[4][n][i], acc.o[5][n][i], acc.o[6][n][i], acc.o[7][n][i]});
+            f16x8 h;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) h[t] = (_Float16)(acc.o[t][n][i] * inv);
+            *reinterpret_cast<u32x4*>(dst + i * 16) = as_u32x4(h);
         }
         if (c == 0) {
-            slot[(int64_t)rows_slot * 128 + row] = acc.m[n];
-            slot[(int64_t)rows_slot * 129 + row] = acc.l[n];
+            slot[(int64_t)rows_slot * 64 + row] = acc.m[n];
+            slot[(int64_t)rows_slot * 65 + row] = acc.l[n];
         }
     }
 }
@@ -868,12 +872,17 @@ __device__ __forceinline__ void write_partial_wide(float* slot, int rows_slot, i
     for (int n = 0; n < NT; ++n) {
         const int row = 16 * (n0 + n) + r;
         if (row >= R) continue;
-        char* dst = reinterpret_cast<char*>(slot + (int64_t)row * 128) + c * 16;
+        const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
+        char* dst = reinterpret_cast<char*>(slot) + (int64_t)row * 256 + c * 8;  // dims 16t + 4c .. +3
 #pragma unroll
-        for (int t = 0; t < 8; ++t) st16(dst + t * 64, acc.o[t][n]);
+        for (int t = 0; t < 8; ++t) {
+            const f16x4 h = {(_Float16)(acc.o[t][n][0] * inv), (_Float16)(acc.o[t][n][1] * inv),
+                             (_Float16)(acc.o[t][n][2] * inv), (_Float16)(acc.o[t][n][3] * inv)};
+            *reinterpret_cast<u32x2*>(dst + t * 32) = __builtin_bit_cast(u32x2, h);
+        }
         if (c == 0) {
-            slot[(int64_t)rows_slot * 128 + row] = acc.m[n];
-            slot[(int64_t)rows_slot * 129 + row] = acc.l[n];
+            slot[(int64_t)rows_slot * 64 + row] = acc.m[n];
+            slot[(int64_t)rows_slot * 65 + row] = acc.l[n];
         }
     }
 }
@@ -1118,17 +1127,21 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     for (int64_t p0 = p_first; p0 <= p_last; p0 += 8) {
         f32x4 ov[8];
         float mv[8], lv[8];
+        u32x2 hv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int64_t p = p0 + u <= p_last ? p0 + u : p_last;
             const float* sl = base + p * a.slot_floats;
-            ov[u] = *reinterpret_cast<const f32x4*>(sl + (int64_t)row * 128 + d0);
-            mv[u] = sl[(int64_t)rows_slot * 128 + row];
-            lv[u] = sl[(int64_t)rows_slot * 129 + row];
+            hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * 256 + d0 * 2);
+            mv[u] = sl[(int64_t)rows_slot * 64 + row];
+            lv[u] = sl[(int64_t)rows_slot * 65 + row];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 8; ++u) {
+            const f16x4 h = __builtin_bit_cast(f16x4, hv[u]);
+            ov[u] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]} * lv[u];  // back to O = l * (O/l)
             if (p0 + u <= p_last) merge_row<1>(M, L, &o, mv[u], lv[u], &ov[u]);
+        }
     }
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;
     const int j = row / a.Gr;

@@ -42,7 +42,7 @@ struct FaArgs {
     int32_t alibi_nlog2;   // 0 = ALiBi off
 
     // split-K bookkeeping (workspace)
-    float* part;           // partial slots of slot_floats floats: O rows [rows][128], then m, l
+    float* part;           // partial slots of slot_floats floats: O/l rows [rows][128] f16, then m, l
     int32_t P;             // work-groups of the split-K launch (prefill: CUs of the device)
     int32_t xcd_remap;     // 1: consecutive tile ranges go to work-groups of one XCD
     int32_t tile_cells;    // KV cells per split tile (decode_tile_cells)
@@ -82,8 +82,8 @@ inline int decode_row_tiles(int64_t rows) {
     return rt <= 3 ? rt : 2 * ((rt + 1) / 2);
 }
 inline int64_t decode_slot_floats(int row_tiles) {
-    // O rows [16*row_tiles][128] f32, then m and l per row
-    return (int64_t)row_tiles * 16 * (128 + 2);
+    // O/l rows [16*row_tiles][128] f16 (64 floats' worth), then m and l per row in f32
+    return (int64_t)row_tiles * 16 * (64 + 2);
 }
 
 }  // namespace sixi
