@@ -208,6 +208,9 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         const char* kt = lds + buf * kKBytes;
 
         // ---- S^T = K Q^T: two 32-cell blocks ----
+        // (the MFMA phases run at raised wave priority, so that the SIMD feeds the matrix core of
+        // the wave in an MFMA phase first while the other wave on the SIMD works its softmax)
+        __builtin_amdgcn_s_setprio(1);
         f32x16 st[2];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
@@ -217,6 +220,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
                 st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 8192 + koff[ks])), qop[ks],
                                       st[cb]);
         }
+
+        __builtin_amdgcn_s_setprio(0);
 
         // ---- scores, row max (lanes l and l^32 hold the row's 64 cells) ----
         float mx = neg_inf();
@@ -304,6 +309,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         }
 
         // ---- O^T += V^T P^T, V^T by transposed reads of the V rows ----
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
@@ -320,6 +326,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
             }
         }
 
+        __builtin_amdgcn_s_setprio(0);
         if (more) wait_vmcnt<0>();  // this wave's share of tile t+1 is in LDS
         __syncthreads();
     };
