@@ -1069,6 +1069,12 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
             pc.te = __builtin_amdgcn_readfirstlane((int)(xe - t0));
             pc.nt_seg = __builtin_amdgcn_readfirstlane(ct - a.seg_cost);
             pc.slot = __builtin_amdgcn_readfirstlane((int)((int64_t)s * Hkv + g + pt.p_log));
+            // the segment's first and last piece tell decode_merge which slots to combine
+            if (threadIdx.x == 0) {
+                const int64_t seg = (int64_t)s * Hkv + g;
+                if (pc.tb == 0) a.seg_pieces[2 * seg] = pt.p_log;
+                if (pc.te == pc.nt_seg) a.seg_pieces[2 * seg + 1] = pt.p_log;
+            }
             fn(pc);
         }
         x = ck + ct;
@@ -1095,43 +1101,32 @@ decode_wide_d128(FaArgs a, int causal) {
 
 // Combines the pieces of every segment that more than one work-group touched, in the order
 // of the work-groups.  grid = (S*Hkv segments, row blocks of 8); 256 threads = 8 rows x 32
-// four-dim chunks, so every (row, chunk) is one thread.
+// four-dim chunks, so every (row, chunk) is one thread.  The split kernel recorded the
+// segment's first and last piece; the stream extents come in the same round trip.
 __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
-    __shared__ StreamTable st;
-    if (threadIdx.x < 64) build_tile_prefix(a, st.ps, st.dims);
-    __syncthreads();
-    const int* ps = st.ps;
     const int64_t k = blockIdx.x;
     const int s = (int)(k / a.Hkv);
     const int g = (int)(k % a.Hkv);
-    const int ct = ps[s + 1] - ps[s];
-    if (ct == 0) return;
-    const int64_t T = (int64_t)a.Hkv * ps[a.S];
-    const int64_t P = T < a.P ? T : a.P;
-    const int64_t ck = (int64_t)a.Hkv * ps[s] + (int64_t)g * ct;
-    // work-groups holding the segment's first and last tile (unit x lies in group
-    // floor(((x+1)P - 1) / T))
-    const int64_t p_first = ((ck + a.seg_cost + 1) * P - 1) / T;
-    const int64_t p_last = ((ck + ct) * P - 1) / T;
-    if (p_first == p_last) return;  // written whole by its only work-group
-
-    const StreamDims sd = table_dims(st, s);
+    const StreamDims sd = stream_dims(a, s);
+    const int p_first = a.seg_pieces[2 * k], p_last = a.seg_pieces[2 * k + 1];
     const int row = blockIdx.y * 8 + (threadIdx.x >> 5);
-    if (row >= a.Gr * sd.ql) return;
+    if (row >= a.Gr * sd.ql) return;  // (a segment without rows has stale entries)
+    if (p_first == p_last) return;    // written whole by its only work-group
+
     const int d0 = (threadIdx.x & 31) * 4;
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
     // eight pieces per step (a segment rarely has more): their loads are independent, so
     // the merge costs one memory latency
-    for (int64_t p0 = p_first; p0 <= p_last; p0 += 8) {
+    for (int p0 = p_first; p0 <= p_last; p0 += 8) {
         f32x4 ov[8];
         float mv[8], lv[8];
         u32x2 hv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int64_t p = p0 + u <= p_last ? p0 + u : p_last;
-            const float* sl = base + p * a.slot_floats;
+            const int p = p0 + u <= p_last ? p0 + u : p_last;
+            const float* sl = base + (int64_t)p * a.slot_floats;
             hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * 256 + d0 * 2);
             mv[u] = sl[(int64_t)rows_slot * 64 + row];
             lv[u] = sl[(int64_t)rows_slot * 65 + row];

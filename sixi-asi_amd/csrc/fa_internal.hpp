@@ -48,6 +48,7 @@ struct FaArgs {
     int32_t tile_cells;    // KV cells per split tile (decode_tile_cells)
     int32_t seg_cost;      // tiles' worth of work charged to each segment in the split
     int64_t slot_floats;   // floats per partial slot
+    int32_t* seg_pieces;   // per segment: logical work-groups of its first and last piece
 };
 
 // Host-side launchers (defined in the .hip files).  hipErrorNotSupported = not built.

@@ -61,6 +61,7 @@ struct Plan {
     int mask_mode = 0;
     int D = 0;
     bool splitk = true;
+    size_t seg_offset = 0;  // split-K: byte offset of the per-segment piece table
     int row_tiles = 0;
     int heads_per_launch = 0;  // split-K: heads of each GQA group per launch (the group in parts)
     size_t ws_bytes = 0;
@@ -201,7 +202,9 @@ int resolve(const sixi_attn_params* p, Plan* out) {
         pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles);
         const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
-        pl.ws_bytes = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
+        // partial slots, then (first, last) piece of every segment
+        pl.seg_offset = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
+        pl.ws_bytes = align_up(pl.seg_offset + (size_t)(S * Hkv) * 2 * sizeof(int32_t), kWsAlign);
     } else {
         // the prefill kernel keeps everything on chip; a token workspace keeps the contract uniform
         if (S * H * ((n_q + 127) / 128) > (int64_t)INT32_MAX) return SIXI_E_UNSUPPORTED;
@@ -238,6 +241,7 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     FaArgs& a = pl.a;
     char* ws = static_cast<char*>(p->workspace);
     a.part = reinterpret_cast<float*>(ws);
+    a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
     hipStream_t stream = static_cast<hipStream_t>(p->stream);
     hipError_t e;
     if (pl.splitk) {
