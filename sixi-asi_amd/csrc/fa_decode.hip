@@ -644,6 +644,9 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 // same staged steps and each stage half of every step (row group 0 the K rows, row group 1
 // the V rows); the lanes take the piece's steps round robin, and the whole group meets at
 // one barrier per step.  The lanes' (m, l, O) are merged in LDS at the end of the piece.
+// One work-group per CU, so each wave has a SIMD and up to 512 registers to itself: a
+// three-slot ring per lane keeps two steps in flight while one is computed, and a step
+// reads all its K and V^T operands from LDS before its first MFMA needs them.
 // A step covers 32 cells:
 //   * O^T += V^T P^T runs on v_mfma_f32_16x16x32_f16 (the 16x16x16 form issues at half
 //     that rate on gfx950), and each row maximum and Q^T operand covers twice the cells;
@@ -658,7 +661,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 // O layout: lane (r, c) holds row 16n + r, dims 16t + 4c + i at o[t][n][i].
 constexpr int kWide = kDecodeTileWide;  // 32 cells
 constexpr int kWideSlot = 16384;        // K [half][ks][lane] x 16 B, then V: 32 swizzled 256-B rows
-struct WideShape { static constexpr int lanes = 2, slots = 2, groups_per_cu = 2; };
+struct WideShape { static constexpr int lanes = 2, slots = 3, groups_per_cu = 1; };
 struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
 constexpr WideSplit kWide64 = {2, 2};         // 64 rows
 constexpr WideSplit kWide96 = {3, 2};         // 96 rows
@@ -732,17 +735,29 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u
     const int c = lane >> 4;
 
     // ---- S^T halves: lane (r, c) receives cells 16h + 4c + i of row r ----
+    f16x8 kop[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kop[h][ks] = as_f16x8(kslot[(h * 4 + ks) * 64 + lane]);
+    // V^T operands (vlane ^ 32t: chunk t of the lane's row), read now so that their latency
+    // hides under the scores and the softmax
+    u32x4 vt[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const lds_char* vp = lds_ptr(vlane ^ (32u * t));
+        const u32x2 lo = ld_tr16(vp);
+        const u32x2 hi = ld_tr16(vp + 4096);
+        vt[t] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
     f32x4 st[2][NT];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const f16x8 kop = as_f16x8(kslot[(h * 4 + ks) * 64 + lane]);
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int n = 0; n < NT; ++n)
-                st[h][n] = mfma16x16x32(kop, qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
-        }
-    }
+                st[h][n] = mfma16x16x32(kop[h][ks], qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
 
     // ---- scores (FAST: raw dot products; GENERIC: log2-domain logits) and row maxima ----
     const float c2 = a.scale_log2;
@@ -828,19 +843,15 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u
         }
     }
 
-    // ---- O^T += V^T P^T, V^T from transposed LDS reads (vlane ^ 32t: chunk t of the lane's row) ----
+    // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-        const lds_char* vp = lds_ptr(vlane ^ (32u * t));
-        const u32x2 lo = ld_tr16(vp);
-        const u32x2 hi = ld_tr16(vp + 4096);
-        const u32x4 vt = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
             if (MODE == MODE_GENERIC && a.mask)
-                acc.o[t][n] = mfma16x16x32(as_f16x8(vt & keep[n]), pt[n], acc.o[t][n]);
+                acc.o[t][n] = mfma16x16x32(as_f16x8(vt[t] & keep[n]), pt[n], acc.o[t][n]);
             else
-                acc.o[t][n] = mfma16x16x32(as_f16x8(vt), pt[n], acc.o[t][n]);
+                acc.o[t][n] = mfma16x16x32(as_f16x8(vt[t]), pt[n], acc.o[t][n]);
         }
     }
 }
@@ -972,14 +983,21 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             dma16x8_to_lds(vrs, o8, base + 8192);
         }
     };
-    // step i reads slot i % 2.  After the barrier of step i every wave has left step i-1, so
-    // step i+1 goes into its slot while step i is computed.
-    static_assert(NS == 2, "one step in flight per lane");
-    if (n_my > 0) issue(0, 0);
+    // Step i reads slot i % NS.  After the barrier of step i every wave has left step i-1, so
+    // step i+NS-1 goes into that step's slot while steps i+1 .. i+NS-2 are still in flight.
+    // Each issue is one batch of 8 loads per wave, and the ring loads are the only loads a
+    // wave has in flight in the step loop, so vmcnt counts the batches issued after step i.
+    static_assert(NS >= 2 && NS <= 4, "ring depth");
+#pragma unroll
+    for (int q = 0; q < NS - 1; ++q)
+        if (q < n_my) issue(q, q);
     auto step = [&](int i, auto masked) {
-        wait_vmcnt<0>();  // this wave's share of step i (the only loads it has in flight)
+        const int later = min(max(n_my - 1 - i, 0), NS - 2);  // batches issued after step i's
+        if (later >= 2) wait_vmcnt<16>();
+        else if (later == 1) wait_vmcnt<8>();
+        else wait_vmcnt<0>();
         __syncthreads();
-        if (i + 1 < n_my) issue(i + 1, (i + 1) % NS);
+        if (i + NS - 1 < n_my) issue(i + NS - 1, (i + NS - 1) % NS);
         if (!decltype(masked)::value || i < n_my) {
             const int t = t0 + i * TL;
             const int sl = i % NS;
