@@ -158,6 +158,69 @@ def time_prefill(fa, steps: int, warmup: int):
     return flops / (t * 1e-3) / 1e12, t * 1e3
 
 
+def time_kv_store(w, dev, steps: int, warmup: int) -> dict:
+    """The KV-cache store before the verify attention (include/sixi_kv.h): the block's K and V
+    rows of every stream (f32, [S, q_len, Hkv, D]) written to cells kv_len .. kv_len+q_len-1,
+    as f16 into the workload's own cache and as q8_0 into a q8_0 cache of the same cells.
+
+    The two launches take a few microseconds of GPU time, less than the host needs to issue
+    them from Python, so they are captured once in a HIP graph (8 K+V stores per graph) and
+    the graph is replayed; the time is GPU time per K+V store."""
+    import ctypes
+
+    import torch
+
+    import sixi_attn as sa
+
+    lib = sa.load_library()
+    res = {}
+    src_k = torch.randn((w.S, w.n_q, w.Hkv, w.D), dtype=torch.float32, device="cuda")
+    src_v = torch.randn_like(src_k)
+    q8_k = torch.zeros((w.S, dev["k"].shape[1], w.Hkv, w.D // 32 * 34), dtype=torch.uint8, device="cuda")
+    q8_v = torch.zeros_like(q8_k)
+    rows = int(sum(w.q_len)) * w.Hkv
+    per_graph = 8
+    for name, ck, cv, row_bytes in (("f16", dev["k"], dev["v"], w.D * 2), ("q8_0", q8_k, q8_v, w.D // 32 * 34)):
+        pk = sa.kv_write_params(src_k, ck, dev["kv_len"], dev["q_len"])
+        pv = sa.kv_write_params(src_v, cv, dev["kv_len"], dev["q_len"])
+
+        def store():
+            st = torch.cuda.current_stream().cuda_stream
+            pk.stream = pv.stream = st
+            for p in (pk, pv):
+                rc = lib.sixi_kv_write(ctypes.byref(p))
+                if rc != sa.OK:
+                    raise sa.SixiAttnError(rc, sa.strerror(rc))
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                store()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(per_graph):
+                store()
+        torch.cuda.synchronize()
+        reps = max(1, steps // per_graph)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / (reps * per_graph) * 1e3
+        nbytes = 2 * rows * (w.D * 4 + row_bytes)  # K and V: f32 rows read, cache rows written
+        res[name] = {"us_k_and_v": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes}
+        del g
+    del q8_k, q8_v
+    return res
+
+
 def prefill_only(steps: int, warmup: int) -> int:
     import sixi_attn as sa
 
@@ -257,6 +320,12 @@ def main() -> int:
                 extra[name] = {"unavailable": str(e)}
             _log(f"{name}: {extra[name]}")
         result["configs"] = extra
+        # the KV-cache store that precedes each verify call (block rows of all streams)
+        try:
+            result["kv_store"] = time_kv_store(w, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
+        except sa.SixiAttnError as e:
+            result["kv_store"] = {"unavailable": str(e)}
+        _log(f"kv_store: {result['kv_store']}")
 
         # chunked causal prefill (2 chunks of 2048 rows on a 2048-cell cache)
         try:

@@ -129,6 +129,32 @@ def dequantize_q8_0(b: np.ndarray, n: int) -> np.ndarray:
     return out
 
 
+def kv_write(src: np.ndarray, cache: np.ndarray, kv_len: Optional[Sequence[int]] = None,
+             q_len: Optional[Sequence[int]] = None) -> np.ndarray:
+    """CPU restatement of the KV-cache store (include/sixi_kv.h, sixi_kv_write): row
+    j < q_len[s] of stream s goes to cell kv_len[s] + j of every kv-head, converted with the
+    reference's codecs (src/core/numeric.cpp:28-106 f16, :349-384 q8_0 -- this module's
+    fp32_to_fp16_bits / quantize_q8_0, pinned against the compiled reference source);
+    rows whose cell lies outside the cache are skipped.  ``src[S, n_rows, Hkv, D]`` float32
+    or float16; ``cache[S, n_cells, Hkv, D]`` uint16 f16 bits, or uint8 q8_0 blocks
+    ``[S, n_cells, Hkv, D/32*34]``.  Returns the updated copy of ``cache``."""
+    out = cache.copy()
+    S, n_rows, Hkv, D = src.shape
+    n_cells = cache.shape[1]
+    q8 = cache.dtype == np.uint8
+    for s in range(S):
+        ql = n_rows if q_len is None else int(q_len[s])
+        base = 0 if kv_len is None else int(kv_len[s])
+        for j in range(min(ql, n_rows)):
+            cell = base + j
+            if cell < 0 or cell >= n_cells:
+                continue
+            x = src[s, j].astype(np.float32)
+            for h in range(Hkv):
+                out[s, cell, h] = quantize_q8_0(x[h]) if q8 else fp32_to_fp16_bits(x[h])
+    return out
+
+
 def fill_normal(seed: int, seq: int, n: int, mul: float = 1.0) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     load().oracle_fill_normal_f32(seed, seq, mul, out.ctypes.data, n)

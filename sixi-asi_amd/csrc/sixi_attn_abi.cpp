@@ -12,12 +12,14 @@
 #include <cstdint>
 #include <cstring>
 
+#include "abi_util.hpp"
 #include "fa_internal.hpp"
 #include "sixi_attn.h"
 
 namespace {
 
 using sixi::FaArgs;
+using namespace sixi_abi;
 
 constexpr size_t kWsAlign = 256;
 constexpr int kMaxHeadDim = 128;       // head dims built for gfx950 in this library
@@ -25,35 +27,6 @@ constexpr int kSplitMaxRows = 16 * sixi::kDecodeMaxRowTiles;  // G * n_q of the 
 constexpr int64_t kQ8MaxRows = 48;  // rows per kv-head group of one q8_0 split-K launch
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
-bool mul_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_mul_overflow(a, b, out); }
-bool add_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_add_overflow(a, b, out); }
-
-// Largest byte offset touched by a view (0 for empty), or -1 on overflow.
-int64_t view_span(const sixi_view& v, int64_t row_bytes) {
-    int64_t span = row_bytes, t = 0;
-    for (int d = 1; d < 4; ++d) {
-        if (v.ne[d] <= 0) return 0;
-        if (!mul_ok(v.ne[d] - 1, v.nb[d], &t) || !add_ok(span, t, &span)) return -1;
-    }
-    return span;
-}
-
-int elem_bytes(int32_t type) {
-    switch (type) {
-        case SIXI_TYPE_F32: return 4;
-        case SIXI_TYPE_F16: return 2;
-        default: return 0;
-    }
-}
-
-// Bytes of one head row of D elements.
-int64_t row_bytes(int32_t type, int64_t D) {
-    if (type == SIXI_TYPE_Q8_0) return D / 32 * 34;
-    return D * elem_bytes(type);
-}
-
-bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)a) == 0; }
 
 struct Plan {
     FaArgs a{};

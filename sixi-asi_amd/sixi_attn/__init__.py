@@ -42,6 +42,9 @@ EXPORTED_SYMBOLS = (
     "sixi_attn_validate",
     "sixi_attn_strerror",
     "sixi_attn_abi_version",
+    "sixi_kv_write",
+    "sixi_kv_write_validate",
+    "sixi_kv_copy",
 )
 
 
@@ -86,6 +89,30 @@ class SixiAttnParams(ctypes.Structure):
     ]
 
 
+class SixiKvWriteParams(ctypes.Structure):
+    _fields_ = [
+        ("src", SixiView),
+        ("dst", SixiView),
+        ("kv_len", ctypes.c_void_p),
+        ("q_len", ctypes.c_void_p),
+        ("flags", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
+class SixiKvCopyParams(ctypes.Structure):
+    _fields_ = [
+        ("cache", SixiView),
+        ("src_stream", ctypes.c_int32),
+        ("dst_stream", ctypes.c_int32),
+        ("src_cell", ctypes.c_int64),
+        ("dst_cell", ctypes.c_int64),
+        ("n_cells", ctypes.c_int64),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -112,6 +139,13 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.sixi_attn_strerror.restype = ctypes.c_char_p
     lib.sixi_attn_abi_version.argtypes = []
     lib.sixi_attn_abi_version.restype = ctypes.c_int
+    PW = ctypes.POINTER(SixiKvWriteParams)
+    lib.sixi_kv_write.argtypes = [PW]
+    lib.sixi_kv_write.restype = ctypes.c_int
+    lib.sixi_kv_write_validate.argtypes = [PW]
+    lib.sixi_kv_write_validate.restype = ctypes.c_int
+    lib.sixi_kv_copy.argtypes = [ctypes.POINTER(SixiKvCopyParams)]
+    lib.sixi_kv_copy.restype = ctypes.c_int
     if path is None:
         _lib = lib
     return lib
@@ -228,3 +262,70 @@ class FlashAttnExt:
         if check and rc != OK:
             raise SixiAttnError(rc, strerror(rc))
         return rc
+
+
+def _cache_view(cache, head_dim):
+    import torch
+
+    if cache.dtype == torch.uint8:
+        return view_of(cache, TYPE_Q8_0, head_dim)
+    return view_of(cache)
+
+
+def kv_write_params(src, cache, kv_len=None, q_len=None, stream=None) -> SixiKvWriteParams:
+    """Parameters of ``sixi_kv_write`` for torch tensors: ``src[S, n_rows, Hkv, D]`` f32 or
+    f16, ``cache[S, n_cells, Hkv, D]`` f16 (or uint8 q8_0 blocks ``[..., D/32*34]``)."""
+    p = SixiKvWriteParams()
+    p.src = view_of(src)
+    p.dst = _cache_view(cache, src.shape[-1])
+    p.kv_len = kv_len.data_ptr() if kv_len is not None else None
+    p.q_len = q_len.data_ptr() if q_len is not None else None
+    p.flags = 0
+    p.stream = stream
+    return p
+
+
+def kv_write(src, cache, kv_len=None, q_len=None, stream=None, check=True) -> int:
+    """Stores the new K (or V) rows of each stream in its cache cells.
+
+    Row j < q_len[s] of stream s goes to cell kv_len[s] + j, converted to the cache type with
+    the reference's codecs (src/core/numeric.cpp:28-106 f16, :349-384 q8_0) -- the store
+    llama.cpp makes (ggml_set_rows into the cache view) inside every llama_decode the
+    reference calls at src/core/core_execution.cpp:2074, :3536 and :3811.  Rows whose cell
+    falls outside the cache are skipped.  Asynchronous on the current stream.
+    """
+    import torch
+
+    lib = load_library()
+    p = kv_write_params(src, cache, kv_len, q_len, stream)
+    if p.stream is None:
+        p.stream = torch.cuda.current_stream(src.device).cuda_stream
+    rc = lib.sixi_kv_write(ctypes.byref(p))
+    if check and rc != OK:
+        raise SixiAttnError(rc, strerror(rc))
+    return rc
+
+
+def kv_copy(cache, src_stream: int, dst_stream: int, n_cells: int, src_cell: int = 0, dst_cell: int = 0,
+            head_dim: Optional[int] = None, stream=None, check=True) -> int:
+    """Copies cells [src_cell, src_cell + n_cells) of one stream to another stream's cells --
+    the data movement of llama_memory_seq_cp between sequences kept in separate streams
+    (src/core/core_execution.cpp:3215-3216, :3245-3246).  ``cache[S, n_cells, Hkv, D]`` f16,
+    or uint8 q8_0 blocks with ``head_dim``.  Overlapping ranges raise."""
+    import torch
+
+    lib = load_library()
+    p = SixiKvCopyParams()
+    if cache.dtype == torch.uint8:
+        if head_dim is None:
+            raise ValueError("a q8_0 cache needs head_dim")
+        p.cache = view_of(cache, TYPE_Q8_0, head_dim)
+    else:
+        p.cache = view_of(cache)
+    p.src_stream, p.dst_stream = int(src_stream), int(dst_stream)
+    p.src_cell, p.dst_cell, p.n_cells = int(src_cell), int(dst_cell), int(n_cells)
+    p.stream = stream if stream is not None else torch.cuda.current_stream(cache.device).cuda_stream
+    rc = lib.sixi_kv_copy(ctypes.byref(p))
+    if check and rc != OK:
+        raise SixiAttnError(rc, strerror(rc))
+    return rc

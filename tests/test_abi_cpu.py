@@ -1,5 +1,5 @@
-"""The C ABI on any host: the library loads, exports what include/sixi_attn.h declares, and
-rejects bad descriptions with the documented status codes before touching a device."""
+"""The C ABI on any host: the library loads, exports what include/*.h declare, and rejects
+bad descriptions with the documented status codes before touching a device."""
 import ctypes
 import pathlib
 import re
@@ -9,12 +9,14 @@ import pytest
 import sixi_attn as sa
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "sixi_attn.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def _declared():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(sixi_attn_\w+)\(", text, re.M)))
+    names = set()
+    for h in HEADERS:
+        names |= set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(sixi_\w+)\(", h.read_text(), re.M))
+    return sorted(names)
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -110,3 +112,91 @@ def test_forward_without_workspace_fails_before_any_launch():
     p.workspace = None
     p.workspace_bytes = 0
     assert sa.load_library().sixi_attn_forward(ctypes.byref(p)) == sa.E_OUT_OF_BOUNDS
+
+
+# ---- include/sixi_kv.h ---------------------------------------------------------------------
+
+def _kv_write_params(S=3, n_rows=16, Hkv=4, D=128, n_cells=4096, src_type=sa.TYPE_F32, dst_type=sa.TYPE_F16):
+    p = sa.SixiKvWriteParams()
+    es = 4 if src_type == sa.TYPE_F32 else 2
+    p.src = sa.make_view(FAKE, src_type, [D, n_rows, Hkv, S], [es, Hkv * D * es, D * es, n_rows * Hkv * D * es])
+    row = D * 2 if dst_type == sa.TYPE_F16 else D // 32 * 34
+    nb0 = 2 if dst_type == sa.TYPE_F16 else 34
+    p.dst = sa.make_view(FAKE, dst_type, [D, n_cells, Hkv, S], [nb0, Hkv * row, row, n_cells * Hkv * row])
+    p.kv_len = FAKE
+    p.q_len = None
+    return p
+
+
+def _kv_validate(p):
+    return sa.load_library().sixi_kv_write_validate(ctypes.byref(p))
+
+
+def test_kv_write_valid_descriptions_pass():
+    for st in (sa.TYPE_F32, sa.TYPE_F16):
+        for dt in (sa.TYPE_F16, sa.TYPE_Q8_0):
+            for D in (128, 256):
+                assert _kv_validate(_kv_write_params(D=D, src_type=st, dst_type=dt)) == sa.OK
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda p: setattr(p, "flags", 2), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.src, "data", None), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.dst, "type", sa.TYPE_F32), sa.E_INVALID_ARGUMENT),      # cache must be f16/q8_0
+    (lambda p: setattr(p.src, "type", sa.TYPE_Q8_0), sa.E_INVALID_ARGUMENT),     # source must be f32/f16
+    (lambda p: p.dst.ne.__setitem__(0, 64), sa.E_INVALID_ARGUMENT),              # head dims differ
+    (lambda p: (p.src.ne.__setitem__(0, 48), p.dst.ne.__setitem__(0, 48)), sa.E_INVALID_ARGUMENT),  # D % 32
+    (lambda p: p.dst.ne.__setitem__(2, 8), sa.E_INVALID_ARGUMENT),               # kv-heads differ
+    (lambda p: p.dst.ne.__setitem__(3, 2), sa.E_INVALID_ARGUMENT),               # streams differ
+    (lambda p: p.src.nb.__setitem__(0, 8), sa.E_INVALID_ARGUMENT),               # rows not contiguous
+    (lambda p: p.dst.nb.__setitem__(1, 128), sa.E_INVALID_ARGUMENT),             # cells would alias
+    (lambda p: p.dst.nb.__setitem__(3, 1024), sa.E_INVALID_ARGUMENT),            # streams would alias
+    (lambda p: setattr(p.src, "data", FAKE + 4), sa.E_ALIGNMENT),
+    (lambda p: p.src.nb.__setitem__(1, 2056), sa.E_ALIGNMENT),
+    (lambda p: setattr(p.dst, "data", FAKE + 8), sa.E_ALIGNMENT),                # f16 rows 16-B aligned
+    (lambda p: p.src.nb.__setitem__(3, 1 << 62), sa.E_INTEGER_OVERFLOW),
+])
+def test_kv_write_rejects(mutate, code):
+    p = _kv_write_params()
+    mutate(p)
+    assert _kv_validate(p) == code
+    assert sa.load_library().sixi_kv_write(ctypes.byref(p)) == code
+
+
+def test_kv_write_q8_rows_need_only_2_byte_alignment():
+    p = _kv_write_params(dst_type=sa.TYPE_Q8_0)
+    p.dst.data = FAKE + 2
+    assert _kv_validate(p) == sa.OK
+
+
+def _kv_copy_params(S=4, Hkv=4, D=128, n_cells=1024, dst_type=sa.TYPE_F16):
+    p = sa.SixiKvCopyParams()
+    row = D * 2 if dst_type == sa.TYPE_F16 else D // 32 * 34
+    nb0 = 2 if dst_type == sa.TYPE_F16 else 34
+    p.cache = sa.make_view(FAKE, dst_type, [D, n_cells, Hkv, S], [nb0, Hkv * row, row, n_cells * Hkv * row])
+    p.src_stream, p.dst_stream, p.src_cell, p.dst_cell, p.n_cells = 0, 1, 0, 0, 512
+    return p
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda p: setattr(p.cache, "data", None), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.cache, "type", sa.TYPE_F32), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p, "dst_stream", 4), sa.E_OUT_OF_BOUNDS),
+    (lambda p: setattr(p, "src_stream", -1), sa.E_OUT_OF_BOUNDS),
+    (lambda p: setattr(p, "src_cell", 600), sa.E_OUT_OF_BOUNDS),                  # 600 + 512 > 1024
+    (lambda p: setattr(p, "n_cells", -1), sa.E_INVALID_ARGUMENT),
+    (lambda p: (setattr(p, "dst_stream", 0), setattr(p, "dst_cell", 256)), sa.E_INVALID_ARGUMENT),  # overlap
+    (lambda p: p.cache.nb.__setitem__(1, 64), sa.E_INVALID_ARGUMENT),             # cells would alias
+    (lambda p: setattr(p.cache, "data", FAKE + 1), sa.E_ALIGNMENT),
+    (lambda p: (setattr(p, "src_cell", 1), setattr(p, "n_cells", (1 << 63) - 1)), sa.E_INTEGER_OVERFLOW),
+])
+def test_kv_copy_rejects(mutate, code):
+    p = _kv_copy_params()
+    mutate(p)
+    assert sa.load_library().sixi_kv_copy(ctypes.byref(p)) == code
+
+
+def test_kv_copy_of_nothing_is_ok_without_a_launch():
+    p = _kv_copy_params()
+    p.n_cells = 0
+    assert sa.load_library().sixi_kv_copy(ctypes.byref(p)) == sa.OK
