@@ -1,7 +1,7 @@
 """Builds the in-tree shared libraries of the MI355X attention path.
 
-    lib/libsixi_attn.so   gfx950 HIP kernels + the C ABIs of include/sixi_attn.h and
-                          include/sixi_kv.h (hipcc)
+    lib/libsixi_attn.so   gfx950 HIP kernels + the C ABIs of include/sixi_attn.h,
+                          include/sixi_kv.h and include/sixi_plan.h (hipcc)
     lib/libsixi_synth.so  seeded synthetic workload generator used by bench.py and tests (g++)
 
 Run as ``python sixi-asi_amd/build.py`` or through ``__graft_entry__.build()``.  Every call
@@ -35,7 +35,8 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
-HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp"]
+HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
+               "sixi_plan.cpp"]
 
 
 def _hipcc() -> str:

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "sixi_kv_write",
     "sixi_kv_write_validate",
     "sixi_kv_copy",
+    "sixi_verify_plan",
 )
 
 
@@ -113,6 +114,17 @@ class SixiKvCopyParams(ctypes.Structure):
     ]
 
 
+class SixiVerifyStream(ctypes.Structure):
+    _fields_ = [("stream", ctypes.c_int32), ("cached", ctypes.c_int32), ("real", ctypes.c_int32)]
+
+
+class SixiVerifySlot(ctypes.Structure):
+    _fields_ = [("part", ctypes.c_int32), ("index", ctypes.c_int32), ("row_offset", ctypes.c_int32),
+                ("rows", ctypes.c_int32)]
+
+
+PAD_REFERENCE, PAD_NONE = 0, 1
+
 _lib = None
 
 
@@ -146,6 +158,9 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.sixi_kv_write_validate.restype = ctypes.c_int
     lib.sixi_kv_copy.argtypes = [ctypes.POINTER(SixiKvCopyParams)]
     lib.sixi_kv_copy.restype = ctypes.c_int
+    lib.sixi_verify_plan.argtypes = [ctypes.POINTER(SixiVerifyStream), ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                     ctypes.POINTER(SixiVerifySlot), ctypes.POINTER(ctypes.c_int32)]
+    lib.sixi_verify_plan.restype = ctypes.c_int
     if path is None:
         _lib = lib
     return lib
@@ -329,3 +344,32 @@ def kv_copy(cache, src_stream: int, dst_stream: int, n_cells: int, src_cell: int
     if check and rc != OK:
         raise SixiAttnError(rc, strerror(rc))
     return rc
+
+
+def plan_verify(streams, n_ctx_seq: int = 0, pad_mode: int = PAD_REFERENCE):
+    """Forms the verify pass(es) of several streams (include/sixi_plan.h): ``streams`` is a list
+    of (stream id, cached tokens N, block rows).  Returns (n_parts, slots) with one
+    (part, index, row_offset, rows) per input stream.  PAD_REFERENCE reproduces the reference's
+    exec_verify_group (src/core/core_execution.cpp:2016-2212); PAD_NONE puts every stream in one
+    pass with its own row count."""
+    n = len(streams)
+    arr = (SixiVerifyStream * max(n, 1))()
+    for i, (sid, cached, real) in enumerate(streams):
+        arr[i].stream, arr[i].cached, arr[i].real = int(sid), int(cached), int(real)
+    out = (SixiVerifySlot * max(n, 1))()
+    n_parts = ctypes.c_int32(0)
+    rc = load_library().sixi_verify_plan(arr, n, int(n_ctx_seq), int(pad_mode), out, ctypes.byref(n_parts))
+    if rc != OK:
+        raise SixiAttnError(rc, strerror(rc))
+    return n_parts.value, [(out[i].part, out[i].index, out[i].row_offset, out[i].rows) for i in range(n)]
+
+
+def part_lengths(streams, slots, part: int, pad_mode: int = PAD_REFERENCE):
+    """(stream ids, kv_len, q_len) of one part, in the part's stream order: kv_len = cached
+    tokens, q_len = padded rows (PAD_REFERENCE: pad rows are computed and stored) or real rows
+    (PAD_NONE)."""
+    members = sorted((sl[1], i) for i, sl in enumerate(slots) if sl[0] == part)
+    ids = [streams[i][0] for _, i in members]
+    kv_len = [streams[i][1] for _, i in members]
+    q_len = [slots[i][3] if pad_mode == PAD_REFERENCE else streams[i][2] for _, i in members]
+    return ids, kv_len, q_len
