@@ -660,7 +660,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 //   * Q^T stays in registers for the whole piece.
 // O layout: lane (r, c) holds row 16n + r, dims 16t + 4c + i at o[t][n][i].
 constexpr int kWide = kDecodeTileWide;  // 32 cells
-constexpr int kWideSlot = 16384;        // K [half][ks][lane] x 16 B, then V: 32 swizzled 256-B rows
+constexpr int kWideSlot = 16384;        // K, then V: 32 cell rows of 256 B each, chunk-swizzled
 struct WideShape { static constexpr int lanes = 2, slots = 3, groups_per_cu = 1; };
 struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
 constexpr WideSplit kWide64 = {2, 2};         // 64 rows
@@ -730,7 +730,7 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
 
 template <int NT, int MODE, bool MASKED>
 __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u32x4* kslot, uint32_t vlane,
-                                          const f16x8 (&qv)[NT][4], int c0,
+                                          const uint32_t (&kofs)[4], const f16x8 (&qv)[NT][4], int c0,
                                           const RowInfo<NT>& ri, const char* mrow, int nc, int lane) {
     const int c = lane >> 4;
 
@@ -739,7 +739,9 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kop[h][ks] = as_f16x8(kslot[(h * 4 + ks) * 64 + lane]);
+        for (int ks = 0; ks < 4; ++ks)
+            kop[h][ks] = as_f16x8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kslot) + kofs[ks] +
+                                                                  4096 * h));
     // V^T operands (vlane ^ 32t: chunk t of the lane's row), read now so that their latency
     // hides under the scores and the softmax
     u32x4 vt[8];
@@ -946,11 +948,17 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     const buf_rsrc vrs = make_rsrc_uniform(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
                                            (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + 256));
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
-    // LDS-DMA source offsets from a step's first cell.  K (row group 0), load (h, ks): lane
-    // (r, c) copies cell 16h + r, dims 32ks + 8c .. +7 to [h][ks][lane].  V (row group 1),
-    // load u: lane t fills LDS row 4u + t/16 at 16-byte position t%16, i.e. 32-byte chunk
-    // (t%16)/2 of that row, which holds dims 16 * (chunk ^ (row % 8)).
-    const uint32_t koff = (uint32_t)r * knb + 16u * c;
+    // LDS-DMA source offsets from a step's first cell; every load copies the 256-byte rows of
+    // four cells (whole cache lines).  K (row group 0), load u: lane t fills LDS row
+    // 4u + t/16 at 16-byte position t%16, which holds 16-byte chunk (t%16) ^ (row % 16)
+    // (dims 8 * chunk); the A operand (h, ks) of lane (r, c) -- cell 16h + r, dims
+    // 32ks + 8c .. +7 -- then sits at 4096h + 256r + 16((4ks + c) ^ r), and the 16 lanes of a
+    // read hit 16 different chunk positions (conflict-free).  V (row group 1), load u: lane t
+    // fills LDS row 4u + t/16 at 16-byte position t%16, i.e. 32-byte chunk (t%16)/2 of that
+    // row, which holds dims 16 * (chunk ^ (row % 8)).
+    uint32_t kofs[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kofs[ks] = 256u * r + 16u * (uint32_t)((4 * ks + c) ^ r);
     uint32_t voff[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -973,9 +981,10 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
         uint32_t o8[8];
         if (rg == 0) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) o8[h * 4 + ks] = (c0 + 16 * h) * knb + koff + ks * 64;
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t cell = 4u * u + (uint32_t)(lane >> 4);
+                o8[u] = (c0 + cell) * knb + 16u * (((uint32_t)lane & 15u) ^ (cell & 15u));
+            }
             dma16x8_to_lds(krs, o8, base);
         } else if (rg == 1) {
 #pragma unroll
@@ -1004,7 +1013,8 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             const u32x4* kslot = ring + sl * SLOT16;
             // the V area is 256-byte aligned, so ^ 32t only moves bits 5..7 of vrow
             const uint32_t vlane = ring_base + sl * kWideSlot + 8192 + vrow;
-            wide_step<NTW, MODE, decltype(masked)::value>(a, acc, kslot, vlane, qv, t * kWide, ri, mrow, sd.nc, lane);
+            wide_step<NTW, MODE, decltype(masked)::value>(a, acc, kslot, vlane, kofs, qv, t * kWide, ri, mrow, sd.nc,
+                                                          lane);
         }
     };
     // Steps that every lane has and that lie below t_full for every lane run unmasked in a
