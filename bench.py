@@ -142,13 +142,18 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
-def time_prefill(fa, steps: int, warmup: int):
-    """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks)."""
+def time_prefill(fa, steps: int, warmup: int, kv_type=None):
+    """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks).
+    kv_type q8_0 runs the same chunks over a q8_0 cache (staged as f16 operands per call)."""
+    import dataclasses
+
     from sixi_attn import workloads as wl
 
     pre = []
     for name in ("prefill_chunk0", "prefill_chunk1"):
         wp = wl.config(name)
+        if kv_type is not None:
+            wp = dataclasses.replace(wp, kv_type=kv_type)
         dp = wl.to_device(wl.make_host(wp))
         msp, _ = time_calls(fa, wp, dp, steps, warmup)
         pre.append((wp, msp))
@@ -335,6 +340,9 @@ def main() -> int:
             result["prefill_roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": F16_PEAK_TFLOPS,
                                           "unit": "TFLOP/s", "frac": round(tf / F16_PEAK_TFLOPS, 4)}
             _log(f"prefill: {us:.1f} us for 2 chunks, {tf:.1f} TFLOP/s")
+            tq, uq = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0)
+            result["configs"]["prefill_q8_0"] = {"us_two_chunks": round(uq, 2), "TFLOPs": round(tq, 2)}
+            _log(f"prefill q8_0 KV: {uq:.1f} us for 2 chunks, {tq:.1f} TFLOP/s")
         except sa.SixiAttnError as e:
             result["prefill_tflops"] = None
             result["prefill_note"] = f"prefill kernel unavailable: {e}"

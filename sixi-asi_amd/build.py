@@ -35,7 +35,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
-HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
+HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "fa_q8_stage.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
                "sixi_plan.cpp"]
 
 

@@ -51,7 +51,25 @@ struct FaArgs {
     int32_t* seg_pieces;   // per segment: logical work-groups of its first and last piece
 };
 
+// q8_0 KV for prefill-sized blocks (fa_q8_stage.hip): K, V and Q staged as dense f16 rows in
+// the workspace, then the f16 prefill kernel.  k16/v16: [S][n_kv][Hkv][128], q16: [S][n_q][H][128].
+struct Q8StageArgs {
+    const char* q;
+    int64_t q_nb1, q_nb2, q_nb3;
+    int32_t q_es, q_f16;
+    const char* k;
+    int64_t k_nb1, k_nb2, k_nb3;
+    const char* v;
+    int64_t v_nb1, v_nb2, v_nb3;
+    const int32_t* kv_len;
+    const int32_t* q_len;
+    int32_t S, H, Hkv, n_q;
+    int64_t n_kv;
+    char *k16, *v16, *q16;
+};
+
 // Host-side launchers (defined in the .hip files).  hipErrorNotSupported = not built.
+hipError_t launch_q8_stage(const Q8StageArgs& a, hipStream_t stream);
 hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream);
 hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim,

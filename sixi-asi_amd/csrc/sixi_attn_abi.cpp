@@ -37,6 +37,9 @@ struct Plan {
     size_t seg_offset = 0;  // split-K: byte offset of the per-segment piece table
     int row_tiles = 0;
     int heads_per_launch = 0;  // split-K: heads of each GQA group per launch (the group in parts)
+    bool q8_stage = false;     // q8_0 KV staged as f16 rows in the workspace, then the f16 kernels
+    size_t stage_k = 0, stage_v = 0, stage_q = 0;  // byte offsets of the staged K, V and Q
+    size_t stage_bytes = 0;    // the split-K workspace follows the staging area
     size_t ws_bytes = 0;
 };
 
@@ -168,8 +171,24 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     // a larger group is covered in launches over disjoint head subsets (each reads the KV).
     pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && rows > kQ8MaxRows) {
-        if (!pl.splitk || n_q > kQ8MaxRows) return SIXI_E_UNSUPPORTED;
-        pl.heads_per_launch = (int)(kQ8MaxRows / n_q);
+        if (pl.splitk && n_q <= kQ8MaxRows) {
+            pl.heads_per_launch = (int)(kQ8MaxRows / n_q);
+        } else {
+            // prefill-sized blocks (or more than 48 rows of one head): K, V and Q are staged
+            // as f16 operands in the workspace (fa_q8_stage.hip) and the f16 kernels run
+            pl.q8_stage = true;
+            pl.kv_type = SIXI_TYPE_F16;
+            int64_t kv_bytes = 0, q_bytes = 0, cells = 0, span = 0;
+            if (!mul_ok(S * Hkv, n_kv, &cells) || !mul_ok(cells, D * 2, &kv_bytes) ||
+                !mul_ok(S * H, n_q, &q_bytes) || !mul_ok(q_bytes, D * 2, &q_bytes) ||
+                !mul_ok(n_kv + sixi::kDecodeTileWide, Hkv * D * 2, &span))
+                return SIXI_E_INTEGER_OVERFLOW;
+            if (span >= (int64_t)UINT32_MAX) return SIXI_E_UNSUPPORTED;
+            pl.stage_k = 0;
+            pl.stage_v = align_up((size_t)kv_bytes, kWsAlign);
+            pl.stage_q = pl.stage_v + align_up((size_t)kv_bytes, kWsAlign);
+            pl.stage_bytes = pl.stage_q + align_up((size_t)q_bytes, kWsAlign);
+        }
     }
     if (pl.splitk) {
         pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q);
@@ -177,11 +196,11 @@ int resolve(const sixi_attn_params* p, Plan* out) {
         const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
         // partial slots, then (first, last) piece of every segment
         pl.seg_offset = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
-        pl.ws_bytes = align_up(pl.seg_offset + (size_t)(S * Hkv) * 2 * sizeof(int32_t), kWsAlign);
+        pl.ws_bytes = pl.stage_bytes + align_up(pl.seg_offset + (size_t)(S * Hkv) * 2 * sizeof(int32_t), kWsAlign);
     } else {
         // the prefill kernel keeps everything on chip; a token workspace keeps the contract uniform
         if (S * H * ((n_q + 127) / 128) > (int64_t)INT32_MAX) return SIXI_E_UNSUPPORTED;
-        pl.ws_bytes = kWsAlign;
+        pl.ws_bytes = pl.stage_bytes > 0 ? pl.stage_bytes : kWsAlign;
     }
     *out = pl;
     return SIXI_OK;
@@ -213,10 +232,28 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     if (!aligned(p->workspace, kWsAlign)) return SIXI_E_ALIGNMENT;
     FaArgs& a = pl.a;
     char* ws = static_cast<char*>(p->workspace);
-    a.part = reinterpret_cast<float*>(ws);
-    a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
     hipStream_t stream = static_cast<hipStream_t>(p->stream);
     hipError_t e;
+    if (pl.q8_stage) {
+        sixi::Q8StageArgs st{};
+        st.q = a.q; st.q_nb1 = a.q_nb1; st.q_nb2 = a.q_nb2; st.q_nb3 = a.q_nb3;
+        st.q_es = a.q_es; st.q_f16 = a.q_f16;
+        st.k = a.k; st.k_nb1 = a.k_nb1; st.k_nb2 = a.k_nb2; st.k_nb3 = a.k_nb3;
+        st.v = a.v; st.v_nb1 = a.v_nb1; st.v_nb2 = a.v_nb2; st.v_nb3 = a.v_nb3;
+        st.kv_len = a.kv_len; st.q_len = a.q_len;
+        st.S = a.S; st.H = a.H; st.Hkv = a.Hkv; st.n_q = a.n_q; st.n_kv = a.n_kv;
+        st.k16 = ws + pl.stage_k; st.v16 = ws + pl.stage_v; st.q16 = ws + pl.stage_q;
+        e = sixi::launch_q8_stage(st, stream);
+        if (e != hipSuccess) return SIXI_E_BACKEND;
+        const int64_t row = (int64_t)pl.D * 2;
+        a.q = st.q16; a.q_nb2 = row; a.q_nb1 = (int64_t)a.H * row; a.q_nb3 = (int64_t)a.n_q * a.H * row;
+        a.q_es = 2; a.q_f16 = 1;
+        a.k = st.k16; a.k_nb2 = row; a.k_nb1 = (int64_t)a.Hkv * row; a.k_nb3 = (int64_t)a.n_kv * a.Hkv * row;
+        a.v = st.v16; a.v_nb2 = row; a.v_nb1 = a.k_nb1; a.v_nb3 = a.k_nb3;
+        ws += pl.stage_bytes;
+    }
+    a.part = reinterpret_cast<float*>(ws);
+    a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
     if (pl.splitk) {
         a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles);
         a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles);

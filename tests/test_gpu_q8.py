@@ -113,10 +113,29 @@ def test_q8_group_in_head_parts(fa, kv_len, q_len, H, Hkv):
     _check(w, host, _run(fa, w, dev), list(range(w.S)), "q8 head parts")
 
 
-def test_q8_prefill_sized_block_is_unsupported(fa):
-    w = wl.Workload("q8_wide", 0x51A7_7100, 1, [100], [64], kv_type=sa.TYPE_Q8_0)
+@pytest.mark.parametrize("name,kv_len,q_len,H,Hkv", [
+    ("q8 64 rows, one stream", [100], [64], 24, 4),              # 384 rows per group: staged prefill
+    ("q8 prefill-sized, ragged", [300, 1000], [200, 130], 24, 4),
+    ("q8 64 rows of one head", [700, 90], [64, 49], 4, 4),       # G = 1: staged split-K
+])
+def test_q8_staged_blocks(fa, name, kv_len, q_len, H, Hkv):
+    """Blocks the q8_0 split-K kernels do not hold: K, V and Q are staged as f16 operands in the
+    workspace and the f16 kernels run on them."""
+    _say(f"{name}: kv_len {kv_len} q_len {q_len} H {H} Hkv {Hkv}")
+    w = wl.Workload("q8_stage", 0x51A7_7100 + sum(q_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv,
+                    kv_type=sa.TYPE_Q8_0)
+    host = wl.make_host(w, poison=True)
+    dev = wl.to_device(host)
+    _check(w, host, _run(fa, w, dev), list(range(w.S)), name)
+
+
+def test_q8_staged_prefill_explicit_mask(fa):
+    w = wl.Workload("q8_stage_mask", 0x51A7_7180, 2, [500, 64], [160, 100], kv_type=sa.TYPE_Q8_0)
     host = wl.make_host(w)
     dev = wl.to_device(host)
-    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
-    rc = fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], check=False)
-    assert rc == sa.E_UNSUPPORTED
+    n_kv = dev["k"].shape[1]
+    mask = oracle.build_kq_mask(n_kv, w.n_q, host["kv_len"], host["q_len"])
+    dmask = torch.from_numpy(mask.view(np.float16)).cuda()
+    _say("q8 staged prefill, explicit mask")
+    got = _run(fa, w, dev, mask_mode=sa.MASK_EXPLICIT, mask=dmask)
+    _check(w, host, got, list(range(w.S)), "q8 staged prefill explicit mask")
