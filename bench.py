@@ -3,7 +3,7 @@
 Headline workload: batched speculative verify -- 32 streams x 16 drafted rows, block-causal,
 per-stream cached lengths drawn from [512, 16384], 24 q-heads / 4 kv-heads x 128, f16 KV in
 per-stream 256-cell pages, f32 Q -- one attention layer per step.  A step is one call of
-the C ABI (sixi_attn_forward), i.e. the split-K kernel (decode_wide_d128, 32-cell steps)
+the C ABI (sixi_attn_forward), i.e. the split-K kernel (decode_wide, 32-cell steps)
 plus its merge kernel, timed with HIP events on the stream the library launches on, inputs
 resident in HBM.
 
@@ -301,7 +301,7 @@ def main() -> int:
         "verify_tflops": head["TFLOPs"],
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_wide_d128<3,2,0> + decode_merge (one sixi_attn_forward call; "
+            "kernel": "decode_wide<3,2,0,128> + decode_merge (one sixi_attn_forward call; "
                       "achieved = algorithmic bytes / call time)",
             "achieved": gbs,
             "peak": HBM_PEAK_GBS,
@@ -313,7 +313,7 @@ def main() -> int:
 
     if not args.no_extra:
         extra = {}
-        for name in ("decode", "verify", "long_q8_decode", "long_q8_verify"):
+        for name in ("decode", "verify", "long_q8_decode", "long_q8_verify", "decode_d256", "batched_verify_d256"):
             try:
                 we = wl.config(name)
                 he = wl.make_host(we)

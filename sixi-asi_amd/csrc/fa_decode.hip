@@ -17,7 +17,8 @@
 //   decode_d128 (<= 48 rows, and q8_0 KV): tiles of 16 cells; two work-groups of four
 //     waves per CU, the waves independent tile lanes with private LDS rings (no barrier
 //     in the tile loop).  Described next.
-//   decode_wide_d128 (f16 KV, 49..96 rows): steps of 32 cells; described further down.
+//   decode_wide (f16 KV: 49..96 rows of 128-dim heads, any rows of 256-dim heads): steps of
+//     32 cells; described further down.
 // K/V reach LDS by direct global->LDS loads (buffer_load_dword{,x4} ... lds), so bytes in
 // flight cost no VGPRs.
 //
@@ -82,9 +83,9 @@ template <int KV> struct Shape;
 template <> struct Shape<SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 4, slots = 2, groups_per_cu = 2; };
 template <> struct Shape<SIXI_TYPE_Q8_0> { static constexpr int waves = 4, lanes = 4, slots = 3, groups_per_cu = 2; };
 
-template <int NT, int NS>
+template <int NT, int NS, int DT = 8>
 struct MergeBuf {
-    f32x4 o[NS][NT * 8 * 64];  // [slot][n*8 + tt][lane]
+    f32x4 o[NS][NT * DT * 64];  // [slot][n*DT + tt][lane]
     float m[NS][NT * 64];
     float l[NS][NT * 64];
 };
@@ -103,21 +104,21 @@ struct DecodeLds {
     int ps[kMaxStreams + 1];  // (no extents table: it would not leave room for two groups per CU)
 };
 
-template <int NT>
+template <int NT, int DT = 8>
 struct Acc {
-    f32x4 o[8][NT];  // O^T tiles: lane (r,c) holds row 16n+r, dims 32c + 8i + t at o[t][n][i]
+    f32x4 o[DT][NT];  // O^T tiles of 16 dims (the kernels state which dims each lane holds)
     float m[NT];     // exponent reference: raw score (FAST) or log2 units (GENERIC, merged)
     float l[NT];     // this lane's share of the row sum until the end of the tile loop
 };
 
-template <int NT>
-__device__ __forceinline__ void acc_clear(Acc<NT>& acc) {
+template <int NT, int DT>
+__device__ __forceinline__ void acc_clear(Acc<NT, DT>& acc) {
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
         acc.m[n] = neg_inf();
         acc.l[n] = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) acc.o[t][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < DT; ++t) acc.o[t][n] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 }
 
@@ -135,38 +136,38 @@ __device__ __forceinline__ void merge_row(float& m, float& l, f32x4* o, float m2
     for (int t = 0; t < K; ++t) o[t] = o[t] * a1 + o2[t] * a2;
 }
 
-template <int NT, int NS>
-__device__ __forceinline__ void acc_to_lds(MergeBuf<NT, NS>& mg, int slot, const Acc<NT>& acc, int lane) {
+template <int NT, int NS, int DT>
+__device__ __forceinline__ void acc_to_lds(MergeBuf<NT, NS, DT>& mg, int slot, const Acc<NT, DT>& acc, int lane) {
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) mg.o[slot][(n * 8 + t) * 64 + lane] = acc.o[t][n];
+        for (int t = 0; t < DT; ++t) mg.o[slot][(n * DT + t) * 64 + lane] = acc.o[t][n];
         mg.m[slot][n * 64 + lane] = acc.m[n];
         mg.l[slot][n * 64 + lane] = acc.l[n];
     }
 }
 
-template <int NT, int NS>
-__device__ __forceinline__ void acc_merge_lds(const MergeBuf<NT, NS>& mg, int slot, Acc<NT>& acc, int lane) {
+template <int NT, int NS, int DT>
+__device__ __forceinline__ void acc_merge_lds(const MergeBuf<NT, NS, DT>& mg, int slot, Acc<NT, DT>& acc, int lane) {
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-        f32x4 o[8], o2[8];
+        f32x4 o[DT], o2[DT];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < DT; ++t) {
             o[t] = acc.o[t][n];
-            o2[t] = mg.o[slot][(n * 8 + t) * 64 + lane];
+            o2[t] = mg.o[slot][(n * DT + t) * 64 + lane];
         }
-        merge_row<8>(acc.m[n], acc.l[n], o, mg.m[slot][n * 64 + lane], mg.l[slot][n * 64 + lane], o2);
+        merge_row<DT>(acc.m[n], acc.l[n], o, mg.m[slot][n * 64 + lane], mg.l[slot][n * 64 + lane], o2);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) acc.o[t][n] = o[t];
+        for (int t = 0; t < DT; ++t) acc.o[t][n] = o[t];
     }
 }
 
 // Merges the tile lanes of each row group into tile lane 0: with four lanes (2,3) -> (0,1)
 // then 1 -> 0, with two lanes 1 -> 0, with one lane nothing.  Every wave must call it.
 // Returns whether this wave owns its rows afterwards.
-template <int NTW, int TL, int NS>
-__device__ __forceinline__ bool merge_lanes(MergeBuf<NTW, NS>& mg, Acc<NTW>& acc, int rg, int tl, int lane) {
+template <int NTW, int TL, int NS, int DT>
+__device__ __forceinline__ bool merge_lanes(MergeBuf<NTW, NS, DT>& mg, Acc<NTW, DT>& acc, int rg, int tl, int lane) {
     constexpr int H = TL / 2;  // merge slots per row group
     static_assert(TL == 1 || TL == 2 || TL == 4, "tile lanes");
     if (TL == 1) return true;
@@ -637,16 +638,19 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 }
 
 // ---------------------------------------------------------------------------------------
-// f16 KV, 49..96 rows per GQA group: 32-cell steps.
+// f16 KV, 49..96 rows per GQA group (128-dim heads), and every row count of 256-dim heads
+// (up to 64 rows per launch): 32-cell steps.
 //
-// Same split as the kernel above.  A work-group holds WideShape::lanes piece lanes of two
-// waves each: the two waves of a lane are its two row groups (NTW row tiles each), read the
-// same staged steps and each stage half of every step (row group 0 the K rows, row group 1
-// the V rows); the lanes take the piece's steps round robin, and the whole group meets at
-// one barrier per step.  The lanes' (m, l, O) are merged in LDS at the end of the piece.
-// One work-group per CU, so each wave has a SIMD and up to 512 registers to itself: a
-// three-slot ring per lane keeps two steps in flight while one is computed, and a step
-// reads all its K and V^T operands from LDS before its first MFMA needs them.
+// Same split as the kernel above.  A work-group holds WideShape::lanes piece lanes of RS
+// waves each: the waves of a lane are its row groups (NTW row tiles each) and read the same
+// staged steps; with two row groups each stages half of every step (row group 0 the K rows,
+// row group 1 the V rows), with one it stages both.  The lanes take the piece's steps round
+// robin, and the whole group meets at one barrier per step.  The lanes' (m, l, O) are merged
+// in LDS at the end of the piece.  One work-group per CU, so each wave has a SIMD and up to
+// 512 registers to itself.  For 128-dim heads a three-slot ring per lane keeps two steps in
+// flight while one is computed, and a step reads all its K and V^T operands from LDS before
+// its first MFMA needs them; 256-dim heads (32 KB steps) use two-slot rings and read the
+// operands as the MFMAs go.
 // A step covers 32 cells:
 //   * O^T += V^T P^T runs on v_mfma_f32_16x16x32_f16 (the 16x16x16 form issues at half
 //     that rate on gfx950), and each row maximum and Q^T operand covers twice the cells;
@@ -660,18 +664,27 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 //   * Q^T stays in registers for the whole piece.
 // O layout: lane (r, c) holds row 16n + r, dims 16t + 4c + i at o[t][n][i].
 constexpr int kWide = kDecodeTileWide;  // 32 cells
-constexpr int kWideSlot = 16384;        // K, then V: 32 cell rows of 256 B each, chunk-swizzled
-struct WideShape { static constexpr int lanes = 2, slots = 3, groups_per_cu = 1; };
+// Per head dim D: a step's K then V, 32 cell rows of ROW = 2D bytes each (chunk-swizzled);
+// KS k-steps of 32 dims, DT output tiles of 16 dims; CPL cells per 1 KB LDS-DMA load.
+template <int D>
+struct WideDim {
+    static constexpr int ROW = 2 * D, KS = D / 32, DT = D / 16, CPL = 1024 / ROW, CPR = ROW / 16;
+    static constexpr int HALF = 16 * ROW;     // bytes of 16 cells (one S^T half)
+    static constexpr int SLOT = 2 * 32 * ROW;  // K + V of one step
+    static constexpr int LOADS = 32 * ROW / 1024;  // LDS-DMA loads per wave per step (K or V)
+    static constexpr int SLOTS = D == 128 ? 3 : 2;  // ring depth (LDS: 2 lanes x SLOTS x SLOT)
+};
+struct WideShape { static constexpr int lanes = 2, groups_per_cu = 1; };
 struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
 constexpr WideSplit kWide64 = {2, 2};         // 64 rows
 constexpr WideSplit kWide96 = {3, 2};         // 96 rows
 
 // RS row groups (waves per lane) of NTW row tiles each.
-template <int NTW, int RS>
+template <int NTW, int RS, int D>
 struct alignas(256) WideLds {
     union {
-        u32x4 ring[WideShape::lanes * WideShape::slots * kWideSlot / 16];
-        MergeBuf<NTW, RS * WideShape::lanes / 2> mg;  // reused after the step loop
+        u32x4 ring[WideShape::lanes * WideDim<D>::SLOTS * WideDim<D>::SLOT / 16];
+        MergeBuf<NTW, RS * WideShape::lanes / 2, WideDim<D>::DT> mg;  // reused after the step loop
     };
     StreamTable st;
 };
@@ -680,9 +693,9 @@ struct alignas(256) WideLds {
 // at dims 32ks + 8c .. +7 as f16 (rows >= R are zero).  All loads are issued before any is
 // used -- padding rows read row 0, which every piece has -- so the piece start pays one
 // memory latency, not one per operand.
-template <int NT>
+template <int NT, int KS>
 __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, int R, int n0, int lane,
-                                                f16x8 (&qv)[NT][4]) {
+                                                f16x8 (&qv)[NT][KS]) {
     const int r = lane & 15, c = lane >> 4;
     const char* src[NT];
     bool valid[NT];
@@ -695,28 +708,28 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
                  (int64_t)s * a.q_nb3 + (int64_t)(8 * c) * a.q_es;
     }
     if (a.q_f16) {
-        u32x4 raw[NT][4];
+        u32x4 raw[NT][KS];
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) raw[n][ks] = ld16(src[n] + 64 * ks);
+            for (int ks = 0; ks < KS; ++ks) raw[n][ks] = ld16(src[n] + 64 * ks);
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) qv[n][ks] = valid[n] ? as_f16x8(raw[n][ks]) : f16x8{};
+            for (int ks = 0; ks < KS; ++ks) qv[n][ks] = valid[n] ? as_f16x8(raw[n][ks]) : f16x8{};
     } else {
-        f32x4 raw[NT][4][2];
+        f32x4 raw[NT][KS][2];
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
+            for (int ks = 0; ks < KS; ++ks) {
                 raw[n][ks][0] = *reinterpret_cast<const f32x4*>(src[n] + 128 * ks);
                 raw[n][ks][1] = *reinterpret_cast<const f32x4*>(src[n] + 128 * ks + 16);
             }
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
+            for (int ks = 0; ks < KS; ++ks) {
                 f16x8 hv;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -728,38 +741,48 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
     }
 }
 
-template <int NT, int MODE, bool MASKED>
-__device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u32x4* kslot, uint32_t vlane,
-                                          const uint32_t (&kofs)[4], const f16x8 (&qv)[NT][4], int c0,
+template <int NT, int MODE, bool MASKED, int D>
+__device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT, WideDim<D>::DT>& acc, const u32x4* kslot,
+                                          uint32_t vlane, const uint32_t (&kofs)[WideDim<D>::KS],
+                                          const f16x8 (&qv)[NT][WideDim<D>::KS], int c0,
                                           const RowInfo<NT>& ri, const char* mrow, int nc, int lane) {
     const int c = lane >> 4;
 
     // ---- S^T halves: lane (r, c) receives cells 16h + 4c + i of row r ----
-    f16x8 kop[2][4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            kop[h][ks] = as_f16x8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kslot) + kofs[ks] +
-                                                                  4096 * h));
-    // V^T operands (vlane ^ 32t: chunk t of the lane's row), read now so that their latency
-    // hides under the scores and the softmax
-    u32x4 vt[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    using W = WideDim<D>;
+    // 128-dim heads read all K and V^T operands of the step before the first MFMA (their
+    // latency hides under the scores and the softmax); 256-dim heads have no registers for it
+    constexpr bool PF = D == 128;
+    auto kread = [&](int h, int ks) {
+        return as_f16x8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kslot) + kofs[ks] + W::HALF * h));
+    };
+    // V^T operand t (vlane ^ 32t: chunk t of the lane's row; the next 16 cells one half on)
+    auto vread = [&](int t) -> u32x4 {
         const lds_char* vp = lds_ptr(vlane ^ (32u * t));
         const u32x2 lo = ld_tr16(vp);
-        const u32x2 hi = ld_tr16(vp + 4096);
-        vt[t] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        const u32x2 hi = ld_tr16(vp + W::HALF);
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
+    f16x8 kop[2][W::KS];
+    u32x4 vt[W::DT];
+    if constexpr (PF) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int ks = 0; ks < W::KS; ++ks) kop[h][ks] = kread(h, ks);
+#pragma unroll
+        for (int t = 0; t < W::DT; ++t) vt[t] = vread(t);
     }
     f32x4 st[2][NT];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 0; ks < W::KS; ++ks) {
+            const f16x8 kk = PF ? kop[h][ks] : kread(h, ks);
 #pragma unroll
             for (int n = 0; n < NT; ++n)
-                st[h][n] = mfma16x16x32(kop[h][ks], qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
+                st[h][n] = mfma16x16x32(kk, qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
+        }
 
     // ---- scores (FAST: raw dot products; GENERIC: log2-domain logits) and row maxima ----
     const float c2 = a.scale_log2;
@@ -814,7 +837,7 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u
             }
             acc.l[n] *= alpha;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) acc.o[t][n] *= alpha;
+            for (int t = 0; t < W::DT; ++t) acc.o[t][n] *= alpha;
         }
     }
 
@@ -847,20 +870,21 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT>& acc, const u
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int t = 0; t < W::DT; ++t) {
+        const u32x4 vv = PF ? vt[t] : vread(t);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
             if (MODE == MODE_GENERIC && a.mask)
-                acc.o[t][n] = mfma16x16x32(as_f16x8(vt[t] & keep[n]), pt[n], acc.o[t][n]);
+                acc.o[t][n] = mfma16x16x32(as_f16x8(vv & keep[n]), pt[n], acc.o[t][n]);
             else
-                acc.o[t][n] = mfma16x16x32(as_f16x8(vt[t]), pt[n], acc.o[t][n]);
+                acc.o[t][n] = mfma16x16x32(as_f16x8(vv), pt[n], acc.o[t][n]);
         }
     }
 }
 
 // Normalised rows (O layout of the 32-cell kernel).
-template <int NT>
-__device__ __forceinline__ void write_rows_wide(const FaArgs& a, const Acc<NT>& acc, int n0, int s, int g, int R,
+template <int NT, int DT>
+__device__ __forceinline__ void write_rows_wide(const FaArgs& a, const Acc<NT, DT>& acc, int n0, int s, int g, int R,
                                                 int lane) {
     const int r = lane & 15, c = lane >> 4;
 #pragma unroll
@@ -872,40 +896,43 @@ __device__ __forceinline__ void write_rows_wide(const FaArgs& a, const Acc<NT>& 
         const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
         char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + c * 16;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) st16(dst + t * 64, acc.o[t][n] * inv);
+        for (int t = 0; t < DT; ++t) st16(dst + t * 64, acc.o[t][n] * inv);
     }
 }
 
 // Partial slot (same format as write_partial) from the 32-cell kernel's O layout.
-template <int NT>
-__device__ __forceinline__ void write_partial_wide(float* slot, int rows_slot, int n0, int R, const Acc<NT>& acc,
+template <int NT, int DT>
+__device__ __forceinline__ void write_partial_wide(float* slot, int rows_slot, int n0, int R, const Acc<NT, DT>& acc,
                                                    int lane) {
+    constexpr int D = 16 * DT;
     const int r = lane & 15, c = lane >> 4;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
         const int row = 16 * (n0 + n) + r;
         if (row >= R) continue;
         const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
-        char* dst = reinterpret_cast<char*>(slot) + (int64_t)row * 256 + c * 8;  // dims 16t + 4c .. +3
+        char* dst = reinterpret_cast<char*>(slot) + (int64_t)row * (2 * D) + c * 8;  // dims 16t + 4c .. +3
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < DT; ++t) {
             const f16x4 h = {(_Float16)(acc.o[t][n][0] * inv), (_Float16)(acc.o[t][n][1] * inv),
                              (_Float16)(acc.o[t][n][2] * inv), (_Float16)(acc.o[t][n][3] * inv)};
             *reinterpret_cast<u32x2*>(dst + t * 32) = __builtin_bit_cast(u32x2, h);
         }
         if (c == 0) {
-            slot[(int64_t)rows_slot * 64 + row] = acc.m[n];
-            slot[(int64_t)rows_slot * 65 + row] = acc.l[n];
+            slot[(int64_t)rows_slot * (D / 2) + row] = acc.m[n];
+            slot[(int64_t)rows_slot * (D / 2 + 1) + row] = acc.l[n];
         }
     }
 }
 
 // One piece of the 32-cell kernel: steps [tb, te) of segment (s, g).
-template <int NTW, int RS, int MODE>
-__device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, RS>& sh, int causal, const Piece& pc) {
+template <int NTW, int RS, int MODE, int D>
+__device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, RS, D>& sh, int causal,
+                                                  const Piece& pc) {
+    using W = WideDim<D>;
     constexpr int TL = WideShape::lanes;
-    constexpr int NS = WideShape::slots;
-    constexpr int SLOT16 = kWideSlot / 16;
+    constexpr int NS = W::SLOTS;
+    constexpr int SLOT16 = W::SLOT / 16;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -921,8 +948,8 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     const int n0 = rg * NTW;
 
     // ---- Q^T operands in registers: row 16(n0+n) + r, dims 32ks + 8c .. +7 ----
-    f16x8 qv[NTW][4];
-    load_q_operands<NTW>(a, s, g, R, n0, lane, qv);
+    f16x8 qv[NTW][W::KS];
+    load_q_operands<NTW, W::KS>(a, s, g, R, n0, lane, qv);
 
     RowInfo<NTW> ri;
 #pragma unroll
@@ -939,34 +966,30 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     const char* mrow = nullptr;
     if (MODE == MODE_GENERIC && a.mask) mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3;
 
-    Acc<NTW> acc;
+    Acc<NTW, W::DT> acc;
     acc_clear(acc);
 
     // cells >= nc read as zeros through the range-checked resources (and are masked)
     const buf_rsrc krs = make_rsrc_uniform(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
-                                           (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + 256));
+                                           (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + W::ROW));
     const buf_rsrc vrs = make_rsrc_uniform(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
-                                           (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + 256));
+                                           (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + W::ROW));
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
-    // LDS-DMA source offsets from a step's first cell; every load copies the 256-byte rows of
-    // four cells (whole cache lines).  K (row group 0), load u: lane t fills LDS row
-    // 4u + t/16 at 16-byte position t%16, which holds 16-byte chunk (t%16) ^ (row % 16)
+    // LDS-DMA source offsets from a step's first cell; every load copies the ROW-byte rows of
+    // CPL cells (1 KB, whole cache lines).  K (row group 0), load u: lane t fills LDS row
+    // CPL*u + t/CPR at 16-byte position t%CPR, which holds 16-byte chunk (t%CPR) ^ (row % 16)
     // (dims 8 * chunk); the A operand (h, ks) of lane (r, c) -- cell 16h + r, dims
-    // 32ks + 8c .. +7 -- then sits at 4096h + 256r + 16((4ks + c) ^ r), and the 16 lanes of a
-    // read hit 16 different chunk positions (conflict-free).  V (row group 1), load u: lane t
-    // fills LDS row 4u + t/16 at 16-byte position t%16, i.e. 32-byte chunk (t%16)/2 of that
-    // row, which holds dims 16 * (chunk ^ (row % 8)).
-    uint32_t kofs[4];
+    // 32ks + 8c .. +7 -- then sits at HALF*h + ROW*r + 16((4ks + c) ^ r), and the 16 lanes of
+    // a read hit 16 different chunk positions (conflict-free).  V (row group 1), load u: lane
+    // t fills LDS row CPL*u + t/CPR at 16-byte position t%CPR, i.e. 32-byte chunk (t%CPR)/2
+    // of that row, which holds dims 16 * (chunk ^ (row % 8)).
+    uint32_t kofs[W::KS];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kofs[ks] = 256u * r + 16u * (uint32_t)((4 * ks + c) ^ r);
-    uint32_t voff[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-        voff[u] = (uint32_t)(lane >> 4) * vnb + 32u * (((lane & 15) >> 1) ^ (4 * u + (lane >> 4))) + 16u * (lane & 1);
+    for (int ks = 0; ks < W::KS; ++ks) kofs[ks] = (uint32_t)W::ROW * r + 16u * (uint32_t)((4 * ks + c) ^ r);
     // transposed reads of a slot's V rows: lane (c, r) reads cell 4c + r/4 (+16h), dims
     // 16t + 4(r%4) .. +3, found in 32-byte chunk t ^ (cell % 8) of the row.  The row offset
-    // has bits 5..7 clear, so chunk t lies at (row + 32*(cell % 8) + 8(r%4)) ^ 32t.
-    const uint32_t vrow = (uint32_t)(4 * c + (r >> 2)) * 256u + 32u * (4 * (c & 1) + (r >> 2)) + 8u * (r & 3);
+    // has bits 5..8 clear, so chunk t lies at (row + 32*(cell % 8) + 8(r%4)) ^ 32t.
+    const uint32_t vrow = (uint32_t)(4 * c + (r >> 2)) * (uint32_t)W::ROW + 32u * (4 * (c & 1) + (r >> 2)) + 8u * (r & 3);
 
     // steps of this lane: tb + tl + TL*i, i < n_my; n_iter is the same for the whole group
     const int t0 = tb + tl;
@@ -977,19 +1000,27 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
 
     auto issue = [&](int i, int slot) {
         const uint32_t c0 = (uint32_t)(t0 + i * TL) * kWide;
-        const uint32_t base = ring_base + (uint32_t)slot * kWideSlot;
-        uint32_t o8[8];
-        if (rg == 0) {
+        const uint32_t base = ring_base + (uint32_t)slot * W::SLOT;
+        const uint32_t pos = (uint32_t)lane % W::CPR;  // 16-byte position in the row
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t cell = 4u * u + (uint32_t)(lane >> 4);
-                o8[u] = (c0 + cell) * knb + 16u * (((uint32_t)lane & 15u) ^ (cell & 15u));
+        for (int b8 = 0; b8 < W::LOADS / 8; ++b8) {
+            uint32_t o8[8];
+            if (rg == 0) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t cell = W::CPL * (8 * b8 + u) + (uint32_t)lane / W::CPR;
+                    o8[u] = (c0 + cell) * knb + 16u * (pos ^ (cell & 15u));
+                }
+                dma16x8_to_lds(krs, o8, base + 8192u * b8);
             }
-            dma16x8_to_lds(krs, o8, base);
-        } else if (rg == 1) {
+            if (rg == (RS == 1 ? 0 : 1)) {  // one row group stages both halves
 #pragma unroll
-            for (int u = 0; u < 8; ++u) o8[u] = (c0 + 4 * u) * vnb + voff[u & 1];
-            dma16x8_to_lds(vrs, o8, base + 8192);
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t cell = W::CPL * (8 * b8 + u) + (uint32_t)lane / W::CPR;
+                    o8[u] = (c0 + cell) * vnb + 32u * ((pos >> 1) ^ (cell & 7u)) + 16u * (pos & 1u);
+                }
+                dma16x8_to_lds(vrs, o8, base + 32 * W::ROW + 8192u * b8);
+            }
         }
     };
     // Step i reads slot i % NS.  After the barrier of step i every wave has left step i-1, so
@@ -1000,10 +1031,12 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
 #pragma unroll
     for (int q = 0; q < NS - 1; ++q)
         if (q < n_my) issue(q, q);
+    // loads one issue puts in flight for each wave (the wave of a single row group stages K and V)
+    constexpr int LPW = (RS == 1 ? 2 : 1) * W::LOADS;
     auto step = [&](int i, auto masked) {
-        const int later = min(max(n_my - 1 - i, 0), NS - 2);  // batches issued after step i's
-        if (later >= 2) wait_vmcnt<16>();
-        else if (later == 1) wait_vmcnt<8>();
+        const int later = min(max(n_my - 1 - i, 0), NS - 2);  // steps issued after step i
+        if (later >= 2) wait_vmcnt<2 * LPW>();
+        else if (later == 1) wait_vmcnt<LPW>();
         else wait_vmcnt<0>();
         __syncthreads();
         if (i + NS - 1 < n_my) issue(i + NS - 1, (i + NS - 1) % NS);
@@ -1012,9 +1045,9 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             const int sl = i % NS;
             const u32x4* kslot = ring + sl * SLOT16;
             // the V area is 256-byte aligned, so ^ 32t only moves bits 5..7 of vrow
-            const uint32_t vlane = ring_base + sl * kWideSlot + 8192 + vrow;
-            wide_step<NTW, MODE, decltype(masked)::value>(a, acc, kslot, vlane, kofs, qv, t * kWide, ri, mrow, sd.nc,
-                                                          lane);
+            const uint32_t vlane = ring_base + sl * W::SLOT + 32 * W::ROW + vrow;
+            wide_step<NTW, MODE, decltype(masked)::value, D>(a, acc, kslot, vlane, kofs, qv, t * kWide, ri, mrow,
+                                                             sd.nc, lane);
         }
     };
     // Steps that every lane has and that lie below t_full for every lane run unmasked in a
@@ -1118,30 +1151,32 @@ decode_d128(FaArgs a, int causal) {
     for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, KV, MODE>(a, sh, causal, pc); });
 }
 
-template <int NTW, int RS, int MODE>
-__global__ __launch_bounds__((RS * WideShape::lanes * 64), (RS * WideShape::lanes * WideShape::groups_per_cu / 4)) void
-decode_wide_d128(FaArgs a, int causal) {
-    __shared__ WideLds<NTW, RS> sh;
+template <int NTW, int RS, int MODE, int D>
+__global__ __launch_bounds__((RS * WideShape::lanes * 64), (RS * WideShape::lanes * WideShape::groups_per_cu + 3) / 4)
+void decode_wide(FaArgs a, int causal) {
+    __shared__ WideLds<NTW, RS, D> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
-    for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE>(a, sh, causal, pc); });
+    for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
 }
 
 // Combines the pieces of every segment that more than one work-group touched, in the order
 // of the work-groups.  grid = (S*Hkv segments, row blocks of 8); 256 threads = 8 rows x 32
 // four-dim chunks, so every (row, chunk) is one thread.  The split kernel recorded the
 // segment's first and last piece; the stream extents come in the same round trip.
+template <int D>
 __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
+    constexpr int TPR = D / 4;  // threads per row (4 dims each)
     const int64_t k = blockIdx.x;
     const int s = (int)(k / a.Hkv);
     const int g = (int)(k % a.Hkv);
     const StreamDims sd = stream_dims(a, s);
     const int p_first = a.seg_pieces[2 * k], p_last = a.seg_pieces[2 * k + 1];
-    const int row = blockIdx.y * 8 + (threadIdx.x >> 5);
+    const int row = blockIdx.y * (256 / TPR) + (int)(threadIdx.x / TPR);
     if (row >= a.Gr * sd.ql) return;  // (a segment without rows has stale entries)
     if (p_first == p_last) return;    // written whole by its only work-group
 
-    const int d0 = (threadIdx.x & 31) * 4;
+    const int d0 = (int)(threadIdx.x % TPR) * 4;
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
@@ -1155,9 +1190,9 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
         for (int u = 0; u < 8; ++u) {
             const int p = p0 + u <= p_last ? p0 + u : p_last;
             const float* sl = base + (int64_t)p * a.slot_floats;
-            hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * 256 + d0 * 2);
-            mv[u] = sl[(int64_t)rows_slot * 64 + row];
-            lv[u] = sl[(int64_t)rows_slot * 65 + row];
+            hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * (2 * D) + d0 * 2);
+            mv[u] = sl[(int64_t)rows_slot * (D / 2) + row];
+            lv[u] = sl[(int64_t)rows_slot * (D / 2 + 1) + row];
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -1172,18 +1207,19 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
 }
 
-template <int NTW, int RS>
+template <int NTW, int RS, int D>
 hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
     const dim3 grid(a.P), block(RS * WideShape::lanes * 64);
     if (generic)
-        hipLaunchKernelGGL((decode_wide_d128<NTW, RS, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_GENERIC, D>), grid, block, 0, stream, a, causal);
     else
-        hipLaunchKernelGGL((decode_wide_d128<NTW, RS, MODE_FAST>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_FAST, D>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int rows_slot = NTW * RS * 16;
-    hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
-                       a, rows_slot);
+    const int rows_wg = 256 / (D / 4);
+    hipLaunchKernelGGL(decode_merge<D>, dim3((unsigned)(a.S * a.Hkv), (unsigned)((rows_slot + rows_wg - 1) / rows_wg)),
+                       dim3(256), 0, stream, a, rows_slot);
     return hipGetLastError();
 }
 
@@ -1197,7 +1233,7 @@ hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stre
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int rows_slot = NTW * 16;
-    hipLaunchKernelGGL(decode_merge, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(decode_merge<128>, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
                        a, rows_slot);
     return hipGetLastError();
 }
@@ -1206,7 +1242,7 @@ hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stre
 
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
     const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + a.tile_cells - 1) / a.tile_cells + a.seg_cost);
-    const int per_cu = row_tiles <= 3 ? Shape<SIXI_TYPE_F16>::groups_per_cu : WideShape::groups_per_cu;
+    const int per_cu = a.tile_cells == kDecodeTile ? Shape<SIXI_TYPE_F16>::groups_per_cu : WideShape::groups_per_cu;
     int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
     if (P > kMaxSplitGroups) P = kMaxSplitGroups;
     if (P > tiles_max) P = tiles_max;
@@ -1219,16 +1255,29 @@ int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
 
 hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream) {
-    if (head_dim != 128) return hipErrorNotSupported;
     const bool generic = mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f;
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
+    if (head_dim == 256) {
+        // 256-dim heads: every row count runs the 32-cell kernel (one or two row groups)
+        if (kv_type != SIXI_TYPE_F16) return hipErrorNotSupported;
+        // at most two row tiles per wave (three spill the 256-dim accumulators) and two row groups
+        // (a third would put two waves on a SIMD): up to 64 rows per launch
+        switch (row_tiles) {
+            case 1: return launch_wide<1, 1, 256>(a, generic, causal, stream);
+            case 2: return launch_wide<2, 1, 256>(a, generic, causal, stream);
+            case 3:
+            case 4: return launch_wide<2, 2, 256>(a, generic, causal, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
+    if (head_dim != 128) return hipErrorNotSupported;
     if (kv_type == SIXI_TYPE_F16) {
         switch (row_tiles) {
             case 1: return launch_nt<1, SIXI_TYPE_F16>(a, generic, causal, stream);
             case 2: return launch_nt<2, SIXI_TYPE_F16>(a, generic, causal, stream);
             case 3: return launch_nt<3, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 4: return launch_wide<kWide64.ntw, kWide64.rs>(a, generic, causal, stream);
-            case 6: return launch_wide<kWide96.ntw, kWide96.rs>(a, generic, causal, stream);
+            case 4: return launch_wide<kWide64.ntw, kWide64.rs, 128>(a, generic, causal, stream);
+            case 6: return launch_wide<kWide96.ntw, kWide96.rs, 128>(a, generic, causal, stream);
             default: return hipErrorNotSupported;
         }
     }

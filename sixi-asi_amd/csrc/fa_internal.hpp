@@ -83,16 +83,20 @@ constexpr int kMaxStreams = 512;       // LDS prefix table bound
 constexpr int kMaxSplitGroups = 2048;  // work-groups of a split-K launch (workspace bound)
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles);
-// Cells per split tile of the decode launch for this KV type and row-tile count.
-inline int decode_tile_cells(int kv_type, int row_tiles) {
-    return (kv_type == SIXI_TYPE_F16 && row_tiles > 3) ? kDecodeTileWide : kDecodeTile;
+// Whether the 32-cell kernel runs this launch: f16 KV with more than 48 rows, or 256-dim heads.
+inline bool decode_wide_kernel(int kv_type, int row_tiles, int head_dim) {
+    return kv_type == SIXI_TYPE_F16 && (row_tiles > 3 || head_dim == 256);
+}
+// Cells per split tile of the decode launch.
+inline int decode_tile_cells(int kv_type, int row_tiles, int head_dim) {
+    return decode_wide_kernel(kv_type, row_tiles, head_dim) ? kDecodeTileWide : kDecodeTile;
 }
 // Fixed cost of starting a piece (loading Q, filling the ring, merging and writing the
 // rows), in tiles of the split: each segment weighs tiles + seg_cost, so a work-group whose
 // range enters a segment gets that many tiles less.
 constexpr int kWideSegCost = 12;
-inline int decode_seg_cost(int kv_type, int row_tiles) {
-    return (kv_type == SIXI_TYPE_F16 && row_tiles > 3) ? kWideSegCost : 0;
+inline int decode_seg_cost(int kv_type, int row_tiles, int head_dim) {
+    return decode_wide_kernel(kv_type, row_tiles, head_dim) ? kWideSegCost : 0;
 }
 // Row tiles the decode kernel runs for `rows` = G * n_q rows: up to 3 per wave; beyond
 // that two row groups of equal size (so 5 tiles run as 6).
@@ -100,9 +104,9 @@ inline int decode_row_tiles(int64_t rows) {
     const int rt = (int)((rows + 15) / 16);
     return rt <= 3 ? rt : 2 * ((rt + 1) / 2);
 }
-inline int64_t decode_slot_floats(int row_tiles) {
-    // O/l rows [16*row_tiles][128] f16 (64 floats' worth), then m and l per row in f32
-    return (int64_t)row_tiles * 16 * (64 + 2);
+inline int64_t decode_slot_floats(int row_tiles, int head_dim) {
+    // O/l rows [16*row_tiles][head_dim] f16 (head_dim/2 floats' worth), then m and l per row
+    return (int64_t)row_tiles * 16 * (head_dim / 2 + 2);
 }
 
 }  // namespace sixi

@@ -22,9 +22,11 @@ using sixi::FaArgs;
 using namespace sixi_abi;
 
 constexpr size_t kWsAlign = 256;
-constexpr int kMaxHeadDim = 128;       // head dims built for gfx950 in this library
+// head dims built for gfx950: 128 everywhere; 256 for f16 KV blocks of <= 96 rows per GQA group
+constexpr bool head_dim_built(int64_t D) { return D == 128 || D == 256; }
 constexpr int kSplitMaxRows = 16 * sixi::kDecodeMaxRowTiles;  // G * n_q of the split-K kernel
 constexpr int64_t kQ8MaxRows = 48;  // rows per kv-head group of one q8_0 split-K launch
+constexpr int64_t kD256MaxRows = 64;  // rows per kv-head group of one 256-dim split-K launch
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -79,7 +81,7 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     if (H % Hkv != 0) return SIXI_E_INVALID_ARGUMENT;
     if (o.ne[0] != D || o.ne[1] != H || o.ne[2] != n_q || o.ne[3] != S) return SIXI_E_INVALID_ARGUMENT;
     if (S > sixi::kMaxStreams || H > 4096 || n_q > (1 << 20) || n_kv > (1 << 26)) return SIXI_E_UNSUPPORTED;
-    if (D != kMaxHeadDim) return SIXI_E_UNSUPPORTED;
+    if (!head_dim_built(D)) return SIXI_E_UNSUPPORTED;
 
     // element strides and alignment
     const int qes = elem_bytes(q.type);
@@ -167,9 +169,17 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
+    // 256-dim heads: the 32-cell split-K kernel only (f16 KV, <= 96 rows per GQA group)
+    if (D == 256 && (!pl.splitk || k.type != SIXI_TYPE_F16)) return SIXI_E_UNSUPPORTED;
     // q8_0 KV runs the 16-cell split-K kernel, which holds up to 48 rows per kv-head group:
     // a larger group is covered in launches over disjoint head subsets (each reads the KV).
     pl.heads_per_launch = a.G;
+    if (D == 256 && rows > kD256MaxRows) {
+        // the 256-dim split-K kernel holds 64 rows: a larger group runs as launches over
+        // disjoint head subsets (each reads the KV)
+        if (n_q > kD256MaxRows) return SIXI_E_UNSUPPORTED;
+        pl.heads_per_launch = (int)(kD256MaxRows / n_q);
+    }
     if (k.type == SIXI_TYPE_Q8_0 && rows > kQ8MaxRows) {
         if (pl.splitk && n_q <= kQ8MaxRows) {
             pl.heads_per_launch = (int)(kQ8MaxRows / n_q);
@@ -192,7 +202,7 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     }
     if (pl.splitk) {
         pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q);
-        a.slot_floats = sixi::decode_slot_floats(pl.row_tiles);
+        a.slot_floats = sixi::decode_slot_floats(pl.row_tiles, pl.D);
         const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
         // partial slots, then (first, last) piece of every segment
         pl.seg_offset = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
@@ -255,8 +265,8 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     a.part = reinterpret_cast<float*>(ws);
     a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
     if (pl.splitk) {
-        a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles);
-        a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles);
+        a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles, pl.D);
+        a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles, pl.D);
         a.P = sixi::decode_num_groups(a, cu_count_cached(), pl.row_tiles);
         a.xcd_remap = 0;
         e = hipSuccess;

@@ -149,6 +149,10 @@ def config(name: str) -> Workload:
     if name in ("long_q8_decode", "long_q8_verify"):
         ql = 1 if name.endswith("decode") else 8
         return Workload(name, SEED_BASE + 5, 8, [65536] * 8, [ql] * 8, kv_type=TYPE_Q8_0)
+    if name in ("decode_d256", "batched_verify_d256"):
+        # the real model's 256-dim heads (configs/qwen3.8-27b-ud-q4-k-xl.sixi: key/value length 256)
+        w = config(name[:-5])
+        return dataclasses.replace(w, name=name, seed=SEED_BASE + 6, D=256)
     raise KeyError(name)
 
 

@@ -1,0 +1,86 @@
+"""256-dim heads (the real model's key/value length, configs/qwen3.8-27b-ud-q4-k-xl.sixi) on the
+32-cell split-K kernel, against the oracle through the C ABI: decode, speculative verify (96 rows
+per group run as two head-subset launches of at most 64 rows), ragged streams, an explicit mask
+and f16 Q.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import sixi_attn as sa
+from sixi_attn import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-3
+REL_L2 = 1e-3
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", file=sys.stderr, flush=True)
+
+
+@pytest.fixture(scope="module")
+def fa():
+    assert torch.cuda.is_available(), "the gpu tests need a GPU"
+    sa.load_library()
+    return sa.FlashAttnExt()
+
+
+def _run_check(fa, w, label, mask_mode=sa.MASK_BLOCK_CAUSAL, explicit=False):
+    host = wl.make_host(w, poison=not explicit)
+    dev = wl.to_device(host)
+    out = torch.full((w.S, w.n_q, w.H, w.D), float("nan"), dtype=torch.float32, device="cuda")
+    mask = None
+    if explicit:
+        m = oracle.build_kq_mask(dev["k"].shape[1], w.n_q, host["kv_len"], host["q_len"])
+        mask = torch.from_numpy(m.view(np.float16)).cuda()
+        mask_mode = sa.MASK_EXPLICIT
+    _say(f"{label}: S={w.S} kv_len={w.kv_len} q_len={w.q_len} H={w.H} Hkv={w.Hkv} D={w.D}")
+    fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=mask_mode, mask=mask)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = oracle.attention_for_workload(host, w.kv_type)
+    ql = host["q_len"]
+    g = np.concatenate([got[s, :ql[s]].ravel() for s in range(w.S)])
+    r = np.concatenate([want[s, :ql[s]].ravel() for s in range(w.S)])
+    m = oracle.diff_metrics(r, g)
+    _say(f"{label}: max_abs={m['max_abs']:.3e} rel_l2={m['rel_l2']:.3e}")
+    assert np.all(np.isfinite(g))
+    assert m["max_abs"] <= MAX_ABS and m["rel_l2"] <= REL_L2, m
+
+
+@pytest.mark.parametrize("label,kv_len,q_len,H,Hkv", [
+    ("decode", [4096], [1], 24, 4),                       # 6 rows per group
+    ("decode ragged", [700, 3000, 5], [1, 1, 1], 24, 4),
+    ("verify", [2000, 8192], [16, 16], 24, 4),            # 96 rows: two launches of 64 and 32 rows
+    ("verify ragged", [1500, 300, 900], [16, 3, 9], 24, 4),
+    ("32 rows", [1200], [8], 16, 4),
+    ("64 rows, one launch", [999], [8], 32, 4),
+    ("MHA", [1000, 64], [16, 5], 4, 4),                    # G = 1
+])
+def test_d256_against_oracle(fa, label, kv_len, q_len, H, Hkv):
+    w = wl.Workload("d256", 0x51A7_9100 + sum(kv_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv, D=256)
+    _run_check(fa, w, label)
+
+
+def test_d256_explicit_mask(fa):
+    w = wl.Workload("d256 mask", 0x51A7_9200, 2, [600, 77], [16, 4], D=256)
+    _run_check(fa, w, "explicit mask", explicit=True)
+
+
+def test_d256_f16_q(fa):
+    w = wl.Workload("d256 f16 q", 0x51A7_9300, 2, [1300, 50], [12, 1], D=256, q_type=sa.TYPE_F16)
+    _run_check(fa, w, "f16 Q")
+
+
+def test_d256_unsupported_forms_report_so(fa):
+    # prefill-sized blocks and q8_0 KV are not built for 256-dim heads
+    for kv_type, q_len in ((sa.TYPE_F16, 128), (sa.TYPE_Q8_0, 1)):
+        w = wl.Workload("d256 unsupported", 0x51A7_9400, 1, [300], [q_len], D=256, kv_type=kv_type)
+        dev = wl.to_device(wl.make_host(w))
+        out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+        rc = fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], check=False)
+        assert rc == sa.E_UNSUPPORTED, (kv_type, q_len, rc)
