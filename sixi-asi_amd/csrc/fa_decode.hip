@@ -641,7 +641,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 // f16 KV, 49..96 rows per GQA group (128-dim heads), and every row count of 256-dim heads
 // (up to 64 rows per launch): 32-cell steps.
 //
-// Same split as the kernel above.  A work-group holds WideShape::lanes piece lanes of RS
+// Same split as the kernel above.  A work-group holds wide_lanes() piece lanes of RS
 // waves each: the waves of a lane are its row groups (NTW row tiles each) and read the same
 // staged steps; with two row groups each stages half of every step (row group 0 the K rows,
 // row group 1 the V rows), with one it stages both.  The lanes take the piece's steps round
@@ -672,9 +672,13 @@ struct WideDim {
     static constexpr int HALF = 16 * ROW;     // bytes of 16 cells (one S^T half)
     static constexpr int SLOT = 2 * 32 * ROW;  // K + V of one step
     static constexpr int LOADS = 32 * ROW / 1024;  // LDS-DMA loads per wave per step (K or V)
-    static constexpr int SLOTS = D == 128 ? 3 : 2;  // ring depth (LDS: 2 lanes x SLOTS x SLOT)
 };
-struct WideShape { static constexpr int lanes = 2, groups_per_cu = 1; };
+struct WideShape { static constexpr int groups_per_cu = 1; };
+// Piece lanes per work-group: two, except 96 rows of 256-dim heads (three row groups of 32
+// rows), which run one lane so that each wave keeps a SIMD and 512 registers.
+template <int RS, int D> constexpr int wide_lanes() { return (D == 256 && RS == 3) ? 1 : 2; }
+// Ring depth per lane (LDS: lanes x slots x SLOT): two steps in flight where it fits.
+template <int D, int TL> constexpr int wide_slots() { return (D == 128 || TL == 1) ? 3 : 2; }
 struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
 constexpr WideSplit kWide64 = {2, 2};         // 64 rows
 constexpr WideSplit kWide96 = {3, 2};         // 96 rows
@@ -683,8 +687,8 @@ constexpr WideSplit kWide96 = {3, 2};         // 96 rows
 template <int NTW, int RS, int D>
 struct alignas(256) WideLds {
     union {
-        u32x4 ring[WideShape::lanes * WideDim<D>::SLOTS * WideDim<D>::SLOT / 16];
-        MergeBuf<NTW, RS * WideShape::lanes / 2, WideDim<D>::DT> mg;  // reused after the step loop
+        u32x4 ring[wide_lanes<RS, D>() * wide_slots<D, wide_lanes<RS, D>()>() * WideDim<D>::SLOT / 16];
+        MergeBuf<NTW, (RS * wide_lanes<RS, D>() + 1) / 2, WideDim<D>::DT> mg;  // reused after the step loop
     };
     StreamTable st;
 };
@@ -930,8 +934,8 @@ template <int NTW, int RS, int MODE, int D>
 __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, RS, D>& sh, int causal,
                                                   const Piece& pc) {
     using W = WideDim<D>;
-    constexpr int TL = WideShape::lanes;
-    constexpr int NS = W::SLOTS;
+    constexpr int TL = wide_lanes<RS, D>();
+    constexpr int NS = wide_slots<D, TL>();
     constexpr int SLOT16 = W::SLOT / 16;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1152,7 +1156,7 @@ decode_d128(FaArgs a, int causal) {
 }
 
 template <int NTW, int RS, int MODE, int D>
-__global__ __launch_bounds__((RS * WideShape::lanes * 64), (RS * WideShape::lanes * WideShape::groups_per_cu + 3) / 4)
+__global__ __launch_bounds__((RS * wide_lanes<RS, D>() * 64), (RS * wide_lanes<RS, D>() * WideShape::groups_per_cu + 3) / 4)
 void decode_wide(FaArgs a, int causal) {
     __shared__ WideLds<NTW, RS, D> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
@@ -1209,7 +1213,7 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
 
 template <int NTW, int RS, int D>
 hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
-    const dim3 grid(a.P), block(RS * WideShape::lanes * 64);
+    const dim3 grid(a.P), block(RS * wide_lanes<RS, D>() * 64);
     if (generic)
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_GENERIC, D>), grid, block, 0, stream, a, causal);
     else
@@ -1260,13 +1264,14 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
     if (head_dim == 256) {
         // 256-dim heads: every row count runs the 32-cell kernel (one or two row groups)
         if (kv_type != SIXI_TYPE_F16) return hipErrorNotSupported;
-        // at most two row tiles per wave (three spill the 256-dim accumulators) and two row groups
-        // (a third would put two waves on a SIMD): up to 64 rows per launch
+        // at most two row tiles per wave (three spill the 256-dim accumulators); 96 rows run as
+        // three row groups of one lane
         switch (row_tiles) {
             case 1: return launch_wide<1, 1, 256>(a, generic, causal, stream);
             case 2: return launch_wide<2, 1, 256>(a, generic, causal, stream);
             case 3:
             case 4: return launch_wide<2, 2, 256>(a, generic, causal, stream);
+            case 6: return launch_wide<2, 3, 256>(a, generic, causal, stream);
             default: return hipErrorNotSupported;
         }
     }

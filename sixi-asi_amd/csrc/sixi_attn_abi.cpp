@@ -26,7 +26,6 @@ constexpr size_t kWsAlign = 256;
 constexpr bool head_dim_built(int64_t D) { return D == 128 || D == 256; }
 constexpr int kSplitMaxRows = 16 * sixi::kDecodeMaxRowTiles;  // G * n_q of the split-K kernel
 constexpr int64_t kQ8MaxRows = 48;  // rows per kv-head group of one q8_0 split-K launch
-constexpr int64_t kD256MaxRows = 64;  // rows per kv-head group of one 256-dim split-K launch
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -174,12 +173,6 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     // q8_0 KV runs the 16-cell split-K kernel, which holds up to 48 rows per kv-head group:
     // a larger group is covered in launches over disjoint head subsets (each reads the KV).
     pl.heads_per_launch = a.G;
-    if (D == 256 && rows > kD256MaxRows) {
-        // the 256-dim split-K kernel holds 64 rows: a larger group runs as launches over
-        // disjoint head subsets (each reads the KV)
-        if (n_q > kD256MaxRows) return SIXI_E_UNSUPPORTED;
-        pl.heads_per_launch = (int)(kD256MaxRows / n_q);
-    }
     if (k.type == SIXI_TYPE_Q8_0 && rows > kQ8MaxRows) {
         if (pl.splitk && n_q <= kQ8MaxRows) {
             pl.heads_per_launch = (int)(kQ8MaxRows / n_q);

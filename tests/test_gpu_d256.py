@@ -1,7 +1,6 @@
 """256-dim heads (the real model's key/value length, configs/qwen3.8-27b-ud-q4-k-xl.sixi) on the
 32-cell split-K kernel, against the oracle through the C ABI: decode, speculative verify (96 rows
-per group run as two head-subset launches of at most 64 rows), ragged streams, an explicit mask
-and f16 Q.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
+per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
 import sys
 
 import numpy as np
@@ -55,7 +54,7 @@ def _run_check(fa, w, label, mask_mode=sa.MASK_BLOCK_CAUSAL, explicit=False):
 @pytest.mark.parametrize("label,kv_len,q_len,H,Hkv", [
     ("decode", [4096], [1], 24, 4),                       # 6 rows per group
     ("decode ragged", [700, 3000, 5], [1, 1, 1], 24, 4),
-    ("verify", [2000, 8192], [16, 16], 24, 4),            # 96 rows: two launches of 64 and 32 rows
+    ("verify", [2000, 8192], [16, 16], 24, 4),            # 96 rows: one lane of three row groups
     ("verify ragged", [1500, 300, 900], [16, 3, 9], 24, 4),
     ("32 rows", [1200], [8], 16, 4),
     ("64 rows, one launch", [999], [8], 32, 4),
