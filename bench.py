@@ -142,7 +142,7 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
-def time_prefill(fa, steps: int, warmup: int, kv_type=None):
+def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None):
     """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks).
     kv_type q8_0 runs the same chunks over a q8_0 cache (staged as f16 operands per call)."""
     import dataclasses
@@ -154,6 +154,8 @@ def time_prefill(fa, steps: int, warmup: int, kv_type=None):
         wp = wl.config(name)
         if kv_type is not None:
             wp = dataclasses.replace(wp, kv_type=kv_type)
+        if head_dim is not None:
+            wp = dataclasses.replace(wp, D=head_dim)
         dp = wl.to_device(wl.make_host(wp))
         msp, _ = time_calls(fa, wp, dp, steps, warmup)
         pre.append((wp, msp))
@@ -343,6 +345,9 @@ def main() -> int:
             tq, uq = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0)
             result["configs"]["prefill_q8_0"] = {"us_two_chunks": round(uq, 2), "TFLOPs": round(tq, 2)}
             _log(f"prefill q8_0 KV: {uq:.1f} us for 2 chunks, {tq:.1f} TFLOP/s")
+            td, ud = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), head_dim=256)
+            result["configs"]["prefill_d256"] = {"us_two_chunks": round(ud, 2), "TFLOPs": round(td, 2)}
+            _log(f"prefill 256-dim heads: {ud:.1f} us for 2 chunks, {td:.1f} TFLOP/s")
         except sa.SixiAttnError as e:
             result["prefill_tflops"] = None
             result["prefill_note"] = f"prefill kernel unavailable: {e}"

@@ -36,15 +36,23 @@ namespace {
 constexpr int kBM = 128;           // rows per work-group
 constexpr int kBN = 64;            // cells per KV tile
 constexpr int kThreads = 256;      // 4 waves x 32 rows
-constexpr int kKBytes = kBN * 256;              // 16 KB
-constexpr int kVBytes = kBN * 256;              // 16 KB
+// Per head dim D: ROW-byte rows, KS k-steps of 16 dims, DB output blocks of 32 dims; a tile of
+// K (or V) is kBN rows; LW 1 KB LDS-DMA loads per wave per tile; CPL cells per load.
+template <int D>
+struct PfDim {
+    static constexpr int ROW = 2 * D, KS = D / 16, DB = D / 32, CPR = ROW / 16, CPL = 1024 / ROW;
+    static constexpr int TILE = kBN * ROW;            // bytes of a K (or V) tile: 16 KB at 128 dims
+    static constexpr int LW = TILE / 1024 / 4;        // loads per wave per tile (4 waves)
+    static constexpr int GROUPS = D == 128 ? 2 : 1;   // work-groups per CU (LDS: 4 tiles each)
+};
 constexpr float kLazyLog2 = 8.0f;
 
 enum { MODE_FAST = 0, MODE_GENERIC = 1 };
 
+template <int D>
 struct PrefillLds {
-    u32x4 k[2][kKBytes / 16];
-    u32x4 v[2][kVBytes / 16];
+    u32x4 k[2][PfDim<D>::TILE / 16];
+    u32x4 v[2][PfDim<D>::TILE / 16];
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -54,9 +62,11 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int causal, int nrb, int n_cu) {
-    __shared__ PrefillLds sh;
+template <int MODE, int D>
+__global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs a, int causal, int nrb, int n_cu) {
+    using P = PfDim<D>;
+    constexpr int kKBytes = P::TILE, kVBytes = P::TILE;
+    __shared__ PrefillLds<D> sh;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -72,7 +82,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     const int b = blockIdx.x;
     const int N = gridDim.x;
     int rank = b;
-    if (N > n_cu && N <= 2 * n_cu) {
+    if (P::GROUPS == 2 && N > n_cu && N <= 2 * n_cu) {
         const int npair = N - n_cu;
         const int alone = n_cu - npair;
         if (b < npair) rank = alone + b;
@@ -98,24 +108,24 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
 
     // ---- Q^T B operands in registers: lane l -> row j, dims 16ks + 8*hl .. +7 ----
     // (every load issued before any is used; rows past the block read its first row)
-    f16x8 qop[8];
+    f16x8 qop[P::KS];
     {
         const char* src = a.q + (int64_t)(row_ok ? j : j0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3;
         if (a.q_f16) {
-            u32x4 raw[8];
+            u32x4 raw[P::KS];
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) raw[ks] = ld16(src + (16 * ks + 8 * hl) * 2);
+            for (int ks = 0; ks < P::KS; ++ks) raw[ks] = ld16(src + (16 * ks + 8 * hl) * 2);
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) qop[ks] = row_ok ? as_f16x8(raw[ks]) : f16x8{};
+            for (int ks = 0; ks < P::KS; ++ks) qop[ks] = row_ok ? as_f16x8(raw[ks]) : f16x8{};
         } else {
-            f32x4 lo[8], hi[8];
+            f32x4 lo[P::KS], hi[P::KS];
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
+            for (int ks = 0; ks < P::KS; ++ks) {
                 lo[ks] = *reinterpret_cast<const f32x4*>(src + (16 * ks + 8 * hl) * 4);
                 hi[ks] = *reinterpret_cast<const f32x4*>(src + (16 * ks + 8 * hl) * 4 + 16);
             }
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
+            for (int ks = 0; ks < P::KS; ++ks) {
                 f16x8 hv;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -129,7 +139,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
 
     // K/V of (stream, kv-head): every tile gets its own range-checked buffer resource whose
     // base is the tile's first cell, so cells >= nc read as zero and no load can fault
-    const int64_t rowb = 128 * 2;
+    const int64_t rowb = P::ROW;
     const char* kbase = a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2;
     const char* vbase = a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2;
     const int64_t kbytes = (int64_t)(sd.nc - 1) * a.k_nb1 + rowb;
@@ -141,51 +151,58 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
     const uint32_t lds0 = lds_addr(&sh);
     constexpr int kVBase = 2 * kKBytes;  // the V buffers follow the two K buffers
     // K A operand of (cb, ks): cell 32cb + rl, chunk (2ks + hl) stored at slot chunk ^ (rl & 15)
-    uint32_t koff[8];
+    uint32_t koff[P::KS];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) koff[ks] = rl * 256 + ((((2 * ks + hl) ^ (rl & 15)) & 15) << 4);
-    // K staging: wave w's load u4 fills cells 4(4w + u4) + l/16; lane fetches chunk (l%16)^cell
-    uint32_t kdo[4];
+    for (int ks = 0; ks < P::KS; ++ks) koff[ks] = rl * P::ROW + ((((2 * ks + hl) ^ (rl & 15)) & (P::CPR - 1)) << 4);
+    // K staging: wave w's load u fills cells CPL(LW w + u) + l/CPR; lane fetches chunk (l%CPR)^cell
+    // (the XOR touches the low four bits of the chunk index)
+    uint32_t kdo[P::LW];
 #pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-        const int cell = 4 * (4 * w + u4) + (lane >> 4);
-        kdo[u4] = (uint32_t)cell * knb + (uint32_t)(((lane & 15) ^ (cell & 15)) * 16);
+    for (int u = 0; u < P::LW; ++u) {
+        const int cell = P::CPL * (P::LW * w + u) + lane / P::CPR;
+        kdo[u] = (uint32_t)cell * knb + (uint32_t)(((lane % P::CPR) ^ (cell & 15)) * 16);
     }
-    // V staging: wave w's load u4 fills LDS rows 4u + t/16 (u = 4w + u4) at 16-byte position
-    // t%16, i.e. 32-byte chunk position (t%16)/2 of the row, which holds dims
-    // 16 * (position ^ (row % 8)); row % 8 = 4(u % 2) + t/16
-    uint32_t vdo[4];
+    // V staging: wave w's load u fills LDS row CPL(LW w + u) + t/CPR at 16-byte position
+    // t%CPR, i.e. 32-byte chunk position (t%CPR)/2 of the row, which holds dims
+    // 16 * (position ^ (row % 8))
+    uint32_t vdo[P::LW];
 #pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-        const int u = 4 * w + u4;
-        vdo[u4] = (uint32_t)(4 * u + (lane >> 4)) * vnb +
-                  32u * (((lane & 15) >> 1) ^ (4 * (u & 1) + (lane >> 4))) + 16u * (lane & 1);
+    for (int u = 0; u < P::LW; ++u) {
+        const int cell = P::CPL * (P::LW * w + u) + lane / P::CPR;
+        const int pos = lane % P::CPR;
+        vdo[u] = (uint32_t)cell * vnb + 32u * (uint32_t)((pos >> 1) ^ (cell & 7)) + 16u * (uint32_t)(pos & 1);
     }
     // V^T A operand of (db, kk), half h: lane (G = l/16, q = l%16) addresses cell
     // 16kk + 8h + 4(G/2) + q/4, dims 32db + 16(G%2) + 4(q%4) .. +3, which sits in chunk
-    // position (2db + G%2) ^ (4(G/2) + q/4).  The row offset has bits 5..7 clear, so the
-    // address is (row + 32*((G%2) ^ (4(G/2) + q/4)) + 8(q%4)) ^ 64db + (16kk + 8h)*256.
-    uint32_t vtr[4];
+    // position (2db + G%2) ^ (4(G/2) + q/4).  The row offset has the bits that 64db touches
+    // clear, so the address is (row + 32*((G%2) ^ (4(G/2) + q/4)) + 8(q%4)) ^ 64db +
+    // (16kk + 8h)*ROW.
+    uint32_t vtr[P::DB];
     {
         const int G = lane >> 4, q = lane & 15;
         const int x = 4 * (G >> 1) + (q >> 2);
-        const uint32_t base = (uint32_t)x * 256u + 32u * (uint32_t)((G & 1) ^ x) + 8u * (uint32_t)(q & 3);
+        const uint32_t base = (uint32_t)x * (uint32_t)P::ROW + 32u * (uint32_t)((G & 1) ^ x) + 8u * (uint32_t)(q & 3);
 #pragma unroll
-        for (int db = 0; db < 4; ++db) vtr[db] = lds0 + kVBase + (base ^ (64u * db));
+        for (int db = 0; db < P::DB; ++db) vtr[db] = lds0 + kVBase + (base ^ (64u * db));
     }
 
     auto issue_kv = [&](int t, int buf) {
         const int64_t ko = (int64_t)t * kBN * knb;
         const buf_rsrc krs = make_rsrc(kbase + ko, (uint32_t)(kbytes > ko ? kbytes - ko : 0));
-        dma16x4_to_lds(krs, kdo, lds0 + buf * kKBytes + 4 * w * 1024);
         const int64_t vo = (int64_t)t * kBN * vnb;
         const buf_rsrc vrs = make_rsrc(vbase + vo, (uint32_t)(vbytes > vo ? vbytes - vo : 0));
-        dma16x4_to_lds(vrs, vdo, lds0 + kVBase + buf * kVBytes + 4 * w * 1024);
+        if constexpr (P::LW == 4) {
+            dma16x4_to_lds(krs, kdo, lds0 + buf * kKBytes + 4 * w * 1024);
+            dma16x4_to_lds(vrs, vdo, lds0 + kVBase + buf * kVBytes + 4 * w * 1024);
+        } else {
+            dma16x8_to_lds(krs, kdo, lds0 + buf * kKBytes + 8 * w * 1024);
+            dma16x8_to_lds(vrs, vdo, lds0 + kVBase + buf * kVBytes + 8 * w * 1024);
+        }
     };
 
-    f32x16 acc[4];  // O^T blocks: dims 32db + 8(i/4) + 4hl + i%4 of row j
+    f32x16 acc[P::DB];  // O^T blocks: dims 32db + 8(i/4) + 4hl + i%4 of row j
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < P::DB; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[db][i] = 0.0f;
     float m_ref = neg_inf();  // raw score (FAST) or log2 units (GENERIC)
@@ -214,11 +231,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         f32x16 st[2];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 8192 + koff[0])), qop[0], zero16);
+            st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 32 * P::ROW + koff[0])), qop[0],
+                                  zero16);
 #pragma unroll
-            for (int ks = 1; ks < 8; ++ks)
-                st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 8192 + koff[ks])), qop[ks],
-                                      st[cb]);
+            for (int ks = 1; ks < P::KS; ++ks)
+                st[cb] = mfma32x32x16(as_f16x8(*reinterpret_cast<const u32x4*>(kt + cb * 32 * P::ROW + koff[ks])),
+                                      qop[ks], st[cb]);
         }
 
         __builtin_amdgcn_s_setprio(0);
@@ -268,7 +286,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
             }
             l_sum *= alpha;
 #pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+            for (int db = 0; db < P::DB; ++db) acc[db] *= alpha;
         }
 
         // ---- probabilities ----
@@ -313,10 +331,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const lds_char* vp = lds_ptr(vtr[db] + buf * kVBytes + kk * 16 * 256);
+            for (int db = 0; db < P::DB; ++db) {
+                const lds_char* vp = lds_ptr(vtr[db] + buf * kVBytes + kk * 16 * P::ROW);
                 const u32x2 lo = ld_tr16(vp);
-                const u32x2 hi = ld_tr16(vp + 8 * 256);
+                const u32x2 hi = ld_tr16(vp + 8 * P::ROW);
                 u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
                 if (MODE == MODE_GENERIC && a.mask) {
 #pragma unroll
@@ -330,8 +348,11 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         if (more) wait_vmcnt<0>();  // this wave's share of tile t+1 is in LDS
         __syncthreads();
     };
+    // (256-dim heads run every tail tile masked: two bodies per buffer in one loop would merge
+    // their accumulator sets, and the registers are all taken; at most one tail tile is
+    // unmasked, and the mask passes its cells)
     auto run_tile = [&](int t, auto BUF) {
-        if (MODE == MODE_FAST && t < t_full)
+        if (D == 128 && MODE == MODE_FAST && t < t_full)
             tile(t, BUF, std::integral_constant<bool, false>{});
         else
             tile(t, BUF, std::integral_constant<bool, true>{});
@@ -368,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
         const float inv = l_sum == 0.0f ? 0.0f : 1.0f / l_sum;
         char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < P::DB; ++db)
 #pragma unroll
             for (int bq = 0; bq < 4; ++bq)
                 st16(dst + (32 * db + 8 * bq + 4 * hl) * 4,
@@ -378,17 +399,24 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_f16_d128(FaArgs a, int ca
 
 }  // namespace
 
-hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim, hipStream_t stream) {
-    if (kv_type != SIXI_TYPE_F16 || head_dim != 128) return hipErrorNotSupported;
+template <int D>
+hipError_t launch_prefill_d(const FaArgs& a, int mask_mode, hipStream_t stream) {
     const bool generic = mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f;
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
     const int nrb = (a.n_q + kBM - 1) / kBM;
     const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
     if (generic)
-        hipLaunchKernelGGL((prefill_f16_d128<MODE_GENERIC>), grid, block, 0, stream, a, causal, nrb, a.P);
+        hipLaunchKernelGGL((prefill_f16<MODE_GENERIC, D>), grid, block, 0, stream, a, causal, nrb, a.P);
     else
-        hipLaunchKernelGGL((prefill_f16_d128<MODE_FAST>), grid, block, 0, stream, a, causal, nrb, a.P);
+        hipLaunchKernelGGL((prefill_f16<MODE_FAST, D>), grid, block, 0, stream, a, causal, nrb, a.P);
     return hipGetLastError();
+}
+
+hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim, hipStream_t stream) {
+    if (kv_type != SIXI_TYPE_F16) return hipErrorNotSupported;
+    if (head_dim == 128) return launch_prefill_d<128>(a, mask_mode, stream);
+    if (head_dim == 256) return launch_prefill_d<256>(a, mask_mode, stream);
+    return hipErrorNotSupported;
 }
 
 }  // namespace sixi

@@ -22,7 +22,7 @@ using sixi::FaArgs;
 using namespace sixi_abi;
 
 constexpr size_t kWsAlign = 256;
-// head dims built for gfx950: 128 everywhere; 256 for f16 KV blocks of <= 96 rows per GQA group
+// head dims built for gfx950: 128 everywhere; 256 for f16 KV
 constexpr bool head_dim_built(int64_t D) { return D == 128 || D == 256; }
 constexpr int kSplitMaxRows = 16 * sixi::kDecodeMaxRowTiles;  // G * n_q of the split-K kernel
 constexpr int64_t kQ8MaxRows = 48;  // rows per kv-head group of one q8_0 split-K launch
@@ -168,8 +168,8 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
-    // 256-dim heads: the 32-cell split-K kernel only (f16 KV, <= 96 rows per GQA group)
-    if (D == 256 && (!pl.splitk || k.type != SIXI_TYPE_F16)) return SIXI_E_UNSUPPORTED;
+    // 256-dim heads: f16 KV only (the q8_0 kernels and staging hold 128-dim rows)
+    if (D == 256 && k.type != SIXI_TYPE_F16) return SIXI_E_UNSUPPORTED;
     // q8_0 KV runs the 16-cell split-K kernel, which holds up to 48 rows per kv-head group:
     // a larger group is covered in launches over disjoint head subsets (each reads the KV).
     pl.heads_per_launch = a.G;

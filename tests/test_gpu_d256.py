@@ -1,6 +1,7 @@
 """256-dim heads (the real model's key/value length, configs/qwen3.8-27b-ud-q4-k-xl.sixi) on the
 32-cell split-K kernel, against the oracle through the C ABI: decode, speculative verify (96 rows
-per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
+per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q; and
+the prefill kernel for 256-dim heads.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
 import sys
 
 import numpy as np
@@ -75,11 +76,25 @@ def test_d256_f16_q(fa):
     _run_check(fa, w, "f16 Q")
 
 
-def test_d256_unsupported_forms_report_so(fa):
-    # prefill-sized blocks and q8_0 KV are not built for 256-dim heads
-    for kv_type, q_len in ((sa.TYPE_F16, 128), (sa.TYPE_Q8_0, 1)):
-        w = wl.Workload("d256 unsupported", 0x51A7_9400, 1, [300], [q_len], D=256, kv_type=kv_type)
-        dev = wl.to_device(wl.make_host(w))
-        out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
-        rc = fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], check=False)
-        assert rc == sa.E_UNSUPPORTED, (kv_type, q_len, rc)
+@pytest.mark.parametrize("label,kv_len,q_len", [
+    ("prefill chunk", [500], [300]),                # 1800 rows per group: the prefill kernel
+    ("prefill ragged", [64, 1000], [200, 129]),
+])
+def test_d256_prefill(fa, label, kv_len, q_len):
+    w = wl.Workload("d256 prefill", 0x51A7_9500 + sum(q_len), len(kv_len), kv_len, q_len, D=256, q_type=sa.TYPE_F16,
+                    mul=0.5)
+    _run_check(fa, w, label)
+
+
+def test_d256_prefill_explicit_mask(fa):
+    w = wl.Workload("d256 prefill mask", 0x51A7_9600, 1, [300], [150], D=256)
+    _run_check(fa, w, "prefill explicit mask", explicit=True)
+
+
+def test_d256_q8_reports_unsupported(fa):
+    # the q8_0 kernels and the f16 staging hold 128-dim rows
+    w = wl.Workload("d256 q8", 0x51A7_9400, 1, [300], [1], D=256, kv_type=sa.TYPE_Q8_0)
+    dev = wl.to_device(wl.make_host(w))
+    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    rc = fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], check=False)
+    assert rc == sa.E_UNSUPPORTED, rc
