@@ -52,7 +52,7 @@ struct FaArgs {
 };
 
 // q8_0 KV for prefill-sized blocks (fa_q8_stage.hip): K, V and Q staged as dense f16 rows in
-// the workspace, then the f16 prefill kernel.  k16/v16: [S][n_kv][Hkv][128], q16: [S][n_q][H][128].
+// the workspace, then the f16 kernels.  k16/v16: [S][n_kv][Hkv][D], q16: [S][n_q][H][D].
 struct Q8StageArgs {
     const char* q;
     int64_t q_nb1, q_nb2, q_nb3;
@@ -63,7 +63,7 @@ struct Q8StageArgs {
     int64_t v_nb1, v_nb2, v_nb3;
     const int32_t* kv_len;
     const int32_t* q_len;
-    int32_t S, H, Hkv, n_q;
+    int32_t S, H, Hkv, n_q, D;
     int64_t n_kv;
     char *k16, *v16, *q16;
 };

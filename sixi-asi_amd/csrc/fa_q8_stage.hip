@@ -1,10 +1,11 @@
-// fa_q8_stage.hip -- q8_0 KV for blocks of more than 96 rows per GQA group (prefill chunks):
-// the operands are staged as f16 in the workspace and the f16 prefill kernel runs on them.
+// fa_q8_stage.hip -- q8_0 KV where the q8_0 split-K kernel does not apply (blocks of more
+// than 48 rows of one head, prefill chunks, 256-dim heads): the operands are staged as f16 in
+// the workspace and the f16 kernels run on them.
 //
 // The values are exactly the MFMA operands the q8_0 split-K kernels use (fa_decode.hip), so
 // both paths compute ggml's q8_0 attention the same way:
 //   K, V  f16(q * d) per element (one rounding; d is the block's f16 scale), written as dense
-//         256-byte f16 rows [stream][cell][kv-head];
+//         f16 rows [stream][cell][kv-head] of D elements;
 //   Q     ggml's conversion of Q to K's dot type, q8_0 per 32-dim block (d = amax/127,
 //         q = round-half-away(x * 127/amax) clamped to +-127, src/core/numeric.cpp:349-384),
 //         entering the MFMA as f16(q * f16(d)); dense rows [stream][row][q-head].
@@ -30,11 +31,12 @@ __global__ __launch_bounds__(256) void q8_kv_to_f16(Q8StageArgs a, int which) {
     const char* src = which ? a.v : a.k;
     const int64_t nb1 = which ? a.v_nb1 : a.k_nb1, nb2 = which ? a.v_nb2 : a.k_nb2, nb3 = which ? a.v_nb3 : a.k_nb3;
     char* dst = which ? a.v16 : a.k16;
-    const int64_t n = (int64_t)a.S * a.n_kv * a.Hkv * 4;  // 4 blocks of 32 per 128-dim row
+    const int nb = a.D / 32;  // q8_0 blocks per head row
+    const int64_t n = (int64_t)a.S * a.n_kv * a.Hkv * nb;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const int b = (int)(i & 3);
-    int64_t r = i >> 2;
+    const int b = (int)(i % nb);
+    int64_t r = i / nb;
     const int h = (int)(r % a.Hkv);
     r /= a.Hkv;
     const int64_t cell = r % a.n_kv;
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(256) void q8_kv_to_f16(Q8StageArgs a, int which) {
     // a q8_0 block is 34 bytes: the f16 scale, then 32 int8 quants (2-byte aligned)
     const uint16_t* blk = reinterpret_cast<const uint16_t*>(src + cell * nb1 + (int64_t)h * nb2 + (int64_t)s * nb3 + b * 34);
     const float d = (float)__builtin_bit_cast(_Float16, blk[0]);
-    u32x4* o = reinterpret_cast<u32x4*>(dst + ((((int64_t)s * a.n_kv + cell) * a.Hkv + h) * 128 + b * 32) * 2);
+    u32x4* o = reinterpret_cast<u32x4*>(dst + ((((int64_t)s * a.n_kv + cell) * a.Hkv + h) * a.D + b * 32) * 2);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         f16x8 hv;
@@ -65,11 +67,12 @@ __global__ __launch_bounds__(256) void q8_kv_to_f16(Q8StageArgs a, int which) {
 }
 
 __global__ __launch_bounds__(256) void q8_q_to_f16(Q8StageArgs a) {
-    const int64_t n = (int64_t)a.S * a.n_q * a.H * 4;
+    const int nb = a.D / 32;
+    const int64_t n = (int64_t)a.S * a.n_q * a.H * nb;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const int b = (int)(i & 3);
-    int64_t r = i >> 2;
+    const int b = (int)(i % nb);
+    int64_t r = i / nb;
     const int h = (int)(r % a.H);
     r /= a.H;
     const int j = (int)(r % a.n_q);
@@ -97,7 +100,7 @@ __global__ __launch_bounds__(256) void q8_q_to_f16(Q8StageArgs a) {
     const float d = am / 127.0f;
     const float id = d != 0.0f ? 127.0f / am : 0.0f;
     const float dh = (float)(_Float16)d;
-    u32x4* o = reinterpret_cast<u32x4*>(a.q16 + ((((int64_t)s * a.n_q + j) * a.H + h) * 128 + b * 32) * 2);
+    u32x4* o = reinterpret_cast<u32x4*>(a.q16 + ((((int64_t)s * a.n_q + j) * a.H + h) * a.D + b * 32) * 2);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         f16x8 hv;
@@ -113,8 +116,8 @@ __global__ __launch_bounds__(256) void q8_q_to_f16(Q8StageArgs a) {
 }  // namespace
 
 hipError_t launch_q8_stage(const Q8StageArgs& a, hipStream_t stream) {
-    const int64_t nkv = (int64_t)a.S * a.n_kv * a.Hkv * 4;
-    const int64_t nq = (int64_t)a.S * a.n_q * a.H * 4;
+    const int64_t nkv = (int64_t)a.S * a.n_kv * a.Hkv * (a.D / 32);
+    const int64_t nq = (int64_t)a.S * a.n_q * a.H * (a.D / 32);
     if (nkv > 0) {
         const unsigned g = (unsigned)((nkv + 255) / 256);
         hipLaunchKernelGGL(q8_kv_to_f16, dim3(g), dim3(256), 0, stream, a, 0);

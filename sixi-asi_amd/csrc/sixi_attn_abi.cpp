@@ -168,17 +168,16 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
-    // 256-dim heads: f16 KV only (the q8_0 kernels and staging hold 128-dim rows)
-    if (D == 256 && k.type != SIXI_TYPE_F16) return SIXI_E_UNSUPPORTED;
     // q8_0 KV runs the 16-cell split-K kernel, which holds up to 48 rows per kv-head group:
     // a larger group is covered in launches over disjoint head subsets (each reads the KV).
     pl.heads_per_launch = a.G;
-    if (k.type == SIXI_TYPE_Q8_0 && rows > kQ8MaxRows) {
-        if (pl.splitk && n_q <= kQ8MaxRows) {
+    if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
+        // (the q8_0 split-K kernel holds 128-dim rows)
+        if (D == 128 && pl.splitk && n_q <= kQ8MaxRows) {
             pl.heads_per_launch = (int)(kQ8MaxRows / n_q);
         } else {
-            // prefill-sized blocks (or more than 48 rows of one head): K, V and Q are staged
-            // as f16 operands in the workspace (fa_q8_stage.hip) and the f16 kernels run
+            // prefill-sized blocks, more than 48 rows of one head, or 256-dim heads: K, V and Q
+            // are staged as f16 operands in the workspace (fa_q8_stage.hip) and the f16 kernels run
             pl.q8_stage = true;
             pl.kv_type = SIXI_TYPE_F16;
             int64_t kv_bytes = 0, q_bytes = 0, cells = 0, span = 0;
@@ -244,7 +243,7 @@ int sixi_attn_forward(const sixi_attn_params* p) {
         st.k = a.k; st.k_nb1 = a.k_nb1; st.k_nb2 = a.k_nb2; st.k_nb3 = a.k_nb3;
         st.v = a.v; st.v_nb1 = a.v_nb1; st.v_nb2 = a.v_nb2; st.v_nb3 = a.v_nb3;
         st.kv_len = a.kv_len; st.q_len = a.q_len;
-        st.S = a.S; st.H = a.H; st.Hkv = a.Hkv; st.n_q = a.n_q; st.n_kv = a.n_kv;
+        st.S = a.S; st.H = a.H; st.Hkv = a.Hkv; st.n_q = a.n_q; st.n_kv = a.n_kv; st.D = pl.D;
         st.k16 = ws + pl.stage_k; st.v16 = ws + pl.stage_v; st.q16 = ws + pl.stage_q;
         e = sixi::launch_q8_stage(st, stream);
         if (e != hipSuccess) return SIXI_E_BACKEND;

@@ -1,7 +1,7 @@
 """256-dim heads (the real model's key/value length, configs/qwen3.8-27b-ud-q4-k-xl.sixi) on the
 32-cell split-K kernel, against the oracle through the C ABI: decode, speculative verify (96 rows
-per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q; and
-the prefill kernel for 256-dim heads.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
+per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q; the
+prefill kernel for 256-dim heads; and q8_0 caches through the f16 staging.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
 import sys
 
 import numpy as np
@@ -91,10 +91,13 @@ def test_d256_prefill_explicit_mask(fa):
     _run_check(fa, w, "prefill explicit mask", explicit=True)
 
 
-def test_d256_q8_reports_unsupported(fa):
-    # the q8_0 kernels and the f16 staging hold 128-dim rows
-    w = wl.Workload("d256 q8", 0x51A7_9400, 1, [300], [1], D=256, kv_type=sa.TYPE_Q8_0)
-    dev = wl.to_device(wl.make_host(w))
-    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
-    rc = fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], check=False)
-    assert rc == sa.E_UNSUPPORTED, rc
+@pytest.mark.parametrize("label,kv_len,q_len", [
+    ("q8_0 decode", [3000, 70], [1, 1]),
+    ("q8_0 verify", [1200, 400], [16, 7]),
+    ("q8_0 prefill", [200], [150]),
+])
+def test_d256_q8_0_staged(fa, label, kv_len, q_len):
+    """q8_0 caches of 256-dim heads run through the f16 staging (the q8_0 split-K kernel holds
+    128-dim rows)."""
+    w = wl.Workload("d256 q8", 0x51A7_9700 + sum(q_len), len(kv_len), kv_len, q_len, D=256, kv_type=sa.TYPE_Q8_0)
+    _run_check(fa, w, label)
