@@ -155,6 +155,103 @@ def kv_write(src: np.ndarray, cache: np.ndarray, kv_len: Optional[Sequence[int]]
     return out
 
 
+# ---------------------------------------------------------------------------------------
+# Layer prologue / epilogue around the attention (include/sixi_layer.h).  Upstream llama.cpp
+# (pinned at a691b234 by scripts/build_llamacpp.sh:12, not in the reference tree) builds these
+# ops for the qwen35 layers of configs/qwen3.8-27b-ud-q4-k-xl.sixi; restated from ggml's CPU
+# ops (ggml_compute_forward_rms_norm_f32, ggml_rope_cache_init + the NEOX rotation,
+# ggml_vec_sigmoid_f32).  Pins: tests/test_oracle_layer.py (closed forms and invariants).
+
+_libm = None
+
+
+def rope_theta_scale(rope_base: float, n_rot: int) -> np.float32:
+    """ggml's theta_scale = powf(freq_base, -2.0f/n_dims) in f32, through the C library's powf
+    (the same function the host side of libsixi_attn.so calls)."""
+    global _libm
+    if _libm is None:
+        import ctypes.util
+
+        _libm = ctypes.CDLL(ctypes.util.find_library("m"))
+        _libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+        _libm.powf.restype = ctypes.c_float
+    if n_rot == 0:
+        return np.float32(1.0)
+    e = np.float32(-2.0) / np.float32(n_rot)
+    return np.float32(_libm.powf(float(np.float32(rope_base)), float(e)))
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """ggml_rms_norm then ggml_mul by the weight, over the last axis: squares in f32 summed in
+    double, mean = f32(sum / D), scale = 1/sqrtf(mean + eps), y = (x * scale) * w."""
+    x = np.asarray(x, dtype=np.float32)
+    ss = (x * x).astype(np.float64).sum(axis=-1, keepdims=True)
+    mean = (ss / x.shape[-1]).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(mean + np.float32(eps))
+    return (x * scale) * np.asarray(w, dtype=np.float32)
+
+
+def rope_neox(x: np.ndarray, pos: np.ndarray, n_rot: int, theta_scale) -> np.ndarray:
+    """NEOX RoPE of ``x[S, n_rows, heads, D]`` at positions ``pos[S, n_rows]``: pair
+    (i, i + n_rot/2), angle t_i with t_0 = f32(pos), t_{i+1} = t_i * theta_scale in f32 (ggml's
+    rope cache), cos/sin of the f32 angle rounded to f32; dims >= n_rot unchanged."""
+    x = np.asarray(x, dtype=np.float32)
+    out = x.copy()
+    if n_rot == 0:
+        return out
+    half = n_rot // 2
+    ts = np.float32(theta_scale)
+    t = np.asarray(pos).astype(np.float32)
+    theta = np.empty(t.shape + (half,), dtype=np.float32)
+    for i in range(half):
+        theta[..., i] = t
+        t = (t * ts).astype(np.float32)
+    c = np.cos(theta.astype(np.float64)).astype(np.float32)[..., None, :]
+    sn = np.sin(theta.astype(np.float64)).astype(np.float32)[..., None, :]
+    x0, x1 = x[..., :half], x[..., half:n_rot]
+    out[..., :half] = x0 * c - x1 * sn
+    out[..., half:n_rot] = x0 * sn + x1 * c
+    return out
+
+
+def qk_prologue(qg: np.ndarray, k: np.ndarray, v: np.ndarray, q_norm: np.ndarray, k_norm: np.ndarray,
+                k_cache: np.ndarray, v_cache: np.ndarray, kv_len: Optional[Sequence[int]] = None,
+                q_len: Optional[Sequence[int]] = None, eps: float = 1e-6, rope_base: float = 1e7,
+                n_rot: int = 64):
+    """CPU restatement of sixi_qk_prologue: ``qg[S, n_rows, H, 2D]`` (query then gate per head),
+    ``k/v[S, n_rows, Hkv, D]``.  Returns (q_out[S, n_rows, H, D] with NaN in rows >= q_len,
+    k_rot[S, n_rows, Hkv, D] (K before the store), k_cache', v_cache')."""
+    S, n_rows, H, D2 = qg.shape
+    D = D2 // 2
+    kl = np.zeros(S, dtype=np.int64) if kv_len is None else np.asarray(kv_len, dtype=np.int64)
+    pos = kl[:, None] + np.arange(n_rows, dtype=np.int64)[None, :]
+    ts = rope_theta_scale(rope_base, n_rot)
+    q = rope_neox(rms_norm(qg[..., :D], q_norm, eps), pos, n_rot, ts)
+    kr = rope_neox(rms_norm(k, k_norm, eps), pos, n_rot, ts)
+    if q_len is not None:
+        for s in range(S):
+            q[s, int(q_len[s]):] = np.nan
+    kc = kv_write(kr, k_cache, kl, q_len)
+    vc = kv_write(np.asarray(v, dtype=np.float32), v_cache, kl, q_len)
+    return q, kr, kc, vc
+
+
+def attn_gate(out: np.ndarray, qg: np.ndarray, q_len: Optional[Sequence[int]] = None) -> np.ndarray:
+    """out * sigmoid(gate) with ggml's sigmoid 1/(1 + expf(-g)) in f32; ``out[S, n_rows, H, D]``,
+    the gate is ``qg[..., D:]``; rows >= q_len keep their value."""
+    out = np.asarray(out, dtype=np.float32)
+    D = out.shape[-1]
+    g = np.asarray(qg[..., D:], dtype=np.float32)
+    with np.errstate(over="ignore"):  # e^-g beyond f32 range is inf, and the sigmoid 0
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+    sig = np.float32(1.0) / (np.float32(1.0) + e)
+    res = out * sig
+    if q_len is not None:
+        for s in range(out.shape[0]):
+            res[s, int(q_len[s]):] = out[s, int(q_len[s]):]
+    return res
+
+
 def fill_normal(seed: int, seq: int, n: int, mul: float = 1.0) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     load().oracle_fill_normal_f32(seed, seq, mul, out.ctypes.data, n)

@@ -46,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "sixi_kv_write_validate",
     "sixi_kv_copy",
     "sixi_verify_plan",
+    "sixi_qk_prologue",
+    "sixi_attn_gate",
 )
 
 
@@ -114,6 +116,35 @@ class SixiKvCopyParams(ctypes.Structure):
     ]
 
 
+class SixiQkPrologueParams(ctypes.Structure):
+    _fields_ = [
+        ("qg", SixiView),
+        ("k", SixiView),
+        ("v", SixiView),
+        ("q_norm", ctypes.c_void_p),
+        ("k_norm", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("rope_base", ctypes.c_float),
+        ("n_rot", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("kv_len", ctypes.c_void_p),
+        ("q_len", ctypes.c_void_p),
+        ("q_out", SixiView),
+        ("k_cache", SixiView),
+        ("v_cache", SixiView),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
+class SixiAttnGateParams(ctypes.Structure):
+    _fields_ = [
+        ("out", SixiView),
+        ("qg", SixiView),
+        ("q_len", ctypes.c_void_p),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
 class SixiVerifyStream(ctypes.Structure):
     _fields_ = [("stream", ctypes.c_int32), ("cached", ctypes.c_int32), ("real", ctypes.c_int32)]
 
@@ -161,6 +192,10 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.sixi_verify_plan.argtypes = [ctypes.POINTER(SixiVerifyStream), ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                      ctypes.POINTER(SixiVerifySlot), ctypes.POINTER(ctypes.c_int32)]
     lib.sixi_verify_plan.restype = ctypes.c_int
+    lib.sixi_qk_prologue.argtypes = [ctypes.POINTER(SixiQkPrologueParams)]
+    lib.sixi_qk_prologue.restype = ctypes.c_int
+    lib.sixi_attn_gate.argtypes = [ctypes.POINTER(SixiAttnGateParams)]
+    lib.sixi_attn_gate.restype = ctypes.c_int
     if path is None:
         _lib = lib
     return lib
@@ -373,3 +408,65 @@ def part_lengths(streams, slots, part: int, pad_mode: int = PAD_REFERENCE):
     kv_len = [streams[i][1] for _, i in members]
     q_len = [slots[i][3] if pad_mode == PAD_REFERENCE else streams[i][2] for _, i in members]
     return ids, kv_len, q_len
+
+
+def qk_prologue_params(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len=None, q_len=None,
+                       eps: float = 1e-6, rope_base: float = 1e7, n_rot: int = 64,
+                       stream=None) -> SixiQkPrologueParams:
+    """Parameters of ``sixi_qk_prologue`` for torch tensors: ``qg[S, n_rows, H, 2D]`` (per head
+    the query, then its gate), ``k/v[S, n_rows, Hkv, D]`` f32, ``q_norm/k_norm[D]`` f32,
+    ``q_out[S, n_rows, H, D]`` f32 (the attention's Q), caches ``[S, n_cells, Hkv, D]`` f16 or
+    uint8 q8_0 blocks."""
+    D = q_out.shape[-1]
+    p = SixiQkPrologueParams()
+    p.qg = view_of(qg, tokens_heads=False)
+    p.k = view_of(k, tokens_heads=False)
+    p.v = view_of(v, tokens_heads=False)
+    p.q_norm = q_norm.data_ptr()
+    p.k_norm = k_norm.data_ptr()
+    p.eps = eps
+    p.rope_base = rope_base
+    p.n_rot = n_rot
+    p.flags = 0
+    p.kv_len = kv_len.data_ptr() if kv_len is not None else None
+    p.q_len = q_len.data_ptr() if q_len is not None else None
+    p.q_out = view_of(q_out)
+    p.k_cache = _cache_view(k_cache, D)
+    p.v_cache = _cache_view(v_cache, D)
+    p.stream = stream
+    return p
+
+
+def qk_prologue(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len=None, q_len=None,
+                eps: float = 1e-6, rope_base: float = 1e7, n_rot: int = 64, stream=None, check=True) -> int:
+    """The Q/K prologue of a Qwen3.8 full-attention layer (include/sixi_layer.h) fused with the
+    KV store: RMS norm times the attn_q_norm / attn_k_norm weight, NEOX RoPE on the first
+    ``n_rot`` dims at position kv_len[s] + j, Q to ``q_out``, K and V into cell kv_len[s] + j of
+    the caches (the codecs of :func:`kv_write`).  Defaults are configs/qwen3.8-27b-ud-q4-k-xl.sixi's
+    rms_norm_eps, rope_freq_base and rope_dim_count.  Asynchronous on the current stream."""
+    import torch
+
+    p = qk_prologue_params(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len, q_len, eps, rope_base,
+                           n_rot, stream)
+    if p.stream is None:
+        p.stream = torch.cuda.current_stream(q_out.device).cuda_stream
+    rc = load_library().sixi_qk_prologue(ctypes.byref(p))
+    if check and rc != OK:
+        raise SixiAttnError(rc, strerror(rc))
+    return rc
+
+
+def attn_gate(out, qg, q_len=None, stream=None, check=True) -> int:
+    """``out[S, n_rows, H, D] *= sigmoid(gate)`` in place, the gate being the second half of
+    each head of ``qg[S, n_rows, H, 2D]`` (include/sixi_layer.h)."""
+    import torch
+
+    p = SixiAttnGateParams()
+    p.out = view_of(out, tokens_heads=False)
+    p.qg = view_of(qg, tokens_heads=False)
+    p.q_len = q_len.data_ptr() if q_len is not None else None
+    p.stream = stream if stream is not None else torch.cuda.current_stream(out.device).cuda_stream
+    rc = load_library().sixi_attn_gate(ctypes.byref(p))
+    if check and rc != OK:
+        raise SixiAttnError(rc, strerror(rc))
+    return rc

@@ -200,3 +200,74 @@ def test_kv_copy_of_nothing_is_ok_without_a_launch():
     p = _kv_copy_params()
     p.n_cells = 0
     assert sa.load_library().sixi_kv_copy(ctypes.byref(p)) == sa.OK
+
+
+def _prologue_params(S=2, R=16, H=24, Hkv=4, D=256, n_cells=4096, cache_type=sa.TYPE_F16, n_rot=64):
+    p = sa.SixiQkPrologueParams()
+    p.qg = sa.make_view(FAKE, sa.TYPE_F32, [2 * D, H, R, S], [4, 2 * D * 4, H * 2 * D * 4, R * H * 2 * D * 4])
+    kv = [4, D * 4, Hkv * D * 4, R * Hkv * D * 4]
+    p.k = sa.make_view(FAKE, sa.TYPE_F32, [D, Hkv, R, S], kv)
+    p.v = sa.make_view(FAKE, sa.TYPE_F32, [D, Hkv, R, S], kv)
+    p.q_norm = p.k_norm = FAKE
+    p.eps, p.rope_base, p.n_rot, p.flags = 1e-6, 1e7, n_rot, 0
+    p.kv_len = FAKE
+    p.q_out = sa.make_view(FAKE, sa.TYPE_F32, [D, R, H, S], [4, H * D * 4, D * 4, R * H * D * 4])
+    row = D * 2 if cache_type == sa.TYPE_F16 else D // 32 * 34
+    nb0 = 2 if cache_type == sa.TYPE_F16 else 34
+    for name in ("k_cache", "v_cache"):
+        setattr(p, name, sa.make_view(FAKE, cache_type, [D, n_cells, Hkv, S], [nb0, Hkv * row, row, n_cells * Hkv * row]))
+    return p
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda p: setattr(p, "flags", 1), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p, "q_norm", None), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.k_cache, "data", None), sa.E_INVALID_ARGUMENT),
+    (lambda p: (p.q_out.ne.__setitem__(0, 64), p.qg.ne.__setitem__(0, 128)), sa.E_UNSUPPORTED),   # head of 64
+    (lambda p: p.qg.ne.__setitem__(0, 256), sa.E_INVALID_ARGUMENT),            # no gate half
+    (lambda p: p.q_out.ne.__setitem__(2, 16), sa.E_INVALID_ARGUMENT),          # q-heads differ
+    (lambda p: p.v.ne.__setitem__(1, 2), sa.E_INVALID_ARGUMENT),               # kv-heads differ
+    (lambda p: p.v_cache.ne.__setitem__(1, 2048), sa.E_INVALID_ARGUMENT),      # caches differ
+    (lambda p: setattr(p.v_cache, "type", sa.TYPE_Q8_0), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.q_out, "type", sa.TYPE_F16), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p, "n_rot", 66), sa.E_INVALID_ARGUMENT),                # not a multiple of D/32
+    (lambda p: setattr(p, "n_rot", 264), sa.E_INVALID_ARGUMENT),               # more than D
+    (lambda p: setattr(p, "eps", -1.0), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p, "rope_base", 0.0), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p, "eps", float("nan")), sa.E_INVALID_ARGUMENT),
+    (lambda p: p.q_out.nb.__setitem__(2, 512), sa.E_INVALID_ARGUMENT),         # q-heads would alias
+    (lambda p: p.k_cache.nb.__setitem__(1, 64), sa.E_INVALID_ARGUMENT),        # cells would alias
+    (lambda p: setattr(p.qg, "data", FAKE + 8), sa.E_ALIGNMENT),
+    (lambda p: setattr(p.k_cache, "data", FAKE + 2), sa.E_ALIGNMENT),          # f16 rows 16-B aligned
+    (lambda p: p.k.nb.__setitem__(2, 1 << 62), sa.E_INTEGER_OVERFLOW),        # 15 rows of 2^62 bytes
+])
+def test_qk_prologue_rejects(mutate, code):
+    p = _prologue_params()
+    mutate(p)
+    assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == code
+
+
+def test_qk_prologue_q8_cache_and_empty_block():
+    p = _prologue_params(cache_type=sa.TYPE_Q8_0)
+    p.k_cache.data = FAKE + 2                      # q8_0 rows need 2-byte alignment only
+    p.flags = 1
+    assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT
+    for cache_type, D in ((sa.TYPE_F16, 128), (sa.TYPE_Q8_0, 256)):
+        p = _prologue_params(S=0, D=D, cache_type=cache_type, n_rot=D)   # nothing to do: no launch
+        assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == sa.OK
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda p: setattr(p.out, "data", None), sa.E_INVALID_ARGUMENT),
+    (lambda p: p.qg.ne.__setitem__(0, 256), sa.E_INVALID_ARGUMENT),
+    (lambda p: (p.out.ne.__setitem__(0, 96), p.qg.ne.__setitem__(0, 192)), sa.E_UNSUPPORTED),
+    (lambda p: p.out.nb.__setitem__(1, 0), sa.E_INVALID_ARGUMENT),             # heads would alias
+    (lambda p: setattr(p.out, "data", FAKE + 4), sa.E_ALIGNMENT),
+])
+def test_attn_gate_rejects(mutate, code):
+    D, H, R, S = 256, 24, 16, 2
+    p = sa.SixiAttnGateParams()
+    p.out = sa.make_view(FAKE, sa.TYPE_F32, [D, H, R, S], [4, D * 4, H * D * 4, R * H * D * 4])
+    p.qg = sa.make_view(FAKE, sa.TYPE_F32, [2 * D, H, R, S], [4, 2 * D * 4, H * 2 * D * 4, R * H * 2 * D * 4])
+    mutate(p)
+    assert sa.load_library().sixi_attn_gate(ctypes.byref(p)) == code
