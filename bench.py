@@ -228,6 +228,89 @@ def time_kv_store(w, dev, steps: int, warmup: int) -> dict:
     return res
 
 
+def _graph_us(fn, steps: int, warmup: int, per_graph: int = 8) -> float:
+    """GPU time per call of ``fn`` (a few short launches): warmed up on a side stream, captured
+    ``per_graph`` times in one HIP graph, the graph replayed; microseconds per call."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * per_graph) * 1e3
+
+
+def time_layer(steps: int, warmup: int) -> dict:
+    """The work around the attention of one Qwen3.8 full-attention layer (include/sixi_layer.h)
+    for the 256-dim verify batch (32 streams x 16 rows, 24 q-heads, 4 kv-heads): the prologue
+    (Q/K RMS norm + RoPE on 64 dims, Q written, K and V stored in the f16 cache) and the output
+    gate.  Algorithmic bytes: prologue 2*H*D*4 (Q half read, Q written) + 2*Hkv*D*4 (K, V read)
+    + 2*Hkv*D*2 (cache rows written) per row; gate 3*H*D*4 per row (output and gate read,
+    output written)."""
+    import ctypes
+
+    import torch
+
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    lib = sa.load_library()
+    w = wl.config("batched_verify_d256")
+    S, R, H, Hkv, D = w.S, w.n_q, w.H, w.Hkv, w.D
+    n_cells = max(a + b for a, b in zip(w.kv_len, w.q_len))
+    qg = torch.randn((S, R, H, 2 * D), dtype=torch.float32, device="cuda")
+    k = torch.randn((S, R, Hkv, D), dtype=torch.float32, device="cuda")
+    v = torch.randn_like(k)
+    wq = torch.rand(D, dtype=torch.float32, device="cuda") + 0.5
+    wk = torch.rand_like(wq) + 0.5
+    q_out = torch.empty((S, R, H, D), dtype=torch.float32, device="cuda")
+    kc = torch.zeros((S, n_cells, Hkv, D), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    kl = torch.tensor(w.kv_len, dtype=torch.int32, device="cuda")
+    ql = torch.tensor(w.q_len, dtype=torch.int32, device="cuda")
+    out = torch.randn((S, R, H, D), dtype=torch.float32, device="cuda")
+    pp = sa.qk_prologue_params(qg, k, v, wq, wk, q_out, kc, vc, kl, ql)
+    pg = sa.SixiAttnGateParams()
+    pg.out = sa.view_of(out, tokens_heads=False)
+    pg.qg = sa.view_of(qg, tokens_heads=False)
+    pg.q_len = ql.data_ptr()
+
+    def call(fn, p):
+        def run():
+            p.stream = torch.cuda.current_stream().cuda_stream
+            rc = fn(ctypes.byref(p))
+            if rc != sa.OK:
+                raise sa.SixiAttnError(rc, sa.strerror(rc))
+        return run
+
+    rows = int(sum(w.q_len))
+    res = {"workload": f"{S} streams x {R} rows, {H} q-heads / {Hkv} kv-heads x {D}, 64 rotated dims, f16 cache"}
+    for name, fn, p, per_row in (("prologue", lib.sixi_qk_prologue, pp, 2 * H * D * 4 + 2 * Hkv * D * 4 + 2 * Hkv * D * 2),
+                                 ("gate", lib.sixi_attn_gate, pg, 3 * H * D * 4)):
+        us = _graph_us(call(fn, p), steps, warmup)
+        nbytes = rows * per_row
+        res[name] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
+                     "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return res
+
+
 def prefill_only(steps: int, warmup: int) -> int:
     import sixi_attn as sa
 
@@ -243,7 +326,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "layer"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -260,6 +343,9 @@ def main() -> int:
         return copy_calibration(max(1, args.steps))
     if args.workload == "prefill":
         return prefill_only(args.steps, args.warmup)
+    if args.workload == "layer":
+        print(json.dumps(time_layer(max(8, args.steps), args.warmup)), flush=True)
+        return 0
 
     import sixi_attn as sa
     from sixi_attn import workloads as wl
@@ -333,6 +419,12 @@ def main() -> int:
         except sa.SixiAttnError as e:
             result["kv_store"] = {"unavailable": str(e)}
         _log(f"kv_store: {result['kv_store']}")
+        # the Q/K prologue with the KV store, and the output gate, of a 256-dim layer
+        try:
+            result["layer_prologue_gate"] = time_layer(max(40, args.steps // 2), max(5, args.warmup // 2))
+        except sa.SixiAttnError as e:
+            result["layer_prologue_gate"] = {"unavailable": str(e)}
+        _log(f"layer prologue/gate: {result['layer_prologue_gate']}")
 
         # chunked causal prefill (2 chunks of 2048 rows on a 2048-cell cache)
         try:

@@ -30,8 +30,8 @@ typedef struct sixi_qk_prologue_params {
     sixi_view qg;           /* [2D, H, n_rows, S] f32: attn_q output, per head D query then D gate */
     sixi_view k;            /* [D, Hkv, n_rows, S] f32: attn_k output                             */
     sixi_view v;            /* [D, Hkv, n_rows, S] f32: attn_v output                             */
-    const float* q_norm;    /* device [D]: attn_q_norm weight                                     */
-    const float* k_norm;    /* device [D]: attn_k_norm weight                                     */
+    const float* q_norm;    /* device [D], 16-byte aligned: attn_q_norm weight                    */
+    const float* k_norm;    /* device [D], 16-byte aligned: attn_k_norm weight                    */
     float eps;              /* RMS norm epsilon                                                   */
     float rope_base;        /* RoPE frequency base                                                */
     int32_t n_rot;          /* RoPE dims: even, a multiple of D/32, at most D                     */

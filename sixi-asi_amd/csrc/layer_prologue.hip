@@ -17,10 +17,11 @@
 //   gate       out *= 1 / (1 + exp(-g)) (ggml_sigmoid, ggml_mul), g the second half of the
 //              head's attn_q output.
 //
-// One wave per (stream, row, head) item with D/64 consecutive elements per lane: the head's
-// sum of squares and the q8_0 block maxima are wave shuffles, the RoPE partner of an element
-// sits n_rot/2 elements away, in the same register of another lane.  Both kernels are
-// HBM-bound byte work (f32 in, f32 or f16/q8_0 out) with no reuse.
+// One block per (stream, row); a wave holds one head row at a time with D/64 consecutive
+// elements per lane: the head's sum of squares and the q8_0 block maxima are wave shuffles,
+// the RoPE partner of an element sits n_rot/2 elements away, in the same register of another
+// lane, and each wave forms the row's cos/sin pairs once for all the heads it takes.
+// Both kernels are HBM-bound byte work (f32 in, f32 or f16/q8_0 out) with no reuse.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -62,10 +63,11 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// RMS norm with weight, then RoPE on the first n_rot dims (whole wave, uniform control flow).
+// RMS norm with weight, then RoPE on the first n_rot dims; c/s hold the cos/sin of the pairs
+// of the lane's elements (whole wave, uniform control flow).
 template <int E>
-__device__ __forceinline__ void norm_rope(float (&x)[E], int lane, const float* w, float eps, int D, int n_rot,
-                                          float theta_scale, float pos) {
+__device__ __forceinline__ void norm_rope(float (&x)[E], int lane, const float (&w)[E], float eps, int D, int n_rot,
+                                          const float (&c)[E], const float (&sn)[E]) {
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) ss += x[e] * x[e];
@@ -75,7 +77,7 @@ __device__ __forceinline__ void norm_rope(float (&x)[E], int lane, const float* 
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const float y = x[e] * scale;
-        x[e] = y * w[lane * E + e];
+        x[e] = y * w[e];
     }
     if (n_rot == 0) return;
     const int lane_off = n_rot / 2 / E;  // lanes between an element and its partner
@@ -86,18 +88,40 @@ __device__ __forceinline__ void norm_rope(float (&x)[E], int lane, const float* 
 #pragma unroll
     for (int e = 0; e < E; ++e) other[e] = __shfl(x[e], partner, 64);
     if (!rotated) return;
-    // angle of pair i: p * theta_scale^i, multiplied out one step at a time
-    const int i0 = (first ? lane : lane - lane_off) * E;
-    float theta = pos;
-    for (int i = 0; i < i0; ++i) theta *= theta_scale;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const float c = cosf(theta), s = sinf(theta);
         if (first)
-            x[e] = x[e] * c - other[e] * s;
+            x[e] = x[e] * c[e] - other[e] * sn[e];
         else
-            x[e] = other[e] * s + x[e] * c;
-        theta *= theta_scale;
+            x[e] = other[e] * sn[e] + x[e] * c[e];
+    }
+}
+
+// cos/sin of the pairs of this lane's elements at position pos: lane p forms pairs p and p + 64
+// (angle p * theta_scale^i, multiplied out one step at a time), then each lane gathers its own.
+template <int E>
+__device__ __forceinline__ void rope_angles(int lane, int n_rot, float theta_scale, float pos, float (&c)[E],
+                                            float (&sn)[E]) {
+    const int half = n_rot / 2;
+    float c0 = 1.0f, s0 = 0.0f, c1 = 1.0f, s1 = 0.0f;
+    if (lane < half) {
+        float theta = pos;
+        for (int i = 0; i < lane; ++i) theta *= theta_scale;
+        sincosf(theta, &s0, &c0);
+        if (lane + 64 < half) {
+            for (int i = 0; i < 64; ++i) theta *= theta_scale;
+            sincosf(theta, &s1, &c1);
+        }
+    }
+    const int lane_off = half / E;
+    const int i0 = (lane < lane_off ? lane : lane - lane_off) * E;  // first pair of the lane's elements
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = i0 + e;
+        const float a0 = __shfl(c0, i & 63, 64), b0 = __shfl(s0, i & 63, 64);
+        const float a1 = __shfl(c1, i & 63, 64), b1 = __shfl(s1, i & 63, 64);
+        c[e] = i < 64 ? a0 : a1;
+        sn[e] = i < 64 ? b0 : b1;
     }
 }
 
@@ -140,73 +164,125 @@ __device__ __forceinline__ void store_q8(char* row, int lane, const float (&x)[E
     }
 }
 
+constexpr int kBatch = 8;  // head rows a wave loads before it computes
+
+// One block of four waves per (stream, row).  Wave w takes the slots w, w+4, ... of the row
+// (q-heads, k-heads, v-heads in that order), kBatch at a time.  The first batch is loaded
+// before the row's q_len is read (every row of the view is in bounds; a row past q_len is
+// dropped afterwards), and each wave forms the row's RoPE angles in its own registers while
+// those loads are in flight: no LDS, no barrier.
 template <int D, bool Q8>
 __global__ __launch_bounds__(256) void qk_prologue(QkPrologueArgs a) {
     constexpr int E = D / 64;
+    const int j = (int)(blockIdx.x % (unsigned)a.n_rows);
+    const int s = (int)(blockIdx.x / (unsigned)a.n_rows);
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar address math
     const int slots = a.H + 2 * a.Hkv;
-    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (int64_t)a.S * a.n_rows * slots) return;
-    const int slot = (int)(item % slots);
-    const int64_t r = item / slots;
-    const int j = (int)(r % a.n_rows);
-    const int s = (int)(r / a.n_rows);
-    const int ql = a.q_len ? a.q_len[s] : a.n_rows;
-    if (j >= ql) return;
+    const char* qrow = a.qg + (int64_t)j * a.qg_nb2 + (int64_t)s * a.qg_nb3;
+    const char* krow = a.k + (int64_t)j * a.k_nb2 + (int64_t)s * a.k_nb3;
+    const char* vrow = a.v + (int64_t)j * a.v_nb2 + (int64_t)s * a.v_nb3;
+    float x[kBatch][E], wq[E], wk[E];
+    auto load_batch = [&](int first) {
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int slot = first + 4 * b;
+            if (slot >= slots) break;
+            const char* src = slot < a.H             ? qrow + (int64_t)slot * a.qg_nb1
+                              : slot < a.H + a.Hkv ? krow + (int64_t)(slot - a.H) * a.k_nb1
+                                                   : vrow + (int64_t)(slot - a.H - a.Hkv) * a.v_nb1;
+            load_row<E>(src, lane, x[b]);
+        }
+    };
     const int64_t pos = (int64_t)(a.kv_len ? a.kv_len[s] : 0) + j;
-    float x[E];
-    if (slot < a.H) {
-        load_row<E>(a.qg + (int64_t)slot * a.qg_nb1 + (int64_t)j * a.qg_nb2 + (int64_t)s * a.qg_nb3, lane, x);
-        norm_rope<E>(x, lane, a.q_norm, a.eps, D, a.n_rot, a.theta_scale, (float)pos);
-        store_row<E>(a.q_out + (int64_t)j * a.qo_nb1 + (int64_t)slot * a.qo_nb2 + (int64_t)s * a.qo_nb3, lane, x);
-        return;
+    load_batch(wave);
+    load_row<E>(reinterpret_cast<const char*>(a.q_norm), lane, wq);
+    load_row<E>(reinterpret_cast<const char*>(a.k_norm), lane, wk);
+    float c[E], sn[E];
+    if (a.n_rot > 0) rope_angles<E>(lane, a.n_rot, a.theta_scale, (float)pos, c, sn);
+    if (j >= (a.q_len ? a.q_len[s] : a.n_rows)) return;
+    const bool in_cache = pos >= 0 && pos < a.n_cells;  // outside the stream's cells: not stored
+    char* qo_row = a.q_out + (int64_t)j * a.qo_nb1 + (int64_t)s * a.qo_nb3;
+    char* kc_row = a.kc + pos * a.kc_nb1 + (int64_t)s * a.kc_nb3;
+    char* vc_row = a.vc + pos * a.vc_nb1 + (int64_t)s * a.vc_nb3;
+    // per batch: every row is computed before the first store, since a store in flight makes
+    // the next load's wait a full drain (one counter covers loads and stores)
+    for (int first = wave; first < slots; first += 4 * kBatch) {
+        if (first != wave) load_batch(first);
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int slot = first + 4 * b;
+            if (slot >= slots) break;
+            if (slot < a.H)
+                norm_rope<E>(x[b], lane, wq, a.eps, D, a.n_rot, c, sn);
+            else if (slot < a.H + a.Hkv && in_cache)
+                norm_rope<E>(x[b], lane, wk, a.eps, D, a.n_rot, c, sn);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int slot = first + 4 * b;
+            if (slot >= slots) break;
+            if (slot < a.H) {
+                store_row<E>(qo_row + (int64_t)slot * a.qo_nb2, lane, x[b]);
+                continue;
+            }
+            if (!in_cache) continue;
+            char* row = slot < a.H + a.Hkv ? kc_row + (int64_t)(slot - a.H) * a.kc_nb2
+                                           : vc_row + (int64_t)(slot - a.H - a.Hkv) * a.vc_nb2;
+            if constexpr (Q8)
+                store_q8<E>(row, lane, x[b]);
+            else
+                store_f16<E>(row, lane, x[b]);
+        }
     }
-    if (pos < 0 || pos >= a.n_cells) return;  // outside the stream's cells: not stored
-    const bool is_k = slot < a.H + a.Hkv;
-    const int h = is_k ? slot - a.H : slot - a.H - a.Hkv;
-    char* row;
-    if (is_k) {
-        load_row<E>(a.k + (int64_t)h * a.k_nb1 + (int64_t)j * a.k_nb2 + (int64_t)s * a.k_nb3, lane, x);
-        norm_rope<E>(x, lane, a.k_norm, a.eps, D, a.n_rot, a.theta_scale, (float)pos);
-        row = a.kc + pos * a.kc_nb1 + (int64_t)h * a.kc_nb2 + (int64_t)s * a.kc_nb3;
-    } else {
-        load_row<E>(a.v + (int64_t)h * a.v_nb1 + (int64_t)j * a.v_nb2 + (int64_t)s * a.v_nb3, lane, x);
-        row = a.vc + pos * a.vc_nb1 + (int64_t)h * a.vc_nb2 + (int64_t)s * a.vc_nb3;
-    }
-    if constexpr (Q8)
-        store_q8<E>(row, lane, x);
-    else
-        store_f16<E>(row, lane, x);
 }
 
+// One block of four waves per (stream, row); wave w gates heads w, w+4, ..., loading kBatch
+// heads' output and gate rows before the first product.
 template <int D>
 __global__ __launch_bounds__(256) void attn_gate(AttnGateArgs a) {
     constexpr int E = D / 64;
+    const int j = (int)(blockIdx.x % (unsigned)a.n_rows);
+    const int s = (int)(blockIdx.x / (unsigned)a.n_rows);
     const int lane = threadIdx.x & 63;
-    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (int64_t)a.S * a.n_rows * a.H) return;
-    const int h = (int)(item % a.H);
-    const int64_t r = item / a.H;
-    const int j = (int)(r % a.n_rows);
-    const int s = (int)(r / a.n_rows);
-    if (a.q_len && j >= a.q_len[s]) return;
-    float g[E], o[E];
-    load_row<E>(a.qg + (int64_t)h * a.g_nb1 + (int64_t)j * a.g_nb2 + (int64_t)s * a.g_nb3 + (int64_t)D * 4, lane, g);
-    char* op = a.out + (int64_t)h * a.o_nb1 + (int64_t)j * a.o_nb2 + (int64_t)s * a.o_nb3;
-    load_row<E>(op, lane, o);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    bool checked = false;
+    for (int first = wave; first < a.H; first += 4 * kBatch) {
+        float g[kBatch][E], o[kBatch][E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) o[e] = o[e] * (1.0f / (1.0f + expf(-g[e])));
-    store_row<E>(op, lane, o);
+        for (int b = 0; b < kBatch; ++b) {
+            const int h = first + 4 * b;
+            if (h >= a.H) break;
+            load_row<E>(a.qg + (int64_t)h * a.g_nb1 + (int64_t)j * a.g_nb2 + (int64_t)s * a.g_nb3 + (int64_t)D * 4, lane,
+                        g[b]);
+            load_row<E>(a.out + (int64_t)h * a.o_nb1 + (int64_t)j * a.o_nb2 + (int64_t)s * a.o_nb3, lane, o[b]);
+        }
+        // the row's length is read once the first loads are in flight (every row is in bounds)
+        if (!checked) {
+            if (a.q_len && j >= a.q_len[s]) return;
+            checked = true;
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            if (first + 4 * b >= a.H) break;
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[b][e] = o[b][e] * (1.0f / (1.0f + expf(-g[b][e])));
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int h = first + 4 * b;
+            if (h >= a.H) break;
+            store_row<E>(a.out + (int64_t)h * a.o_nb1 + (int64_t)j * a.o_nb2 + (int64_t)s * a.o_nb3, lane, o[b]);
+        }
+    }
 }
-
-unsigned waves_grid(int64_t items) { return (unsigned)((items + 3) / 4); }
 
 }  // namespace
 
 hipError_t launch_qk_prologue(const QkPrologueArgs& a, hipStream_t stream) {
-    const int64_t items = (int64_t)a.S * a.n_rows * (a.H + 2 * a.Hkv);
-    if (items == 0) return hipSuccess;
-    const dim3 grid(waves_grid(items)), block(256);
+    const int64_t rows = (int64_t)a.S * a.n_rows;
+    if (rows == 0 || a.H + 2 * a.Hkv == 0) return hipSuccess;
+    const dim3 grid((unsigned)rows), block(256);
     if (a.D == 128) {
         if (a.cache_q8)
             hipLaunchKernelGGL((qk_prologue<128, true>), grid, block, 0, stream, a);
@@ -222,9 +298,9 @@ hipError_t launch_qk_prologue(const QkPrologueArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_attn_gate(const AttnGateArgs& a, hipStream_t stream) {
-    const int64_t items = (int64_t)a.S * a.n_rows * a.H;
-    if (items == 0) return hipSuccess;
-    const dim3 grid(waves_grid(items)), block(256);
+    const int64_t rows = (int64_t)a.S * a.n_rows;
+    if (rows == 0 || a.H == 0) return hipSuccess;
+    const dim3 grid((unsigned)rows), block(256);
     if (a.D == 128)
         hipLaunchKernelGGL(attn_gate<128>, grid, block, 0, stream, a);
     else

@@ -53,9 +53,8 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     if (!std::isfinite(p->eps) || p->eps < 0.0f) return SIXI_E_INVALID_ARGUMENT;
     if (!std::isfinite(p->rope_base) || p->rope_base <= 0.0f) return SIXI_E_INVALID_ARGUMENT;
     if (H > INT32_MAX || Hkv > INT32_MAX || n_rows > INT32_MAX || S > INT32_MAX) return SIXI_E_INTEGER_OVERFLOW;
-    int64_t rows = 0, items = 0;  // one wave per (stream, row, head) item, four waves a block
-    if (!mul_ok(S, n_rows, &rows) || !mul_ok(rows, H + 2 * Hkv, &items) || items / 4 >= (int64_t)UINT32_MAX)
-        return SIXI_E_INTEGER_OVERFLOW;
+    int64_t rows = 0;  // one block per (stream, row)
+    if (!mul_ok(S, n_rows, &rows) || rows >= (int64_t)UINT32_MAX) return SIXI_E_INTEGER_OVERFLOW;
     const int64_t crb = row_bytes(kc.type, D);
     if (view_span(qg, 2 * D * 4) < 0 || view_span(k, D * 4) < 0 || view_span(v, D * 4) < 0 ||
         view_span(qo, D * 4) < 0 || view_span(kc, crb) < 0 || view_span(vc, crb) < 0)
@@ -63,6 +62,7 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     // written rows must not alias one another
     if (!rows_disjoint(qo, D * 4) || !rows_disjoint(kc, crb) || !rows_disjoint(vc, crb)) return SIXI_E_INVALID_ARGUMENT;
     if (!rows16(qg) || !rows16(k) || !rows16(v) || !rows16(qo)) return SIXI_E_ALIGNMENT;
+    if (!aligned(p->q_norm, 16) || !aligned(p->k_norm, 16)) return SIXI_E_ALIGNMENT;
     if (kc.type == SIXI_TYPE_F16 ? (!rows16(kc) || !rows16(vc))
                                  : (!aligned(kc.data, 2) || !aligned(vc.data, 2) || kc.nb[1] % 2 || kc.nb[2] % 2 ||
                                     kc.nb[3] % 2 || vc.nb[1] % 2 || vc.nb[2] % 2 || vc.nb[3] % 2))
@@ -120,9 +120,8 @@ int resolve_gate(const sixi_attn_gate_params* p, sixi::AttnGateArgs* out) {
     if (D != 128 && D != 256) return SIXI_E_UNSUPPORTED;
     if (!dims_are(g, 2 * D, H, n_rows, S)) return SIXI_E_INVALID_ARGUMENT;
     if (H > INT32_MAX || n_rows > INT32_MAX || S > INT32_MAX) return SIXI_E_INTEGER_OVERFLOW;
-    int64_t items = 0;
-    if (!mul_ok(S, n_rows, &items) || !mul_ok(items, H, &items) || items / 4 >= (int64_t)UINT32_MAX)
-        return SIXI_E_INTEGER_OVERFLOW;
+    int64_t rows = 0;  // one block per (stream, row)
+    if (!mul_ok(S, n_rows, &rows) || rows >= (int64_t)UINT32_MAX) return SIXI_E_INTEGER_OVERFLOW;
     if (view_span(o, D * 4) < 0 || view_span(g, 2 * D * 4) < 0) return SIXI_E_INTEGER_OVERFLOW;
     if (!rows_disjoint(o, D * 4)) return SIXI_E_INVALID_ARGUMENT;
     if (!rows16(o) || !rows16(g)) return SIXI_E_ALIGNMENT;

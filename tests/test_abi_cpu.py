@@ -238,6 +238,7 @@ def _prologue_params(S=2, R=16, H=24, Hkv=4, D=256, n_cells=4096, cache_type=sa.
     (lambda p: p.q_out.nb.__setitem__(2, 512), sa.E_INVALID_ARGUMENT),         # q-heads would alias
     (lambda p: p.k_cache.nb.__setitem__(1, 64), sa.E_INVALID_ARGUMENT),        # cells would alias
     (lambda p: setattr(p.qg, "data", FAKE + 8), sa.E_ALIGNMENT),
+    (lambda p: setattr(p, "k_norm", FAKE + 4), sa.E_ALIGNMENT),
     (lambda p: setattr(p.k_cache, "data", FAKE + 2), sa.E_ALIGNMENT),          # f16 rows 16-B aligned
     (lambda p: p.k.nb.__setitem__(2, 1 << 62), sa.E_INTEGER_OVERFLOW),        # 15 rows of 2^62 bytes
 ])
