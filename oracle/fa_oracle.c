@@ -465,3 +465,50 @@ void oracle_fill_normal_f32(uint64_t seed, uint64_t seq, float mul, float* out, 
         if (i + 1 < n) out[i + 1] = (float)(rad * sin(two_pi * u2) * (double)mul);
     }
 }
+
+/* ---------------------------------------------------------------------------------------
+ * Gated-delta-rule recurrent verify: GdnOperator::step_token (src/core/core_execution.cpp:
+ * 254-335) for every row of every stream.  Per group g and state row h:
+ *   sk = sum_s S[h][s] k[s] (serial, :314-317), delta = beta (v[h] - sk) (:318),
+ *   S[h][s] = alpha S[h][s] + delta k[s], y[h] = sum_s S[h][s] q[s] (:319-329).
+ * The state kept is the one after snap rows: a copy is taken when that row is reached. */
+void oracle_gdn_verify(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                       float* state, float* y, int64_t S, int64_t n_rows, int64_t G, int64_t K, int64_t HD,
+                       const int32_t* q_len, const int32_t* snap, int decay_first) {
+    float* work = (float*)malloc((size_t)(G * HD * K) * sizeof(float));
+    if (!work) return;
+    for (int64_t s = 0; s < S; ++s) {
+        int64_t ql = q_len ? q_len[s] : n_rows;
+        ql = ql < 0 ? 0 : (ql > n_rows ? n_rows : ql);
+        int64_t sn = snap ? snap[s] : ql;
+        sn = sn < 0 ? 0 : (sn > ql ? ql : sn);
+        float* st = state + s * G * HD * K;
+        memcpy(work, st, (size_t)(G * HD * K) * sizeof(float));
+        for (int64_t t = 0; t < ql; ++t) {
+            const int64_t row = s * n_rows + t;
+            for (int64_t g = 0; g < G; ++g) {
+                const float* qg = q + (row * G + g) * K;
+                const float* kg = k + (row * G + g) * K;
+                const float* vg = v + (row * G + g) * HD;
+                const float a = alpha[row * G + g], b = beta[row * G + g];
+                float* yg = y + (row * G + g) * HD;
+                for (int64_t h = 0; h < HD; ++h) {
+                    float* rs = work + (g * HD + h) * K;
+                    float sk = 0.0f;
+                    for (int64_t c = 0; c < K; ++c) sk += rs[c] * kg[c];
+                    if (decay_first) sk *= a;
+                    const float delta = b * (vg[h] - sk);
+                    float acc = 0.0f;
+                    for (int64_t c = 0; c < K; ++c) {
+                        const float upd = a * rs[c] + delta * kg[c];
+                        rs[c] = upd;
+                        acc += upd * qg[c];
+                    }
+                    yg[h] = acc;
+                }
+            }
+            if (t + 1 == sn) memcpy(st, work, (size_t)(G * HD * K) * sizeof(float));
+        }
+    }
+    free(work);
+}

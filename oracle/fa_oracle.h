@@ -99,6 +99,16 @@ double   oracle_pcg32_uniform01(oracle_pcg32* r);   /* 53-bit: (u64 >> 11) * 2^-
 /* n N(0,1) draws (Box-Muller in float64, both outputs used), times `mul`, cast to f32 */
 void     oracle_fill_normal_f32(uint64_t seed, uint64_t seq, float mul, float* out, int64_t n);
 
+/* Gated-delta-rule recurrent verify (restates GdnOperator::step_token,
+ * src/core/core_execution.cpp:254-335, applied token by token as the reference's verify does,
+ * :823): dense arrays q, k [S][n_rows][G][K], v, y [S][n_rows][G][HD], alpha, beta
+ * [S][n_rows][G], state [S][G][HD][K] (updated in place to the state after snap[s] rows;
+ * NULL q_len / snap = n_rows / q_len).  decay_first multiplies sk by alpha (ggml's order).
+ * Sums run serially over the K columns in index order, as the reference's loops do. */
+void oracle_gdn_verify(const float* q, const float* k, const float* v, const float* alpha, const float* beta,
+                       float* state, float* y, int64_t S, int64_t n_rows, int64_t G, int64_t K, int64_t HD,
+                       const int32_t* q_len, const int32_t* snap, int decay_first);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,8 @@ def load() -> ctypes.CDLL:
         lib.oracle_pcg32_uniform01.argtypes = [ctypes.POINTER(Pcg32)]
         lib.oracle_pcg32_uniform01.restype = ctypes.c_double
         lib.oracle_fill_normal_f32.argtypes = [u64, u64, ctypes.c_float, vp, i64]
+        lib.oracle_gdn_verify.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, ctypes.c_int]
+        lib.oracle_gdn_verify.restype = None
         _lib = lib
     return _lib
 
@@ -250,6 +252,28 @@ def attn_gate(out: np.ndarray, qg: np.ndarray, q_len: Optional[Sequence[int]] = 
         for s in range(out.shape[0]):
             res[s, int(q_len[s]):] = out[s, int(q_len[s]):]
     return res
+
+
+def gdn_verify(q: np.ndarray, k: np.ndarray, v: np.ndarray, alpha: np.ndarray, beta: np.ndarray,
+               state: np.ndarray, q_len: Optional[Sequence[int]] = None, snap: Optional[Sequence[int]] = None,
+               decay_first: bool = False):
+    """The reference's gated-delta-rule step (GdnOperator::step_token,
+    src/core/core_execution.cpp:254-335) over every row of every stream (fa_oracle.c).
+    ``q/k[S, n_rows, G, K]``, ``v[S, n_rows, G, HD]``, ``alpha/beta[S, n_rows, G]``,
+    ``state[S, G, HD, K]``.  Returns (y[S, n_rows, G, HD] with NaN past q_len, the state after
+    snap[s] rows)."""
+    q, k, v, alpha, beta = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v, alpha, beta))
+    S, n_rows, G, K = q.shape
+    HD = v.shape[-1]
+    st = np.ascontiguousarray(state, dtype=np.float32).copy()
+    y = np.full((S, n_rows, G, HD), np.nan, dtype=np.float32)
+    ql = None if q_len is None else np.ascontiguousarray(q_len, dtype=np.int32)
+    sn = None if snap is None else np.ascontiguousarray(snap, dtype=np.int32)
+    load().oracle_gdn_verify(q.ctypes.data, k.ctypes.data, v.ctypes.data, alpha.ctypes.data, beta.ctypes.data,
+                             st.ctypes.data, y.ctypes.data, S, n_rows, G, K, HD,
+                             ql.ctypes.data if ql is not None else None, sn.ctypes.data if sn is not None else None,
+                             1 if decay_first else 0)
+    return y, st
 
 
 def fill_normal(seed: int, seq: int, n: int, mul: float = 1.0) -> np.ndarray:

@@ -1,8 +1,8 @@
 """Builds the in-tree shared libraries of the MI355X attention path.
 
     lib/libsixi_attn.so   gfx950 HIP kernels + the C ABIs of include/sixi_attn.h,
-                          include/sixi_kv.h, include/sixi_plan.h and
-                          include/sixi_layer.h (hipcc)
+                          include/sixi_kv.h, include/sixi_plan.h,
+                          include/sixi_layer.h and include/sixi_gdn.h (hipcc)
     lib/libsixi_synth.so  seeded synthetic workload generator used by bench.py and tests (g++)
 
 Run as ``python sixi-asi_amd/build.py`` or through ``__graft_entry__.build()``.  Every call
@@ -37,7 +37,8 @@ HIP_FLAGS = [
     f"-I{CSRC}",
 ]
 HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "fa_q8_stage.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
-               "sixi_plan.cpp", "layer_prologue.hip", "sixi_layer_abi.cpp"]
+               "sixi_plan.cpp", "layer_prologue.hip", "sixi_layer_abi.cpp",
+               "gdn_verify.hip", "sixi_gdn_abi.cpp"]
 
 
 def _hipcc() -> str:

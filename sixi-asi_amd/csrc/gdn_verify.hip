@@ -1,0 +1,176 @@
+// gdn_verify.hip -- the gated-delta-rule recurrent verify: q_len[s] tokens of every stream
+// through that stream's state of one linear-attention layer, in one launch.
+//
+// Per token, per group g and state row h (src/core/core_execution.cpp:254-335, the reference's
+// GdnOperator::step_token; src/cuda/sixi_kernels.cu:241-281 is its CUDA twin):
+//   sk = sum_s S[h][s] k[s]    (times alpha first with SIXI_GDN_DECAY_FIRST, ggml's order)
+//   delta = beta * (v[h] - sk);   S[h][s] = alpha S[h][s] + delta k[s];   y[h] = sum_s S[h][s] q[s]
+// The reference runs one launch per token and stream with the state in HBM; here one work-group
+// owns the Hd x K state of one (stream, group) in registers for the whole block, so the state is
+// read once and written once (at the snapshot row), and each token costs 3 Hd K FMAs on chip.
+//
+// Mapping (256 threads): a thread holds R consecutive state rows x C = 16 consecutive columns;
+// the TPR = K/16 lanes that share the rows form a row group (adjacent lanes), whose partial
+// dot products are summed by xor shuffles.  The block's tokens are staged through LDS TC at a
+// time (q, k, v, alpha, beta of TC rows); every lane of a row group reads the same q/k columns,
+// so those LDS reads are broadcasts.  y leaves from the row group's first lane as R floats.
+//
+// Roofline: the state dominates the bytes (2 * 4 Hd K per group and stream: read + write);
+// each token adds 3 Hd K FMAs, so a block of n rows does 3n/8 FMA per state byte moved --
+// a 16-row verify block is VALU-bound on gfx950's FP32 rate (packed FP32 is not used).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gdn_internal.hpp"
+
+namespace sixi {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kC = 16;   // state columns per thread
+constexpr int kTC = 16;  // tokens staged per pass
+
+template <int K, int HD>
+struct GdnShape {
+    static constexpr int TPR = K / kC;         // lanes per row group
+    static constexpr int GROUPS = 256 / TPR;   // row groups per block
+    static constexpr int R = HD / GROUPS;      // state rows per thread
+    static_assert(R >= 1 && GROUPS * R == HD, "shape");
+};
+
+template <int TPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < TPR; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+template <int K, int HD, bool DECAY_FIRST>
+__global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
+    using Sh = GdnShape<K, HD>;
+    constexpr int R = Sh::R, TPR = Sh::TPR;
+    __shared__ f32x4 lq[kTC][K / 4], lk[kTC][K / 4];
+    __shared__ float lv[kTC][HD], la[kTC], lb[kTC];
+
+    const int g = (int)(blockIdx.x % (unsigned)a.G);
+    const int s = (int)(blockIdx.x / (unsigned)a.G);
+    const int tid = threadIdx.x;
+    const int part = tid % TPR;           // column block: columns part*16 .. part*16+15
+    const int row0 = (tid / TPR) * R;     // first state row of the thread
+    int ql = a.q_len ? a.q_len[s] : a.n_rows;
+    ql = ql < 0 ? 0 : (ql > a.n_rows ? a.n_rows : ql);
+    int snap = a.snap ? a.snap[s] : ql;
+    snap = snap < 0 ? 0 : (snap > ql ? ql : snap);
+
+    float st[R][kC];
+    const char* sin_base = a.s_in + (int64_t)g * a.si_nb2 + (int64_t)s * a.si_nb3 + part * kC * 4;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int u = 0; u < kC / 4; ++u) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(sin_base + (int64_t)(row0 + r) * a.si_nb1 + 16 * u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) st[r][4 * u + e] = x[e];
+        }
+    char* sout_base = a.s_out + (int64_t)g * a.so_nb2 + (int64_t)s * a.so_nb3 + part * kC * 4;
+    auto write_state = [&]() {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int u = 0; u < kC / 4; ++u)
+                *reinterpret_cast<f32x4*>(sout_base + (int64_t)(row0 + r) * a.so_nb1 + 16 * u) =
+                    f32x4{st[r][4 * u], st[r][4 * u + 1], st[r][4 * u + 2], st[r][4 * u + 3]};
+    };
+    if (snap == 0) write_state();
+
+    for (int t0 = 0; t0 < ql; t0 += kTC) {
+        const int nt = ql - t0 < kTC ? ql - t0 : kTC;
+        // stage q, k (K/4 vectors per row), v (HD/4), alpha, beta of rows t0 .. t0+nt-1
+        for (int i = tid; i < nt * (K / 4); i += 256) {
+            const int t = i / (K / 4), c = i % (K / 4);
+            const int64_t off = (int64_t)g * a.q_nb1 + (int64_t)(t0 + t) * a.q_nb2 + (int64_t)s * a.q_nb3 + 16 * c;
+            lq[t][c] = *reinterpret_cast<const f32x4*>(a.q + off);
+            const int64_t offk = (int64_t)g * a.k_nb1 + (int64_t)(t0 + t) * a.k_nb2 + (int64_t)s * a.k_nb3 + 16 * c;
+            lk[t][c] = *reinterpret_cast<const f32x4*>(a.k + offk);
+        }
+        for (int i = tid; i < nt * (HD / 4); i += 256) {
+            const int t = i / (HD / 4), c = i % (HD / 4);
+            const f32x4 x = *reinterpret_cast<const f32x4*>(a.v + (int64_t)g * a.v_nb1 + (int64_t)(t0 + t) * a.v_nb2 +
+                                                            (int64_t)s * a.v_nb3 + 16 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) lv[t][4 * c + e] = x[e];
+        }
+        if (tid < nt) {
+            la[tid] = *reinterpret_cast<const float*>(a.alpha + (int64_t)g * a.a_nb0 + (int64_t)(t0 + tid) * a.a_nb1 +
+                                                      (int64_t)s * a.a_nb2);
+            lb[tid] = *reinterpret_cast<const float*>(a.beta + (int64_t)g * a.b_nb0 + (int64_t)(t0 + tid) * a.b_nb1 +
+                                                      (int64_t)s * a.b_nb2);
+        }
+        __syncthreads();
+        for (int t = 0; t < nt; ++t) {
+            float kv[kC], qv[kC];
+#pragma unroll
+            for (int u = 0; u < kC / 4; ++u) {
+                const f32x4 x = lk[t][part * (kC / 4) + u], y = lq[t][part * (kC / 4) + u];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kv[4 * u + e] = x[e];
+                    qv[4 * u + e] = y[e];
+                }
+            }
+            const float al = la[t], be = lb[t];
+            float yo[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float sk = 0.0f;
+#pragma unroll
+                for (int c = 0; c < kC; ++c) sk += st[r][c] * kv[c];
+                sk = group_sum<TPR>(sk);
+                if (DECAY_FIRST) sk *= al;
+                const float delta = be * (lv[t][row0 + r] - sk);
+                float yv = 0.0f;
+#pragma unroll
+                for (int c = 0; c < kC; ++c) {
+                    st[r][c] = al * st[r][c] + delta * kv[c];
+                    yv += st[r][c] * qv[c];
+                }
+                yo[r] = group_sum<TPR>(yv);
+            }
+            if (part == 0) {
+                char* yp = a.y + (int64_t)g * a.y_nb1 + (int64_t)(t0 + t) * a.y_nb2 + (int64_t)s * a.y_nb3 + row0 * 4;
+                if constexpr (R == 4)
+                    *reinterpret_cast<f32x4*>(yp) = f32x4{yo[0], yo[1], yo[2], yo[3]};
+                else
+#pragma unroll
+                    for (int r = 0; r < R; ++r) reinterpret_cast<float*>(yp)[r] = yo[r];
+            }
+            if (t0 + t + 1 == snap) write_state();
+        }
+        __syncthreads();  // the next pass overwrites the staged rows
+    }
+}
+
+template <int K, int HD>
+hipError_t launch_shape(const GdnArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)((int64_t)a.S * a.G)), block(256);
+    if (a.decay_first)
+        hipLaunchKernelGGL((gdn_verify_kernel<K, HD, true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((gdn_verify_kernel<K, HD, false>), grid, block, 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gdn_verify(const GdnArgs& a, hipStream_t stream) {
+    if ((int64_t)a.S * a.G == 0) return hipSuccess;
+    if (a.K == 128 && a.HD == 128) return launch_shape<128, 128>(a, stream);
+    if (a.K == 128 && a.HD == 64) return launch_shape<128, 64>(a, stream);
+    if (a.K == 64 && a.HD == 128) return launch_shape<64, 128>(a, stream);
+    if (a.K == 64 && a.HD == 64) return launch_shape<64, 64>(a, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace sixi

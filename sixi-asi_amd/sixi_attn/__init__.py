@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "sixi_verify_plan",
     "sixi_qk_prologue",
     "sixi_attn_gate",
+    "sixi_gdn_verify",
 )
 
 
@@ -145,6 +146,27 @@ class SixiAttnGateParams(ctypes.Structure):
     ]
 
 
+class SixiGdnParams(ctypes.Structure):
+    _fields_ = [
+        ("q", SixiView),
+        ("k", SixiView),
+        ("v", SixiView),
+        ("alpha", SixiView),
+        ("beta", SixiView),
+        ("y", SixiView),
+        ("state_in", SixiView),
+        ("state_out", SixiView),
+        ("q_len", ctypes.c_void_p),
+        ("snap", ctypes.c_void_p),
+        ("flags", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
+GDN_DECAY_FIRST = 1
+
+
 class SixiVerifyStream(ctypes.Structure):
     _fields_ = [("stream", ctypes.c_int32), ("cached", ctypes.c_int32), ("real", ctypes.c_int32)]
 
@@ -196,6 +218,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.sixi_qk_prologue.restype = ctypes.c_int
     lib.sixi_attn_gate.argtypes = [ctypes.POINTER(SixiAttnGateParams)]
     lib.sixi_attn_gate.restype = ctypes.c_int
+    lib.sixi_gdn_verify.argtypes = [ctypes.POINTER(SixiGdnParams)]
+    lib.sixi_gdn_verify.restype = ctypes.c_int
     if path is None:
         _lib = lib
     return lib
@@ -467,6 +491,51 @@ def attn_gate(out, qg, q_len=None, stream=None, check=True) -> int:
     p.q_len = q_len.data_ptr() if q_len is not None else None
     p.stream = stream if stream is not None else torch.cuda.current_stream(out.device).cuda_stream
     rc = load_library().sixi_attn_gate(ctypes.byref(p))
+    if check and rc != OK:
+        raise SixiAttnError(rc, strerror(rc))
+    return rc
+
+
+def _plain_view(t) -> SixiView:
+    """ggml view of a torch tensor of up to 4 dims (the reversed shape, missing dims of 1)."""
+    import torch
+
+    es = t.element_size()
+    ne = list(reversed(t.shape)) + [1] * (4 - t.dim())
+    nb = [t.stride(i) * es for i in reversed(range(t.dim()))]
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1] if nb else es)
+    return make_view(t.data_ptr(), {torch.float32: TYPE_F32, torch.float16: TYPE_F16}[t.dtype], ne, nb)
+
+
+def gdn_verify_params(q, k, v, alpha, beta, y, state_in, state_out=None, q_len=None, snap=None,
+                      decay_first: bool = False, stream=None) -> SixiGdnParams:
+    """Parameters of ``sixi_gdn_verify`` for torch tensors: ``q/k[S, n_rows, G, K]``,
+    ``v/y[S, n_rows, G, HD]``, ``alpha/beta[S, n_rows, G]``, ``state[S, G, HD, K]`` f32."""
+    p = SixiGdnParams()
+    p.q, p.k, p.v, p.y = (_plain_view(t) for t in (q, k, v, y))
+    p.alpha, p.beta = _plain_view(alpha), _plain_view(beta)
+    p.state_in = _plain_view(state_in)
+    p.state_out = _plain_view(state_in if state_out is None else state_out)
+    p.q_len = q_len.data_ptr() if q_len is not None else None
+    p.snap = snap.data_ptr() if snap is not None else None
+    p.flags = GDN_DECAY_FIRST if decay_first else 0
+    p.stream = stream
+    return p
+
+
+def gdn_verify(q, k, v, alpha, beta, y, state_in, state_out=None, q_len=None, snap=None,
+               decay_first: bool = False, stream=None, check=True) -> int:
+    """The gated-delta-rule recurrent verify (include/sixi_gdn.h): rows j < q_len[s] of every
+    stream through its state -- the reference's GdnOperator::step_token
+    (src/core/core_execution.cpp:254-335) once per row -- writing y and the state after snap[s]
+    rows to ``state_out`` (``state_in`` itself when None: in place)."""
+    import torch
+
+    p = gdn_verify_params(q, k, v, alpha, beta, y, state_in, state_out, q_len, snap, decay_first, stream)
+    if p.stream is None:
+        p.stream = torch.cuda.current_stream(q.device).cuda_stream
+    rc = load_library().sixi_gdn_verify(ctypes.byref(p))
     if check and rc != OK:
         raise SixiAttnError(rc, strerror(rc))
     return rc

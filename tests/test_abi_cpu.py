@@ -272,3 +272,43 @@ def test_attn_gate_rejects(mutate, code):
     p.qg = sa.make_view(FAKE, sa.TYPE_F32, [2 * D, H, R, S], [4, 2 * D * 4, H * 2 * D * 4, R * H * 2 * D * 4])
     mutate(p)
     assert sa.load_library().sixi_attn_gate(ctypes.byref(p)) == code
+
+
+def _gdn_params(S=2, n=16, G=48, K=128, HD=128):
+    def v4(ne):
+        nb = [4]
+        for d in range(3):
+            nb.append(nb[-1] * ne[d])
+        return sa.make_view(FAKE, sa.TYPE_F32, ne, nb)
+    p = sa.SixiGdnParams()
+    p.q, p.k = v4([K, G, n, S]), v4([K, G, n, S])
+    p.v, p.y = v4([HD, G, n, S]), v4([HD, G, n, S])
+    p.alpha, p.beta = v4([G, n, S, 1]), v4([G, n, S, 1])
+    p.state_in = p.state_out = v4([K, HD, G, S])
+    p.flags = 0
+    return p
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda p: setattr(p, "flags", 4), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.q, "data", None), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.v, "type", sa.TYPE_F16), sa.E_INVALID_ARGUMENT),
+    (lambda p: (p.q.ne.__setitem__(0, 96), p.k.ne.__setitem__(0, 96)), sa.E_UNSUPPORTED),     # state size 96
+    (lambda p: p.k.ne.__setitem__(1, 16), sa.E_INVALID_ARGUMENT),               # groups differ
+    (lambda p: p.alpha.ne.__setitem__(1, 8), sa.E_INVALID_ARGUMENT),            # rows differ
+    (lambda p: p.state_out.ne.__setitem__(2, 24), sa.E_INVALID_ARGUMENT),
+    (lambda p: p.y.nb.__setitem__(1, 0), sa.E_INVALID_ARGUMENT),                # outputs would alias
+    (lambda p: setattr(p.state_out, "data", FAKE + 4096), sa.E_INVALID_ARGUMENT),  # overlaps the input state
+    (lambda p: setattr(p.q, "data", FAKE + 4), sa.E_ALIGNMENT),
+    (lambda p: setattr(p.beta, "data", FAKE + 2), sa.E_ALIGNMENT),
+    (lambda p: p.v.nb.__setitem__(2, 1 << 62), sa.E_INTEGER_OVERFLOW),
+])
+def test_gdn_verify_rejects(mutate, code):
+    p = _gdn_params()
+    mutate(p)
+    assert sa.load_library().sixi_gdn_verify(ctypes.byref(p)) == code
+
+
+def test_gdn_verify_without_streams_launches_nothing():
+    for K, HD in ((64, 64), (128, 128)):
+        assert sa.load_library().sixi_gdn_verify(ctypes.byref(_gdn_params(S=0, K=K, HD=HD))) == sa.OK
