@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT / "sixi-asi_amd"))
 METRIC = "verify-attn µs/layer & HBM GB/s (32 streams×16 tok, 8k ctx); prefill TFLOP/s"
 HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3  # published dense FP32 (vector) peak
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_verify_b32_counters.txt"
 
 
@@ -311,6 +312,45 @@ def time_layer(steps: int, warmup: int) -> dict:
     return res
 
 
+def time_gdn(steps: int, warmup: int) -> dict:
+    """The gated-delta-rule verify (include/sixi_gdn.h) of one linear-attention layer for the
+    verify batch: 32 streams x 16 rows, 48 value heads of 128 with 128-dim keys (the model's
+    ssm_time_step_rank / ssm_state_size).  Algorithmic bytes: the state read and written once
+    (2 * 4 * 128 * 128 per group and stream) plus q, k, v, y (4 * 128 each per row and group) and
+    alpha, beta; FLOPs: 3 * 2 * 128 * 128 per row and group (read, update, output)."""
+    import ctypes
+
+    import torch
+
+    import sixi_attn as sa
+
+    lib = sa.load_library()
+    S, n, G, K, HD = 32, 16, 48, 128, 128
+    q = torch.randn((S, n, G, K), device="cuda") / K ** 0.5
+    k = torch.nn.functional.normalize(torch.randn((S, n, G, K), device="cuda"), dim=-1)
+    v = torch.randn((S, n, G, HD), device="cuda")
+    al = torch.rand((S, n, G), device="cuda") * 0.2 + 0.8
+    be = torch.rand((S, n, G), device="cuda")
+    y = torch.empty((S, n, G, HD), device="cuda")
+    st = torch.randn((S, G, HD, K), device="cuda") * 0.5
+    p = sa.gdn_verify_params(q, k, v, al, be, y, st)
+
+    def run():
+        p.stream = torch.cuda.current_stream().cuda_stream
+        rc = lib.sixi_gdn_verify(ctypes.byref(p))
+        if rc != sa.OK:
+            raise sa.SixiAttnError(rc, sa.strerror(rc))
+
+    us = _graph_us(run, steps, warmup)
+    nbytes = S * G * (2 * 4 * HD * K + n * (4 * (2 * K + 2 * HD) + 8))
+    flops = S * n * G * 6 * HD * K
+    return {"workload": f"{S} streams x {n} rows, {G} groups, state {HD} x {K} f32, in place", "us": round(us, 2),
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
+            "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2), "flops": flops,
+            "frac_of_fp32_peak": round(flops / (us * 1e-6) / 1e12 / FP32_PEAK_TFLOPS, 4)}
+
+
 def prefill_only(steps: int, warmup: int) -> int:
     import sixi_attn as sa
 
@@ -326,7 +366,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "layer"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "layer", "gdn"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -345,6 +385,9 @@ def main() -> int:
         return prefill_only(args.steps, args.warmup)
     if args.workload == "layer":
         print(json.dumps(time_layer(max(8, args.steps), args.warmup)), flush=True)
+        return 0
+    if args.workload == "gdn":
+        print(json.dumps(time_gdn(max(8, args.steps), args.warmup)), flush=True)
         return 0
 
     import sixi_attn as sa
@@ -425,6 +468,12 @@ def main() -> int:
         except sa.SixiAttnError as e:
             result["layer_prologue_gate"] = {"unavailable": str(e)}
         _log(f"layer prologue/gate: {result['layer_prologue_gate']}")
+        # the gated-delta-rule verify of one linear-attention layer
+        try:
+            result["gdn_verify"] = time_gdn(max(40, args.steps // 2), max(5, args.warmup // 2))
+        except sa.SixiAttnError as e:
+            result["gdn_verify"] = {"unavailable": str(e)}
+        _log(f"gdn verify: {result['gdn_verify']}")
 
         # chunked causal prefill (2 chunks of 2048 rows on a 2048-cell cache)
         try:
