@@ -11,7 +11,7 @@
 //
 // Mapping (256 threads): a thread holds R consecutive state rows x C = 16 consecutive columns;
 // the TPR = K/16 lanes that share the rows form a row group (adjacent lanes), whose partial
-// dot products are summed by xor shuffles.  The block's tokens are staged through LDS TC at a
+// dot products are summed by DPP lane moves (ds_bpermute shuffles measured 94 against 83 us).  The block's tokens are staged through LDS TC at a
 // time (q, k, v, alpha, beta of TC rows); every lane of a row group reads the same q/k columns,
 // so those LDS reads are broadcasts.  y leaves from the row group's first lane as R floats.
 //
@@ -40,10 +40,21 @@ struct GdnShape {
     static_assert(R >= 1 && GROUPS * R == HD, "shape");
 };
 
+// DPP lane moves (GFX9 encodings): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror (lane i of
+// each 8-lane half-row reads lane 7 - i)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the TPR (4 or 8) adjacent lanes of a row group, the total in every lane of it: two quad
+// swaps give each quad its sum, and for 8 lanes the half-row mirror adds the other quad's.
 template <int TPR>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = 1; o < TPR; o <<= 1) v += __shfl_xor(v, o, 64);
+    static_assert(TPR == 4 || TPR == 8, "row groups of 4 or 8 lanes");
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    if constexpr (TPR == 8) v += dpp<0x141>(v);
     return v;
 }
 

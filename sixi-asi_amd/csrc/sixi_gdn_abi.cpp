@@ -73,6 +73,8 @@ int resolve(const sixi_gdn_params* p, sixi::GdnArgs* out) {
         if (a0 < b1 && b0 < a1) return SIXI_E_INVALID_ARGUMENT;
     }
     if (!rows16(q) || !rows16(k) || !rows16(v) || !rows16(y) || !rows16(si) || !rows16(so)) return SIXI_E_ALIGNMENT;
+    // state rows are whole rows of K values apart
+    if (si.nb[1] < K * 4) return SIXI_E_INVALID_ARGUMENT;
     if (!aligned(al.data, 4) || !aligned(be.data, 4)) return SIXI_E_ALIGNMENT;
     for (int d = 0; d < 3; ++d)
         if (al.nb[d] % 4 || be.nb[d] % 4) return SIXI_E_ALIGNMENT;

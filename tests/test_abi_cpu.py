@@ -312,3 +312,10 @@ def test_gdn_verify_rejects(mutate, code):
 def test_gdn_verify_without_streams_launches_nothing():
     for K, HD in ((64, 64), (128, 128)):
         assert sa.load_library().sixi_gdn_verify(ctypes.byref(_gdn_params(S=0, K=K, HD=HD))) == sa.OK
+
+
+def test_gdn_verify_input_state_rows_must_not_overlap():
+    p = _gdn_params()
+    p.state_out = sa.make_view(FAKE + (1 << 40), sa.TYPE_F32, list(p.state_in.ne), list(p.state_in.nb))
+    p.state_in.nb[1] = 256                       # input rows of 512 bytes 256 apart
+    assert sa.load_library().sixi_gdn_verify(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT
