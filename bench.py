@@ -451,6 +451,13 @@ def main() -> int:
                 de = wl.to_device(he)
                 mse, pere = time_calls(fa, we, de, max(20, args.steps // 2), max(5, args.warmup // 2))
                 extra[name] = summarize(we, mse, pere)
+                # the eager figure includes the host's issue time when a call is shorter than it
+                # (decode); GPU time per call from HIP-graph replays of the same call
+                oute = torch.empty((we.S, we.n_q, we.H, we.D), dtype=torch.float32, device="cuda")
+                usg = _graph_us(lambda: fa(de["q"], de["k"], de["v"], oute, kv_len=de["kv_len"], q_len=de["q_len"],
+                                           mask_mode=we.mask_mode), max(40, args.steps // 2), 3)
+                extra[name]["us_graph"] = round(usg, 2)
+                extra[name]["GBps_graph"] = round(we.bytes() / (usg * 1e-6) / 1e9, 1)
                 del de
             except sa.SixiAttnError as e:
                 extra[name] = {"unavailable": str(e)}

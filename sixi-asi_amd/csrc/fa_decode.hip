@@ -9,8 +9,8 @@
 // lengths balances over the CUs and a work-group that has to start an extra segment gets
 // correspondingly fewer tiles.  The share of work-group p inside a segment is a piece.  A
 // work-group that owns a whole segment writes the rows directly; every other piece leaves
-// (m, l, O) in a workspace slot, and a second launch (decode_merge) combines the pieces of
-// each split segment in a fixed order.  The kernel boundary orders the two launches, so
+// (m, l, O) in a workspace slot, and a second launch combines the pieces of each split
+// segment in a fixed order (decode_merge_rows; decode_merge_pieces for segments of many pieces).  The kernel boundary orders the two launches, so
 // neither needs device-scope fences or atomics.
 //
 // Two kernels share this split:
@@ -54,7 +54,7 @@ constexpr int kTile = kDecodeTile;  // 16 cells
 constexpr int kQ8Row = 136;         // bytes of one q8_0 head row (4 blocks of 34)
 constexpr int kQ8Dma = 9;           // dword LDS-DMA loads covering 16 q8_0 rows (2304 >= 2176 B)
 constexpr float kLazyLog2 = 8.0f;   // headroom (log2 units) before the exponent reference moves
-constexpr int kMaxPieces = 16;      // target bound on the pieces of one full-length segment
+constexpr int kMaxPieces = 64;      // target bound on the pieces of one full-length segment
 
 enum { MODE_FAST = 0, MODE_GENERIC = 1 };
 
@@ -1134,7 +1134,7 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
             pc.te = __builtin_amdgcn_readfirstlane((int)(xe - t0));
             pc.nt_seg = __builtin_amdgcn_readfirstlane(ct - a.seg_cost);
             pc.slot = __builtin_amdgcn_readfirstlane((int)((int64_t)s * Hkv + g + pt.p_log));
-            // the segment's first and last piece tell decode_merge which slots to combine
+            // the segment's first and last piece tell the merge which slots to combine
             if (threadIdx.x == 0) {
                 const int64_t seg = (int64_t)s * Hkv + g;
                 if (pc.tb == 0) a.seg_pieces[2 * seg] = pt.p_log;
@@ -1164,12 +1164,77 @@ void decode_wide(FaArgs a, int causal) {
     for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
 }
 
-// Combines the pieces of every segment that more than one work-group touched, in the order
-// of the work-groups.  grid = (S*Hkv segments, row blocks of 8); 256 threads = 8 rows x 32
+// Combines the pieces of every segment that more than one work-group touched, for segments of
+// many pieces (a few long streams: single-stream decode and verify).  grid = (S*Hkv segments,
+// rows); 256 threads = PG piece groups x D/4 threads of four dims.  Group pg folds
+// pieces p_first + pg, + PG, ... in increasing order, eight loads per step, all independent, so
+// up to 8 PG pieces (64 at 128-dim heads) cost one memory latency; group 0 then folds the
+// groups' partials in group order through LDS.  The order is fixed, so the result is
+// deterministic.  The split kernel recorded the segment's first and last piece; the stream
+// extents come in the same round trip.
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_pieces(FaArgs a, int rows_slot) {
+    constexpr int TPR = D / 4;     // threads per piece group (4 dims each)
+    constexpr int PG = 256 / TPR;  // piece groups: 8 (128-dim heads) or 4 (256)
+    __shared__ f32x4 lo[PG][TPR];
+    __shared__ float lm[PG], ll[PG];
+    const int64_t k = blockIdx.x;
+    const int s = (int)(k / a.Hkv);
+    const int g = (int)(k % a.Hkv);
+    const StreamDims sd = stream_dims(a, s);
+    const int p_first = a.seg_pieces[2 * k], p_last = a.seg_pieces[2 * k + 1];
+    const int row = blockIdx.y;
+    if (row >= a.Gr * sd.ql) return;  // (a segment without rows has stale entries)
+    if (p_first == p_last) return;    // written whole by its only work-group
+
+    const int pg = (int)(threadIdx.x / TPR), c = (int)(threadIdx.x % TPR);
+    const int d0 = c * 4;
+    const float* base = a.part + k * a.slot_floats;
+    float M = neg_inf(), L = 0.0f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int p0 = p_first + pg; p0 <= p_last; p0 += 8 * PG) {
+        f32x4 ov[8];
+        float mv[8], lv[8];
+        u32x2 hv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int p = p0 + PG * u <= p_last ? p0 + PG * u : p_last;
+            const float* sl = base + (int64_t)p * a.slot_floats;
+            hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * (2 * D) + d0 * 2);
+            mv[u] = sl[(int64_t)rows_slot * (D / 2) + row];
+            lv[u] = sl[(int64_t)rows_slot * (D / 2 + 1) + row];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const f16x4 h = __builtin_bit_cast(f16x4, hv[u]);
+            ov[u] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]} * lv[u];  // back to O = l * (O/l)
+            if (p0 + PG * u <= p_last) merge_row<1>(M, L, &o, mv[u], lv[u], &ov[u]);
+        }
+    }
+    lo[pg][c] = o;
+    if (c == 0) {
+        lm[pg] = M;
+        ll[pg] = L;
+    }
+    __syncthreads();
+    if (pg != 0) return;
+#pragma unroll
+    for (int q = 1; q < PG; ++q) {
+        const f32x4 oq = lo[q][c];
+        merge_row<1>(M, L, &o, lm[q], ll[q], &oq);  // a group without pieces adds l = 0, o = 0
+    }
+    const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+    const int j = row / a.Gr;
+    const int h = g * a.G + a.hoff + row % a.Gr;
+    st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
+}
+
+// Combines the pieces of every segment that more than one work-group touched, for segments of
+// few pieces (at most eight on average), in the order of the work-groups.  grid = (S*Hkv segments, row blocks of 8); 256 threads = 8 rows x 32
 // four-dim chunks, so every (row, chunk) is one thread.  The split kernel recorded the
 // segment's first and last piece; the stream extents come in the same round trip.
 template <int D>
-__global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
+__global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot) {
     constexpr int TPR = D / 4;  // threads per row (4 dims each)
     const int64_t k = blockIdx.x;
     const int s = (int)(k / a.Hkv);
@@ -1211,6 +1276,21 @@ __global__ __launch_bounds__(256) void decode_merge(FaArgs a, int rows_slot) {
     st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
 }
 
+// The merge form for a split launch: the piece-parallel one once segments average more than
+// eight pieces (the row-block form then needs several dependent load steps per row).
+template <int D>
+void launch_merge(const FaArgs& a, int rows_slot, hipStream_t stream) {
+    if ((int64_t)a.P > 8 * (int64_t)a.S * a.Hkv) {
+        hipLaunchKernelGGL(decode_merge_pieces<D>, dim3((unsigned)(a.S * a.Hkv), (unsigned)rows_slot), dim3(256), 0,
+                           stream, a, rows_slot);
+    } else {
+        const int rows_wg = 256 / (D / 4);
+        hipLaunchKernelGGL(decode_merge_rows<D>,
+                           dim3((unsigned)(a.S * a.Hkv), (unsigned)((rows_slot + rows_wg - 1) / rows_wg)), dim3(256), 0,
+                           stream, a, rows_slot);
+    }
+}
+
 template <int NTW, int RS, int D>
 hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
     const dim3 grid(a.P), block(RS * wide_lanes<RS, D>() * 64);
@@ -1220,10 +1300,7 @@ hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t st
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_FAST, D>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int rows_slot = NTW * RS * 16;
-    const int rows_wg = 256 / (D / 4);
-    hipLaunchKernelGGL(decode_merge<D>, dim3((unsigned)(a.S * a.Hkv), (unsigned)((rows_slot + rows_wg - 1) / rows_wg)),
-                       dim3(256), 0, stream, a, rows_slot);
+    launch_merge<D>(a, NTW * RS * 16, stream);
     return hipGetLastError();
 }
 
@@ -1236,9 +1313,7 @@ hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stre
         hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_FAST>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int rows_slot = NTW * 16;
-    hipLaunchKernelGGL(decode_merge<128>, dim3((unsigned)(a.S * a.Hkv), (unsigned)(rows_slot / 8)), dim3(256), 0, stream,
-                       a, rows_slot);
+    launch_merge<128>(a, NTW * 16, stream);
     return hipGetLastError();
 }
 
