@@ -432,7 +432,7 @@ def main() -> int:
         "verify_tflops": head["TFLOPs"],
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_wide<3,2,0,128> + decode_merge (one sixi_attn_forward call; "
+            "kernel": "decode_wide<3,2,0,128> + decode_merge_rows<128> (one sixi_attn_forward call; "
                       "achieved = algorithmic bytes / call time)",
             "achieved": gbs,
             "peak": HBM_PEAK_GBS,
