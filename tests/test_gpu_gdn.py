@@ -99,3 +99,14 @@ def test_long_block_several_staging_passes():
 
 def test_no_lengths():
     _run(*_inputs(2, 3, 3, 128, 128, 41), label="no lengths")
+
+
+def test_extreme_gates():
+    # alpha 0 resets the state to the row's write, alpha 1 keeps it; beta 0 writes nothing, beta 1
+    # writes the whole correction
+    q, k, v, al, be, S0 = _inputs(2, 8, 6, 128, 128, 51)
+    al[:, ::2] = 0.0
+    al[:, 1::4] = 1.0
+    be[:, :, ::3] = 0.0
+    be[:, :, 1::3] = 1.0
+    _run(q, k, v, al, be, S0, q_len=[8, 5], snap=[8, 4], label="alpha 0/1, beta 0/1")

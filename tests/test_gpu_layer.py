@@ -149,6 +149,22 @@ def test_prologue_without_lengths():
     _run_prologue(2, 4, 4, 2, 256, 8, None, None, False, 256, 31, "no lengths, full rotation")
 
 
+@pytest.mark.parametrize("q8", [False, True])
+def test_prologue_zero_rows(q8, monkeypatch):
+    # rows of zeros (pad rows of a ragged block): the norm divides by sqrt(eps) and gives zeros
+    real = _inputs
+
+    def zeroed(S, R, H, Hkv, D, seed):
+        qg, k, v, wq, wk = real(S, R, H, Hkv, D, seed)
+        qg[:, 1::2] = 0.0
+        k[:, 1::2] = 0.0
+        v[:, 1::2] = 0.0
+        return qg, k, v, wq, wk
+
+    monkeypatch.setattr(sys.modules[__name__], "_inputs", zeroed)
+    _run_prologue(2, 6, 24, 4, 256, 64, [10, 40], [6, 4], q8, 64, 61, "zero rows")
+
+
 @pytest.mark.parametrize("D", [128, 256])
 def test_gate(D):
     rng = np.random.default_rng(41 + D)
