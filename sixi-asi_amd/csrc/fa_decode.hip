@@ -1291,8 +1291,14 @@ void launch_merge(const FaArgs& a, int rows_slot, hipStream_t stream) {
     }
 }
 
+// A launch writes partial slots of `rows` rows of D dims: the workspace must hold them.
+inline bool slot_fits(const FaArgs& a, int rows, int D) {
+    return (int64_t)rows * (D / 2 + 2) <= a.slot_floats;
+}
+
 template <int NTW, int RS, int D>
 hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
+    if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(RS * wide_lanes<RS, D>() * 64);
     if (generic)
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_GENERIC, D>), grid, block, 0, stream, a, causal);
@@ -1306,6 +1312,7 @@ hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t st
 
 template <int NTW, int KV>
 hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
+    if (!slot_fits(a, NTW * 16, 128)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(Shape<KV>::waves * 64);
     if (generic)
         hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
@@ -1339,12 +1346,11 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
     if (head_dim == 256) {
         // 256-dim heads: every row count runs the 32-cell kernel (one or two row groups)
         if (kv_type != SIXI_TYPE_F16) return hipErrorNotSupported;
-        // at most two row tiles per wave (three spill the 256-dim accumulators); 96 rows run as
-        // three row groups of one lane
+        // at most two row tiles per wave (three spill the 256-dim accumulators), so 33-48 rows
+        // run as 64 (decode_row_tiles maps 3 to 4); 96 rows run as three row groups of one lane
         switch (row_tiles) {
             case 1: return launch_wide<1, 1, 256>(a, generic, causal, stream);
             case 2: return launch_wide<2, 1, 256>(a, generic, causal, stream);
-            case 3:
             case 4: return launch_wide<2, 2, 256>(a, generic, causal, stream);
             case 6: return launch_wide<2, 3, 256>(a, generic, causal, stream);
             default: return hipErrorNotSupported;

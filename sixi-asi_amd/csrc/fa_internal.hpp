@@ -98,11 +98,14 @@ constexpr int kWideSegCost = 12;
 inline int decode_seg_cost(int kv_type, int row_tiles, int head_dim) {
     return decode_wide_kernel(kv_type, row_tiles, head_dim) ? kWideSegCost : 0;
 }
-// Row tiles the decode kernel runs for `rows` = G * n_q rows: up to 3 per wave; beyond
-// that two row groups of equal size (so 5 tiles run as 6).
-inline int decode_row_tiles(int64_t rows) {
+// Row tiles the decode kernel runs for `rows` = G * n_q rows, i.e. exactly the rows of the
+// launched kernel's partial slots (16 per tile): 128-dim heads run up to 3 per wave, beyond
+// that two row groups of equal size (so 5 tiles run as 6); 256-dim heads hold at most two
+// per wave, so 3 tiles run as two row groups of two.
+inline int decode_row_tiles(int64_t rows, int head_dim) {
     const int rt = (int)((rows + 15) / 16);
-    return rt <= 3 ? rt : 2 * ((rt + 1) / 2);
+    if (rt <= 2 || (rt == 3 && head_dim != 256)) return rt;
+    return 2 * ((rt + 1) / 2);
 }
 inline int64_t decode_slot_floats(int row_tiles, int head_dim) {
     // O/l rows [16*row_tiles][head_dim] f16 (head_dim/2 floats' worth), then m and l per row

@@ -57,6 +57,14 @@ int cu_count_cached() {
     return cached;
 }
 
+// Split-K workspace after the staging area: `slots` partial slots, then the (first, last)
+// piece of every segment.
+void splitk_layout(Plan& pl, int64_t slots) {
+    const int64_t segs = (int64_t)pl.a.S * pl.a.Hkv;
+    pl.seg_offset = align_up((size_t)(slots * pl.a.slot_floats) * sizeof(float), kWsAlign);
+    pl.ws_bytes = pl.stage_bytes + align_up(pl.seg_offset + (size_t)segs * 2 * sizeof(int32_t), kWsAlign);
+}
+
 // Resolves and validates a description.  Touches no device memory.
 int resolve(const sixi_attn_params* p, Plan* out) {
     if (!p || !out) return SIXI_E_INVALID_ARGUMENT;
@@ -193,12 +201,12 @@ int resolve(const sixi_attn_params* p, Plan* out) {
         }
     }
     if (pl.splitk) {
-        pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q);
+        pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q, pl.D);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles, pl.D);
-        const int64_t slots = S * Hkv + sixi::kMaxSplitGroups;
-        // partial slots, then (first, last) piece of every segment
-        pl.seg_offset = align_up((size_t)(slots * a.slot_floats) * sizeof(float), kWsAlign);
-        pl.ws_bytes = pl.stage_bytes + align_up(pl.seg_offset + (size_t)(S * Hkv) * 2 * sizeof(int32_t), kWsAlign);
+        a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles, pl.D);
+        a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles, pl.D);
+        // slot indices run up to S*Hkv + P - 2 for a launch of P <= kMaxSplitGroups work-groups
+        splitk_layout(pl, S * Hkv + sixi::kMaxSplitGroups);
     } else {
         // the prefill kernel keeps everything on chip; a token workspace keeps the contract uniform
         if (S * H * ((n_q + 127) / 128) > (int64_t)INT32_MAX) return SIXI_E_UNSUPPORTED;
@@ -206,6 +214,53 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     }
     *out = pl;
     return SIXI_OK;
+}
+
+// Work-groups of the launch: the split-K grid, or (prefill) the CU count its order needs.
+int launch_groups(const Plan& pl) {
+    return pl.splitk ? sixi::decode_num_groups(pl.a, cu_count_cached(), pl.row_tiles) : cu_count_cached();
+}
+
+// Launches a resolved call on `ws` (laid out as pl says).
+int run(Plan& pl, char* ws, hipStream_t stream) {
+    FaArgs& a = pl.a;
+    hipError_t e;
+    if (pl.q8_stage) {
+        sixi::Q8StageArgs st{};
+        st.q = a.q; st.q_nb1 = a.q_nb1; st.q_nb2 = a.q_nb2; st.q_nb3 = a.q_nb3;
+        st.q_es = a.q_es; st.q_f16 = a.q_f16;
+        st.k = a.k; st.k_nb1 = a.k_nb1; st.k_nb2 = a.k_nb2; st.k_nb3 = a.k_nb3;
+        st.v = a.v; st.v_nb1 = a.v_nb1; st.v_nb2 = a.v_nb2; st.v_nb3 = a.v_nb3;
+        st.kv_len = a.kv_len; st.q_len = a.q_len;
+        st.S = a.S; st.H = a.H; st.Hkv = a.Hkv; st.n_q = a.n_q; st.n_kv = a.n_kv; st.D = pl.D;
+        st.k16 = ws + pl.stage_k; st.v16 = ws + pl.stage_v; st.q16 = ws + pl.stage_q;
+        e = sixi::launch_q8_stage(st, stream);
+        if (e != hipSuccess) return SIXI_E_BACKEND;
+        const int64_t row = (int64_t)pl.D * 2;
+        a.q = st.q16; a.q_nb2 = row; a.q_nb1 = (int64_t)a.H * row; a.q_nb3 = (int64_t)a.n_q * a.H * row;
+        a.q_es = 2; a.q_f16 = 1;
+        a.k = st.k16; a.k_nb2 = row; a.k_nb1 = (int64_t)a.Hkv * row; a.k_nb3 = (int64_t)a.n_kv * a.Hkv * row;
+        a.v = st.v16; a.v_nb2 = row; a.v_nb1 = a.k_nb1; a.v_nb3 = a.k_nb3;
+        ws += pl.stage_bytes;
+    }
+    a.part = reinterpret_cast<float*>(ws);
+    a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
+    a.P = launch_groups(pl);
+    if (pl.splitk) {
+        a.xcd_remap = 0;
+        e = hipSuccess;
+        // one launch pair per head subset, ordered on the stream (they share the workspace)
+        for (int h0 = 0; h0 < a.G && e == hipSuccess; h0 += pl.heads_per_launch) {
+            a.hoff = h0;
+            a.Gr = std::min(pl.heads_per_launch, a.G - h0);
+            e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D,
+                                    sixi::decode_row_tiles((int64_t)a.Gr * a.n_q, pl.D), stream);
+        }
+    } else {
+        e = sixi::launch_prefill(a, pl.kv_type, pl.mask_mode, pl.D, stream);
+    }
+    if (e == hipErrorNotSupported) return SIXI_E_UNSUPPORTED;
+    return e == hipSuccess ? SIXI_OK : SIXI_E_BACKEND;
 }
 
 }  // namespace
@@ -232,49 +287,7 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     if (rc != SIXI_OK) return rc;
     if (!p->workspace || p->workspace_bytes < pl.ws_bytes) return SIXI_E_OUT_OF_BOUNDS;
     if (!aligned(p->workspace, kWsAlign)) return SIXI_E_ALIGNMENT;
-    FaArgs& a = pl.a;
-    char* ws = static_cast<char*>(p->workspace);
-    hipStream_t stream = static_cast<hipStream_t>(p->stream);
-    hipError_t e;
-    if (pl.q8_stage) {
-        sixi::Q8StageArgs st{};
-        st.q = a.q; st.q_nb1 = a.q_nb1; st.q_nb2 = a.q_nb2; st.q_nb3 = a.q_nb3;
-        st.q_es = a.q_es; st.q_f16 = a.q_f16;
-        st.k = a.k; st.k_nb1 = a.k_nb1; st.k_nb2 = a.k_nb2; st.k_nb3 = a.k_nb3;
-        st.v = a.v; st.v_nb1 = a.v_nb1; st.v_nb2 = a.v_nb2; st.v_nb3 = a.v_nb3;
-        st.kv_len = a.kv_len; st.q_len = a.q_len;
-        st.S = a.S; st.H = a.H; st.Hkv = a.Hkv; st.n_q = a.n_q; st.n_kv = a.n_kv; st.D = pl.D;
-        st.k16 = ws + pl.stage_k; st.v16 = ws + pl.stage_v; st.q16 = ws + pl.stage_q;
-        e = sixi::launch_q8_stage(st, stream);
-        if (e != hipSuccess) return SIXI_E_BACKEND;
-        const int64_t row = (int64_t)pl.D * 2;
-        a.q = st.q16; a.q_nb2 = row; a.q_nb1 = (int64_t)a.H * row; a.q_nb3 = (int64_t)a.n_q * a.H * row;
-        a.q_es = 2; a.q_f16 = 1;
-        a.k = st.k16; a.k_nb2 = row; a.k_nb1 = (int64_t)a.Hkv * row; a.k_nb3 = (int64_t)a.n_kv * a.Hkv * row;
-        a.v = st.v16; a.v_nb2 = row; a.v_nb1 = a.k_nb1; a.v_nb3 = a.k_nb3;
-        ws += pl.stage_bytes;
-    }
-    a.part = reinterpret_cast<float*>(ws);
-    a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
-    if (pl.splitk) {
-        a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles, pl.D);
-        a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles, pl.D);
-        a.P = sixi::decode_num_groups(a, cu_count_cached(), pl.row_tiles);
-        a.xcd_remap = 0;
-        e = hipSuccess;
-        // one launch pair per head subset, ordered on the stream (they share the workspace)
-        for (int h0 = 0; h0 < a.G && e == hipSuccess; h0 += pl.heads_per_launch) {
-            a.hoff = h0;
-            a.Gr = std::min(pl.heads_per_launch, a.G - h0);
-            e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D,
-                                    sixi::decode_row_tiles((int64_t)a.Gr * a.n_q), stream);
-        }
-    } else {
-        a.P = cu_count_cached();  // the prefill grid order depends on the CU count
-        e = sixi::launch_prefill(a, pl.kv_type, pl.mask_mode, pl.D, stream);
-    }
-    if (e == hipErrorNotSupported) return SIXI_E_UNSUPPORTED;
-    return e == hipSuccess ? SIXI_OK : SIXI_E_BACKEND;
+    return run(pl, static_cast<char*>(p->workspace), static_cast<hipStream_t>(p->stream));
 }
 
 const char* sixi_attn_strerror(int code) {

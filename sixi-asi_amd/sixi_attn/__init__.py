@@ -270,7 +270,11 @@ def view_of(t, type_id: Optional[int] = None, head_dim: Optional[int] = None,
 class FlashAttnExt:
     """``ggml_flash_attn_ext`` over per-stream KV caches on one gfx950 GPU.
 
-    Keeps a device workspace (grown on demand) so repeated calls allocate nothing.
+    Keeps a device workspace (grown on demand) so repeated calls allocate nothing.  A buffer
+    that a larger call supersedes stays allocated for the life of the object, so a HIP graph
+    captured over an earlier call still owns the memory its kernels write.  A caller may
+    also pass its own ``workspace`` (a uint8 device tensor of at least
+    :meth:`workspace_bytes`), e.g. one sized once before capture.
     """
 
     def __init__(self, device=None):
@@ -279,6 +283,7 @@ class FlashAttnExt:
         self.lib = load_library()
         self.device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
         self._ws = None
+        self._retired = []  # superseded workspaces: graphs captured before a regrowth still use them
 
     def params(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
                scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None) -> SixiAttnParams:
@@ -315,11 +320,14 @@ class FlashAttnExt:
         import torch
 
         if self._ws is None or self._ws.numel() < nbytes:
+            if self._ws is not None:
+                self._retired.append(self._ws)
             self._ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
         return self._ws
 
     def __call__(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
-                 scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None, check=True) -> int:
+                 scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None, check=True,
+                 workspace=None) -> int:
         import torch
 
         p = self.params(q, k, v, out, kv_len, q_len, mask_mode, mask, scale, max_bias, logit_softcap,
@@ -329,9 +337,9 @@ class FlashAttnExt:
         n = ctypes.c_size_t(0)
         rc = self.lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n))
         if rc == OK:
-            ws = self._workspace(n.value)
+            ws = self._workspace(n.value) if workspace is None else workspace
             p.workspace = ws.data_ptr()
-            p.workspace_bytes = ws.numel()
+            p.workspace_bytes = ws.numel() * ws.element_size()
             rc = self.lib.sixi_attn_forward(ctypes.byref(p))
         if check and rc != OK:
             raise SixiAttnError(rc, strerror(rc))

@@ -71,6 +71,31 @@ def test_valid_descriptions_pass_and_size_a_workspace():
         assert n.value > 0 and n.value % 256 == 0
 
 
+def _launched_rows(rows, D):
+    """Rows of one partial slot of the split-K kernel launched for `rows` rows per kv-head
+    group: 16-row tiles; 128-dim heads run 1-3 tiles on the 16-cell kernel, then 64 or 96 rows
+    (two row groups); 256-dim heads run at most two tiles per wave, so 33-64 rows run as 64."""
+    t = -(-rows // 16)
+    if t <= 2 or (t == 3 and D == 128):
+        return 16 * t
+    return 64 if t <= 4 else 96
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_workspace_holds_the_launched_slots(D):
+    """The workspace has room for (S*Hkv + 2048) partial slots of the rows the launched kernel
+    writes: normalised rows in f16 (D/2 floats each) plus m and l."""
+    lib = sa.load_library()
+    for G, n_q in ((6, 1), (6, 2), (6, 5), (6, 6), (6, 7), (6, 8), (6, 10), (6, 13), (6, 16), (3, 16), (1, 33)):
+        S, Hkv = 3, 4
+        p = _params(S=S, n_q=n_q, H=G * Hkv, Hkv=Hkv, D=D)
+        n = ctypes.c_size_t(0)
+        assert lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n)) == sa.OK
+        rows = _launched_rows(G * n_q, D)
+        need = (S * Hkv + 2048) * rows * (D // 2 + 2) * 4
+        assert n.value >= need, (G, n_q, D, n.value, need)
+
+
 @pytest.mark.parametrize("mutate,code", [
     (lambda p: setattr(p, "flags", 1), sa.E_INVALID_ARGUMENT),
     (lambda p: setattr(p.q, "data", None), sa.E_INVALID_ARGUMENT),

@@ -59,15 +59,23 @@ def _slice_host(host, s, a, b):
 
 
 @pytest.mark.parametrize("name", ["prefill_chunk0", "prefill_chunk1"])
-def test_prefill_chunks_parity_on_row_slices(fa, name):
-    _say(f"config {name}")
+def test_prefill_chunks_parity_every_row(fa, name):
+    """All 2048 rows of the chunk against the oracle, on the whole and per 128-row block (the
+    prefill kernel's work-group), so a fault in one row block cannot hide in the aggregate."""
+    _say(f"config {name} (every row)")
     w = wl.config(name)
     host = wl.make_host(w, poison=True)
     dev = wl.to_device(host)
     got = _run(fa, w, dev)
-    for a, b in ((0, 96), (1000, 1100), (w.q_len[0] - 96, w.q_len[0])):
-        want = oracle.attention_for_workload(_slice_host(host, 0, a, b), w.kv_type)
-        _check(want[0], got[0, a:b], f"{name} rows [{a},{b})")
+    want = oracle.attention_for_workload(host, w.kv_type)
+    _check(want[0], got[0], f"{name} rows [0,{w.q_len[0]})")
+    for a in range(0, w.q_len[0], 128):
+        m = oracle.diff_metrics(want[0, a:a + 128], got[0, a:a + 128])
+        assert m["max_abs"] <= MAX_ABS and m["rel_l2"] <= REL_L2, (a, m)
+    # a row slice is the same block over a longer cache: the slice's oracle agrees
+    a, b = 1000, 1100
+    sl = oracle.attention_for_workload(_slice_host(host, 0, a, b), w.kv_type)
+    _check(sl[0], got[0, a:b], f"{name} rows [{a},{b}) as their own block")
 
 
 @pytest.mark.parametrize("kv_len,q_len,H,Hkv", [
