@@ -104,6 +104,18 @@ typedef struct sixi_attn_params {
  * written.  kv_len[s] is clamped to [0, n_kv - q_len[s]] on the device. */
 int sixi_attn_forward(const sixi_attn_params* p);
 
+/* sixi_attn_forward without a caller workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The call allocates nothing: its scratch is a fixed
+ * SIXI_ATTN_NOALLOC_SCRATCH_BYTES array in the library's device code, one per GPU, held
+ * until the process ends; `workspace` and `workspace_bytes` are ignored.  A description
+ * whose scratch (split-K partials, q8_0 staging) exceeds that size returns
+ * SIXI_E_OUT_OF_BOUNDS before any launch.  The scratch needs no initialisation, but every
+ * call on a GPU shares it: calls that may overlap on one GPU (different streams, or
+ * threads without ordering) race; order them on one stream. */
+#define SIXI_ATTN_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int sixi_attn_forward_noalloc(const sixi_attn_params* p);
+
 /* Workspace the call needs for this description (depends on S, H, Hkv, D, n_q, n_kv and
  * the device's CU count; not on the device-side lengths). */
 int sixi_attn_workspace_bytes(const sixi_attn_params* p, size_t* bytes);

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <mutex>
 
 #include "abi_util.hpp"
 #include "fa_internal.hpp"
@@ -216,6 +217,30 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     return SIXI_OK;
 }
 
+// ---- scratch of the no-allocation entry point ----
+// One copy per GPU the library runs on, held until the process ends.  On the host `scratch`
+// names a stand-in, not device memory: host code only ever uses the device address that
+// scratch_base() looks up (once per device, with that device current).
+constexpr size_t kScratchBytes = SIXI_ATTN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of the current device's `scratch`, or null if the lookup fails.
+char* scratch_base() {
+    static std::mutex mu;
+    static char* base[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!base[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        base[dev] = static_cast<char*>(ptr);
+    }
+    return base[dev];
+}
+
 // Work-groups of the launch: the split-K grid, or (prefill) the CU count its order needs.
 int launch_groups(const Plan& pl) {
     return pl.splitk ? sixi::decode_num_groups(pl.a, cu_count_cached(), pl.row_tiles) : cu_count_cached();
@@ -290,11 +315,24 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     return run(pl, static_cast<char*>(p->workspace), static_cast<hipStream_t>(p->stream));
 }
 
+int sixi_attn_forward_noalloc(const sixi_attn_params* p) {
+    Plan pl;
+    int rc = resolve(p, &pl);
+    if (rc != SIXI_OK) return rc;
+    // exact slots for this launch's work-groups, not the workspace bound of any launch
+    if (pl.splitk) splitk_layout(pl, (int64_t)pl.a.S * pl.a.Hkv + launch_groups(pl));
+    if (pl.ws_bytes > kScratchBytes) return SIXI_E_OUT_OF_BOUNDS;
+    char* base = scratch_base();
+    if (!base) return SIXI_E_BACKEND;
+    return run(pl, base, static_cast<hipStream_t>(p->stream));
+}
+
 const char* sixi_attn_strerror(int code) {
     switch (code) {
         case SIXI_OK: return "ok";
         case SIXI_E_INVALID_ARGUMENT: return "invalid argument";
-        case SIXI_E_OUT_OF_BOUNDS: return "out of bounds (workspace too small)";
+        case SIXI_E_OUT_OF_BOUNDS:
+            return "out of bounds (workspace too small, or beyond the no-allocation entry point's fixed scratch)";
         case SIXI_E_INTEGER_OVERFLOW: return "integer overflow in view extents";
         case SIXI_E_ALIGNMENT: return "misaligned pointer or stride";
         case SIXI_E_BACKEND: return "HIP launch failed";

@@ -38,6 +38,7 @@ E_UNSUPPORTED = -24
 
 EXPORTED_SYMBOLS = (
     "sixi_attn_forward",
+    "sixi_attn_forward_noalloc",
     "sixi_attn_workspace_bytes",
     "sixi_attn_validate",
     "sixi_attn_strerror",
@@ -196,6 +197,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     P = ctypes.POINTER(SixiAttnParams)
     lib.sixi_attn_forward.argtypes = [P]
     lib.sixi_attn_forward.restype = ctypes.c_int
+    lib.sixi_attn_forward_noalloc.argtypes = [P]
+    lib.sixi_attn_forward_noalloc.restype = ctypes.c_int
     lib.sixi_attn_validate.argtypes = [P]
     lib.sixi_attn_validate.restype = ctypes.c_int
     lib.sixi_attn_workspace_bytes.argtypes = [P, ctypes.POINTER(ctypes.c_size_t)]
@@ -327,13 +330,20 @@ class FlashAttnExt:
 
     def __call__(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
                  scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None, check=True,
-                 workspace=None) -> int:
+                 workspace=None, noalloc=False) -> int:
+        """One call.  ``noalloc=True`` runs sixi_attn_forward_noalloc (the library's fixed
+        device scratch, no workspace)."""
         import torch
 
         p = self.params(q, k, v, out, kv_len, q_len, mask_mode, mask, scale, max_bias, logit_softcap,
                         kv_type, stream)
         if p.stream is None:
             p.stream = torch.cuda.current_stream(self.device).cuda_stream
+        if noalloc:
+            rc = self.lib.sixi_attn_forward_noalloc(ctypes.byref(p))
+            if check and rc != OK:
+                raise SixiAttnError(rc, strerror(rc))
+            return rc
         n = ctypes.c_size_t(0)
         rc = self.lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n))
         if rc == OK:
