@@ -97,6 +97,8 @@ def ref_numeric() -> Optional[ctypes.CDLL]:
         lib.ref_quantize_row_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
         lib.ref_quantize_row_q8_0.restype = ctypes.c_int
         lib.ref_q8_0_block_bytes.restype = ctypes.c_int
+        lib.ref_diff_metrics.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        lib.ref_diff_metrics.restype = ctypes.c_int
         _ref = lib
     return _ref
 
@@ -365,16 +367,61 @@ def attention_for_workload(host: dict, kv_type: int, streams: Optional[Sequence[
 
 
 def diff_metrics(ref: np.ndarray, out: np.ndarray) -> dict:
-    """max-abs, rel-L2 (||out-ref|| / ||ref||) and cosine in float64 (after numeric.cpp:701-791)."""
-    r = np.asarray(ref, dtype=np.float64).ravel()
-    o = np.asarray(out, dtype=np.float64).ravel()
-    d = o - r
-    nr = np.linalg.norm(r)
+    """The reference's compute_diff_metrics (src/core/numeric.cpp:701-791) in float64, plus
+    rel-L2 = ||out - ref|| / ||ref||: max-abs, mean-abs and RMSE of |out - ref|; cosine (1 when
+    both norms are 0, 0 when one is); the top-1 indices (first maximum) and whether they match;
+    KL(softmax(ref) || softmax(out)) over the flat arrays, log-partition functions taken from the
+    maxima, terms with p_ref = 0 skipped, clamped at 0.  Like the reference, non-finite values
+    are an error (ValueError)."""
+    r = np.asarray(ref, dtype=np.float32).astype(np.float64).ravel()
+    o = np.asarray(out, dtype=np.float32).astype(np.float64).ravel()
+    if r.size != o.size:
+        raise ValueError("reference and candidate differ in size")
+    if r.size == 0:
+        return {"max_abs": 0.0, "mean_abs": 0.0, "rmse": 0.0, "rel_l2": 0.0, "cosine": 1.0, "kl": 0.0,
+                "top1_match": True, "ref_top1": -1, "test_top1": -1}
+    if not (np.all(np.isfinite(r)) and np.all(np.isfinite(o))):
+        raise ValueError("NaN or Inf encountered in diff_metrics")
+    d = np.abs(r - o)
+    nr2, no2 = float(np.dot(r, r)), float(np.dot(o, o))
+    if nr2 > 0.0 and no2 > 0.0:
+        cos = float(np.dot(r, o)) / (np.sqrt(nr2) * np.sqrt(no2))
+    else:
+        cos = 1.0 if nr2 == 0.0 and no2 == 0.0 else 0.0
+    log_z_r = r.max() + np.log(np.sum(np.exp(r - r.max())))
+    log_z_o = o.max() + np.log(np.sum(np.exp(o - o.max())))
+    lp_r, lp_o = r - log_z_r, o - log_z_o
+    p_r = np.exp(lp_r)
+    pos = p_r > 0.0
+    kl = float(np.sum(p_r[pos] * (lp_r[pos] - lp_o[pos])))
+    i_r, i_o = int(np.argmax(r)), int(np.argmax(o))
     return {
-        "max_abs": float(np.max(np.abs(d))) if d.size else 0.0,
-        "rel_l2": float(np.linalg.norm(d) / nr) if nr > 0 else float(np.linalg.norm(d)),
-        "cosine": float(np.dot(r, o) / (nr * np.linalg.norm(o))) if nr > 0 and np.linalg.norm(o) > 0 else 1.0,
+        "max_abs": float(d.max()),
+        "mean_abs": float(d.sum() / d.size),
+        "rmse": float(np.sqrt(np.dot(d, d) / d.size)),
+        "rel_l2": float(np.sqrt(np.dot(d, d)) / np.sqrt(nr2)) if nr2 > 0 else float(np.sqrt(np.dot(d, d))),
+        "cosine": cos,
+        "kl": max(0.0, kl),
+        "top1_match": i_r == i_o,
+        "ref_top1": i_r,
+        "test_top1": i_o,
     }
+
+
+def ref_diff_metrics(ref: np.ndarray, out: np.ndarray) -> Optional[dict]:
+    """compute_diff_metrics of the reference itself (oracle/_ref), or None when not built.
+    Raises ValueError with the reference's error code on a rejected input."""
+    lib = ref_numeric()
+    if lib is None:
+        return None
+    r = np.ascontiguousarray(ref, dtype=np.float32).ravel()
+    o = np.ascontiguousarray(out, dtype=np.float32).ravel()
+    res = np.zeros(8, dtype=np.float64)
+    rc = lib.ref_diff_metrics(r.ctypes.data, o.ctypes.data, r.size, res.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"compute_diff_metrics rejected the input (ErrorCode {rc})")
+    return {"max_abs": res[0], "mean_abs": res[1], "rmse": res[2], "cosine": res[3], "kl": res[4],
+            "top1_match": bool(res[5]), "ref_top1": int(res[6]), "test_top1": int(res[7])}
 
 
 def cpu_threads() -> int:

@@ -31,10 +31,21 @@ bool rows16(const sixi_view& v) {
     return v.nb[0] == 4 && aligned(v.data, 16) && v.nb[1] % 16 == 0 && v.nb[2] % 16 == 0 && v.nb[3] % 16 == 0;
 }
 
-// byte range [lo, hi) a view touches
-void byte_range(const sixi_view& v, int64_t row_bytes, uintptr_t* lo, uintptr_t* hi) {
+// byte range [lo, hi) a view of 4-byte elements touches (every dim at its own stride; the
+// spans were checked for overflow before)
+void byte_range(const sixi_view& v, uintptr_t* lo, uintptr_t* hi) {
+    int64_t span = 4;
+    for (int d = 0; d < 4; ++d)
+        if (v.ne[d] > 0) span += (v.ne[d] - 1) * v.nb[d];
     *lo = reinterpret_cast<uintptr_t>(v.data);
-    *hi = *lo + (uintptr_t)view_span(v, row_bytes);
+    *hi = *lo + (uintptr_t)span;
+}
+
+bool overlap(const sixi_view& a, const sixi_view& b) {
+    uintptr_t a0, a1, b0, b1;
+    byte_range(a, &a0, &a1);
+    byte_range(b, &b0, &b1);
+    return a0 < b1 && b0 < a1;
 }
 
 int resolve(const sixi_gdn_params* p, sixi::GdnArgs* out) {
@@ -64,14 +75,17 @@ int resolve(const sixi_gdn_params* p, sixi::GdnArgs* out) {
     }
     // written rows must not alias one another
     if (!rows_disjoint(y, HD * 4) || !rows_disjoint(so, K * 4)) return SIXI_E_INVALID_ARGUMENT;
-    // the state is updated in place (the same view) or written to memory the input does not touch
+    // Work-groups read and write in no fixed order across streams and groups, so what a call
+    // writes (y, the output state) must not overlap what it reads or each other.  The one
+    // exception is the state updated in place: the output state is the input view itself.
     const bool same = si.data == so.data && si.nb[1] == so.nb[1] && si.nb[2] == so.nb[2] && si.nb[3] == so.nb[3];
-    if (!same && blocks > 0) {
-        uintptr_t a0, a1, b0, b1;
-        byte_range(si, K * 4, &a0, &a1);
-        byte_range(so, K * 4, &b0, &b1);
-        if (a0 < b1 && b0 < a1) return SIXI_E_INVALID_ARGUMENT;
+    if (blocks > 0 && n_rows > 0) {
+        for (const sixi_view* x : {&q, &k, &v, &al, &be, &si, &so})
+            if (overlap(y, *x)) return SIXI_E_INVALID_ARGUMENT;
+        for (const sixi_view* x : {&q, &k, &v, &al, &be})
+            if (overlap(so, *x)) return SIXI_E_INVALID_ARGUMENT;
     }
+    if (!same && blocks > 0 && overlap(si, so)) return SIXI_E_INVALID_ARGUMENT;
     if (!rows16(q) || !rows16(k) || !rows16(v) || !rows16(y) || !rows16(si) || !rows16(so)) return SIXI_E_ALIGNMENT;
     // state rows are whole rows of K values apart
     if (si.nb[1] < K * 4) return SIXI_E_INVALID_ARGUMENT;

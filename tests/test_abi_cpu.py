@@ -300,11 +300,14 @@ def test_attn_gate_rejects(mutate, code):
 
 
 def _gdn_params(S=2, n=16, G=48, K=128, HD=128):
-    def v4(ne):
+    base = [FAKE]
+
+    def v4(ne):  # each view in an address range of its own
         nb = [4]
         for d in range(3):
             nb.append(nb[-1] * ne[d])
-        return sa.make_view(FAKE, sa.TYPE_F32, ne, nb)
+        base[0] += 1 << 32
+        return sa.make_view(base[0], sa.TYPE_F32, ne, nb)
     p = sa.SixiGdnParams()
     p.q, p.k = v4([K, G, n, S]), v4([K, G, n, S])
     p.v, p.y = v4([HD, G, n, S]), v4([HD, G, n, S])
@@ -323,9 +326,13 @@ def _gdn_params(S=2, n=16, G=48, K=128, HD=128):
     (lambda p: p.alpha.ne.__setitem__(1, 8), sa.E_INVALID_ARGUMENT),            # rows differ
     (lambda p: p.state_out.ne.__setitem__(2, 24), sa.E_INVALID_ARGUMENT),
     (lambda p: p.y.nb.__setitem__(1, 0), sa.E_INVALID_ARGUMENT),                # outputs would alias
-    (lambda p: setattr(p.state_out, "data", FAKE + 4096), sa.E_INVALID_ARGUMENT),  # overlaps the input state
-    (lambda p: setattr(p.q, "data", FAKE + 4), sa.E_ALIGNMENT),
-    (lambda p: setattr(p.beta, "data", FAKE + 2), sa.E_ALIGNMENT),
+    (lambda p: setattr(p.state_out, "data", p.state_in.data + 4096), sa.E_INVALID_ARGUMENT),  # overlaps the input state
+    (lambda p: setattr(p.y, "data", p.q.data + 512), sa.E_INVALID_ARGUMENT),   # y over an input
+    (lambda p: setattr(p.y, "data", p.beta.data), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.y, "data", p.state_in.data), sa.E_INVALID_ARGUMENT),  # y over the (in-place) state
+    (lambda p: setattr(p.q, "data", p.state_out.data + 64), sa.E_INVALID_ARGUMENT),  # the state written over q
+    (lambda p: setattr(p.q, "data", p.q.data + 4), sa.E_ALIGNMENT),
+    (lambda p: setattr(p.beta, "data", p.beta.data + 2), sa.E_ALIGNMENT),
     (lambda p: p.v.nb.__setitem__(2, 1 << 62), sa.E_INTEGER_OVERFLOW),
 ])
 def test_gdn_verify_rejects(mutate, code):
@@ -341,6 +348,6 @@ def test_gdn_verify_without_streams_launches_nothing():
 
 def test_gdn_verify_input_state_rows_must_not_overlap():
     p = _gdn_params()
-    p.state_out = sa.make_view(FAKE + (1 << 40), sa.TYPE_F32, list(p.state_in.ne), list(p.state_in.nb))
+    p.state_out = sa.make_view(FAKE + (1 << 44), sa.TYPE_F32, list(p.state_in.ne), list(p.state_in.nb))
     p.state_in.nb[1] = 256                       # input rows of 512 bytes 256 apart
     assert sa.load_library().sixi_gdn_verify(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT

@@ -117,6 +117,13 @@ def test_gate_closed_forms():
     assert np.array_equal(O.attn_gate(out, qg), out)
     qg[..., 128:] = -200.0                                         # sigmoid -> 0 (e^200 overflows f32)
     assert np.all(O.attn_gate(out, qg) == 0)
+    # interior points: sigmoid(ln 3) = 3/4 and sigmoid(-ln 3) = 1/4 (a slip such as
+    # sigmoid(g/2) gives 0.634 and 0.366)
+    ones = np.ones_like(out)
+    qg[..., 128:] = np.float32(np.log(3.0))
+    np.testing.assert_allclose(O.attn_gate(ones, qg), 0.75, rtol=2e-7)
+    qg[..., 128:] = np.float32(-np.log(3.0))
+    np.testing.assert_allclose(O.attn_gate(ones, qg), 0.25, rtol=5e-7)
     qg[..., :128] = 1e9                                            # the query half plays no part
     qg[..., 128:] = 0.0
     assert np.array_equal(O.attn_gate(out, qg, q_len=[3, 1])[1, 1:], out[1, 1:])
