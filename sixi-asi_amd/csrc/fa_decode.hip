@@ -678,7 +678,11 @@ struct WideShape { static constexpr int groups_per_cu = 1; };
 // rows), which run one lane so that each wave keeps a SIMD and 512 registers.
 template <int RS, int D> constexpr int wide_lanes() { return (D == 256 && RS == 3) ? 1 : 2; }
 // Ring depth per lane (LDS: lanes x slots x SLOT): two steps in flight where it fits.
-template <int D, int TL> constexpr int wide_slots() { return (D == 128 || TL == 1) ? 3 : 2; }
+// The software-pipelined step loop (128-dim heads) needs a four-slot ring.
+constexpr bool kWidePipelined = false;
+template <int D, int TL> constexpr int wide_slots() {
+    return (D == 128 && kWidePipelined) ? 4 : ((D == 128 || TL == 1) ? 3 : 2);
+}
 struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
 constexpr WideSplit kWide64 = {2, 2};         // 64 rows
 constexpr WideSplit kWide96 = {3, 2};         // 96 rows
@@ -745,37 +749,51 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
     }
 }
 
-template <int NT, int MODE, bool MASKED, int D>
-__device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT, WideDim<D>::DT>& acc, const u32x4* kslot,
-                                          uint32_t vlane, const uint32_t (&kofs)[WideDim<D>::KS],
-                                          const f16x8 (&qv)[NT][WideDim<D>::KS], int c0,
-                                          const RowInfo<NT>& ri, const char* mrow, int nc, int lane) {
+// V^T operand t of a step (vlane ^ 32t: chunk t of the lane's row; the next 16 cells one half
+// on).
+template <int D>
+__device__ __forceinline__ u32x4 wide_vread(uint32_t vlane, int t) {
+    const lds_char* vp = lds_ptr(vlane ^ (32u * t));
+    const u32x2 lo = ld_tr16(vp);
+    const u32x2 hi = ld_tr16(vp + WideDim<D>::HALF);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// Softmax state of one step between its score phase and its PV phase.
+template <int NT, int D>
+struct WideStep {
+    float sv[NT][8];              // scores (FAST: raw dot products; GENERIC: log2-domain logits)
+    float mx[NT];                 // row maxima of the step
+    bool need[NT];                // the row's exponent reference moves
+    u32x4 vt[WideDim<D>::DT];     // V^T operands, when read ahead with the K operands
+};
+
+// Score phase of a step: S^T = K Q^T, the mask, the row maxima and whether a row's lazy
+// exponent reference has to move; returns that for any row of the wave (uniform).
+template <int NT, int MODE, bool MASKED, int D, bool PF = (D == 128)>
+__device__ __forceinline__ bool wide_scores(const FaArgs& a, const Acc<NT, WideDim<D>::DT>& acc, WideStep<NT, D>& ws,
+                                            const u32x4* kslot, uint32_t vlane,
+                                            const uint32_t (&kofs)[WideDim<D>::KS],
+                                            const f16x8 (&qv)[NT][WideDim<D>::KS], int c0, const RowInfo<NT>& ri,
+                                            const char* mrow, int nc, int lane) {
     const int c = lane >> 4;
 
     // ---- S^T halves: lane (r, c) receives cells 16h + 4c + i of row r ----
     using W = WideDim<D>;
-    // 128-dim heads read all K and V^T operands of the step before the first MFMA (their
-    // latency hides under the scores and the softmax); 256-dim heads have no registers for it
-    constexpr bool PF = D == 128;
+    // PF: read all K and V^T operands of the step before the first MFMA, so that their
+    // latency hides under the scores and the softmax (128-dim heads in the plain step loop;
+    // the pipelined loop hides it under the other step's work instead)
     auto kread = [&](int h, int ks) {
         return as_f16x8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kslot) + kofs[ks] + W::HALF * h));
     };
-    // V^T operand t (vlane ^ 32t: chunk t of the lane's row; the next 16 cells one half on)
-    auto vread = [&](int t) -> u32x4 {
-        const lds_char* vp = lds_ptr(vlane ^ (32u * t));
-        const u32x2 lo = ld_tr16(vp);
-        const u32x2 hi = ld_tr16(vp + W::HALF);
-        return u32x4{lo[0], lo[1], hi[0], hi[1]};
-    };
     f16x8 kop[2][W::KS];
-    u32x4 vt[W::DT];
     if constexpr (PF) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int ks = 0; ks < W::KS; ++ks) kop[h][ks] = kread(h, ks);
 #pragma unroll
-        for (int t = 0; t < W::DT; ++t) vt[t] = vread(t);
+        for (int t = 0; t < W::DT; ++t) ws.vt[t] = wide_vread<D>(vlane, t);
     }
     f32x4 st[2][NT];
 #pragma unroll
@@ -788,10 +806,7 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT, WideDim<D>::D
                 st[h][n] = mfma16x16x32(kk, qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
         }
 
-    // ---- scores (FAST: raw dot products; GENERIC: log2-domain logits) and row maxima ----
-    const float c2 = a.scale_log2;
-    float sv[NT][8];
-    float mx[NT];
+    // ---- scores and row maxima ----
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
 #pragma unroll
@@ -816,36 +831,50 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT, WideDim<D>::D
             } else if (MASKED) {
                 if (cell >= ri.vis[n]) x = neg_inf();
             }
-            sv[n][e] = x;
+            ws.sv[n][e] = x;
         }
-        mx[n] = max4_rowgroups(max3f(max3f(sv[n][0], sv[n][1], sv[n][2]), max3f(sv[n][3], sv[n][4], sv[n][5]),
-                                     max2f(sv[n][6], sv[n][7])));
+        ws.mx[n] = max4_rowgroups(max3f(max3f(ws.sv[n][0], ws.sv[n][1], ws.sv[n][2]),
+                                        max3f(ws.sv[n][3], ws.sv[n][4], ws.sv[n][5]), max2f(ws.sv[n][6], ws.sv[n][7])));
     }
 
-    // ---- lazy exponent reference (as in tile_step) ----
-    const float thr = (MODE == MODE_FAST) ? kLazyLog2 / c2 : kLazyLog2;
-    bool need[NT];
+    // ---- lazy exponent reference: it moves only when the step's max exceeds it by 2^8 ----
+    const float thr = (MODE == MODE_FAST) ? kLazyLog2 / a.scale_log2 : kLazyLog2;
     bool need_any = false;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
-        need[n] = mx[n] > acc.m[n] + thr;
-        need_any |= need[n];
+        ws.need[n] = ws.mx[n] > acc.m[n] + thr;
+        need_any |= ws.need[n];
     }
-    if (__builtin_amdgcn_ballot_w64(need_any) != 0) {
-#pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            float alpha = 1.0f;
-            if (need[n]) {
-                alpha = fast_exp2((MODE == MODE_FAST) ? (acc.m[n] - mx[n]) * c2 : acc.m[n] - mx[n]);
-                acc.m[n] = mx[n];
-            }
-            acc.l[n] *= alpha;
-#pragma unroll
-            for (int t = 0; t < W::DT; ++t) acc.o[t][n] *= alpha;
-        }
-    }
+    return __builtin_amdgcn_ballot_w64(need_any) != 0;
+}
 
-    // ---- probabilities: P^T operand in the lane's own cell order, f32 row sums ----
+// Moves the exponent reference of the rows that need it and rescales their l and O.
+template <int NT, int MODE, int D>
+__device__ __forceinline__ void wide_rescale(const FaArgs& a, Acc<NT, WideDim<D>::DT>& acc, const WideStep<NT, D>& ws) {
+    const float c2 = a.scale_log2;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        float alpha = 1.0f;
+        if (ws.need[n]) {
+            alpha = fast_exp2((MODE == MODE_FAST) ? (acc.m[n] - ws.mx[n]) * c2 : acc.m[n] - ws.mx[n]);
+            acc.m[n] = ws.mx[n];
+        }
+        acc.l[n] *= alpha;
+#pragma unroll
+        for (int t0 = 0; t0 < WideDim<D>::DT; t0 += 8) acc_settle8(acc.o, n, t0);
+#pragma unroll
+        for (int t = 0; t < WideDim<D>::DT; ++t) acc.o[t][n] *= alpha;
+    }
+}
+
+// PV phase of a step: probabilities against the (settled) exponent reference, their f32 row
+// sums, and O^T += V^T P^T.
+template <int NT, int MODE, int D, bool PF = (D == 128)>
+__device__ __forceinline__ void wide_pv(const FaArgs& a, Acc<NT, WideDim<D>::DT>& acc, const WideStep<NT, D>& ws,
+                                        uint32_t vlane, int lane) {
+    using W = WideDim<D>;
+    const int c = lane >> 4;
+    const float c2 = a.scale_log2;
     f16x8 pt[NT];
     u32x4 keep[NT];
 #pragma unroll
@@ -855,7 +884,7 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT, WideDim<D>::D
         float ps[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            ps[e] = fast_exp2((MODE == MODE_FAST) ? fmaf(sv[n][e], c2, -mc) : sv[n][e] - mc);
+            ps[e] = fast_exp2((MODE == MODE_FAST) ? fmaf(ws.sv[n][e], c2, -mc) : ws.sv[n][e] - mc);
             pt[n][e] = (_Float16)ps[e];
         }
         acc.l[n] += ((ps[0] + ps[1]) + (ps[2] + ps[3])) + ((ps[4] + ps[5]) + (ps[6] + ps[7]));
@@ -872,17 +901,43 @@ __device__ __forceinline__ void wide_step(const FaArgs& a, Acc<NT, WideDim<D>::D
         }
     }
 
-    // ---- O^T += V^T P^T ----
+    // ---- O^T += V^T P^T (asm MFMAs, the accumulators pinned in place) ----
+    u32x4 vv[W::DT];
 #pragma unroll
-    for (int t = 0; t < W::DT; ++t) {
-        const u32x4 vv = PF ? vt[t] : vread(t);
+    for (int t = 0; t < W::DT; ++t) vv[t] = PF ? ws.vt[t] : wide_vread<D>(vlane, t);
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            if (MODE == MODE_GENERIC && a.mask)
-                acc.o[t][n] = mfma16x16x32(as_f16x8(vv & keep[n]), pt[n], acc.o[t][n]);
-            else
-                acc.o[t][n] = mfma16x16x32(as_f16x8(vv), pt[n], acc.o[t][n]);
+    for (int n = 0; n < NT; ++n) {
+        if (MODE == MODE_GENERIC && a.mask) {
+            u32x4 vm[W::DT];
+#pragma unroll
+            for (int t = 0; t < W::DT; ++t) vm[t] = vv[t] & keep[n];
+#pragma unroll
+            for (int t0 = 0; t0 < W::DT; t0 += 8) acc_mfma8(acc.o, n, t0, vm, pt[n]);
+        } else {
+#pragma unroll
+            for (int t0 = 0; t0 < W::DT; t0 += 8) acc_mfma8(acc.o, n, t0, vv, pt[n]);
         }
+    }
+}
+
+// Instruction order of the pipelined step body, which holds the next step's K reads, QK^T
+// MFMAs and row maxima and this step's probabilities, V^T reads and PV MFMAs: each QK^T MFMA
+// is followed by four VALU instructions (the probabilities), each PV MFMA by two (the row
+// maxima), so the MFMA pipe and the VALU work side by side.  Sched-group barriers: DS read
+// 0x100, MFMA 0x008, VALU 0x002.
+template <int NT>
+__device__ __forceinline__ void wide_pipeline_order() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int k = 0; k < 8 * NT; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+#pragma unroll
+    for (int k = 0; k < 8 * NT; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
     }
 }
 
@@ -1027,43 +1082,125 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             }
         }
     };
-    // Step i reads slot i % NS.  After the barrier of step i every wave has left step i-1, so
-    // step i+NS-1 goes into that step's slot while steps i+1 .. i+NS-2 are still in flight.
-    // Each issue is one batch of 8 loads per wave, and the ring loads are the only loads a
-    // wave has in flight in the step loop, so vmcnt counts the batches issued after step i.
-    static_assert(NS >= 2 && NS <= 4, "ring depth");
-#pragma unroll
-    for (int q = 0; q < NS - 1; ++q)
-        if (q < n_my) issue(q, q);
     // loads one issue puts in flight for each wave (the wave of a single row group stages K and V)
     constexpr int LPW = (RS == 1 ? 2 : 1) * W::LOADS;
-    auto step = [&](int i, auto masked) {
-        const int later = min(max(n_my - 1 - i, 0), NS - 2);  // steps issued after step i
-        if (later >= 2) wait_vmcnt<2 * LPW>();
-        else if (later == 1) wait_vmcnt<LPW>();
-        else wait_vmcnt<0>();
-        __syncthreads();
-        if (i + NS - 1 < n_my) issue(i + NS - 1, (i + NS - 1) % NS);
-        if (!decltype(masked)::value || i < n_my) {
-            const int t = t0 + i * TL;
-            const int sl = i % NS;
-            const u32x4* kslot = ring + sl * SLOT16;
-            // the V area is 256-byte aligned, so ^ 32t only moves bits 5..7 of vrow
-            const uint32_t vlane = ring_base + sl * W::SLOT + 32 * W::ROW + vrow;
-            wide_step<NTW, MODE, decltype(masked)::value, D>(a, acc, kslot, vlane, kofs, qv, t * kWide, ri, mrow,
-                                                             sd.nc, lane);
-        }
-    };
-    // Steps that every lane has and that lie below t_full for every lane run unmasked in a
-    // loop of their own, the rest masked in a second loop.  (One loop choosing the body per
-    // step makes the compiler merge two accumulator sets every step: 96 register copies per
-    // step, and spills.)
+    // V^T read address of slot sl for this lane (the V area is 256-byte aligned, so ^ 32t
+    // only moves bits 5..7 of vrow)
+    auto vlane_of = [&](int i) { return ring_base + (uint32_t)(i % NS) * W::SLOT + 32 * W::ROW + vrow; };
+    // Steps that every lane has and that lie below t_full for every lane run the unmasked
+    // score phase, the rest the masked one.  (One loop choosing the body per step makes the
+    // compiler merge two accumulator sets every step: register copies and spills.)
     const int n_plain = min(max((t_full - tb) / TL, 0), (te - tb) / TL);
-    int i = 0;
+    if constexpr (D == 128 && kWidePipelined) {
+        // Software-pipelined: iteration i scores step i+1 (QK^T MFMAs, row maxima) and
+        // finishes step i (probabilities, PV MFMAs).  The two halves are independent, so in
+        // one basic block the MFMAs of one overlap the VALU work of the other.
+        // Ring of four slots, step j in slot j % 4: during iteration i slot i is read for V
+        // and slot i+1 for K while steps i+2 and i+3 are in flight.  The barrier of step j
+        // (in iteration j-1) comes after every wave's V reads of step j-2 (iteration j-2), so
+        // step j+2 is issued into that slot there.  Each issue is one batch of LPW loads per
+        // wave, the ring loads are a wave's only loads in the step loop, so vmcnt counts the
+        // batches issued after step j.
+        static_assert(NS == 4, "pipelined ring");
+        const int n_both = (te - tb) / TL;  // steps that every lane has
+        if (0 < n_my) issue(0, 0);
+        if (1 < n_my) issue(1, 1);
+        auto barrier_step = [&](int j) {
+            if (j + 1 < n_my) wait_vmcnt<LPW>();
+            else wait_vmcnt<0>();
+            __syncthreads();
+            if (j + 2 < n_my) issue(j + 2, (j + 2) % NS);
+        };
+        auto qk = [&](int j, auto masked, WideStep<NTW, D>& ws) -> bool {
+            const u32x4* kslot = ring + (j % NS) * SLOT16;
+            return wide_scores<NTW, MODE, decltype(masked)::value, D, false>(a, acc, ws, kslot, vlane_of(j), kofs, qv,
+                                                                              (t0 + j * TL) * kWide, ri, mrow, sd.nc,
+                                                                              lane);
+        };
+        auto pv = [&](int j, const WideStep<NTW, D>& ws) { wide_pv<NTW, MODE, D, false>(a, acc, ws, vlane_of(j), lane); };
+        WideStep<NTW, D> cur, nxt;
+        bool need_cur = false, need_nxt = false;
+        barrier_step(0);
+        if (0 < n_my) {
+            if (n_plain > 0) need_cur = qk(0, std::false_type{}, cur);
+            else need_cur = qk(0, std::true_type{}, cur);
+        }
+        int i = 0;
+        // every lane has steps i and i+1; step i+1 unmasked
 #pragma unroll 1
-    for (; i < n_plain; ++i) step(i, std::false_type{});
+        for (; i < n_plain - 1; ++i) {
+            if (need_cur) wide_rescale<NTW, MODE, D>(a, acc, cur);
+            barrier_step(i + 1);
+            need_nxt = qk(i + 1, std::false_type{}, nxt);
+            pv(i, cur);
+            wide_pipeline_order<NTW>();
+            cur = nxt;
+            need_cur = need_nxt;
+        }
+        // every lane has steps i and i+1; step i+1 masked
 #pragma unroll 1
-    for (; i < n_iter; ++i) step(i, std::true_type{});
+        for (; i < n_both - 1; ++i) {
+            if (need_cur) wide_rescale<NTW, MODE, D>(a, acc, cur);
+            barrier_step(i + 1);
+            need_nxt = qk(i + 1, std::true_type{}, nxt);
+            pv(i, cur);
+            wide_pipeline_order<NTW>();
+            cur = nxt;
+            need_cur = need_nxt;
+        }
+        // the last steps, which some lane may not have
+#pragma unroll 1
+        for (; i < n_iter; ++i) {
+            if (i < n_my && need_cur) wide_rescale<NTW, MODE, D>(a, acc, cur);
+            if (i + 1 < n_iter) barrier_step(i + 1);
+            if (i + 1 < n_my) need_nxt = qk(i + 1, std::true_type{}, nxt);
+            if (i < n_my) pv(i, cur);
+            cur = nxt;
+            need_cur = need_nxt;
+        }
+    } else {
+        // Step i reads slot i % NS.  After the barrier of step i every wave has left step i-1,
+        // so step i+NS-1 goes into that step's slot while steps i+1 .. i+NS-2 are still in
+        // flight.  Each issue is one batch of LPW loads per wave, and the ring loads are the
+        // only loads a wave has in flight in the step loop, so vmcnt counts the batches issued
+        // after step i.
+        static_assert(NS >= 2 && NS <= 3, "ring depth");
+#pragma unroll
+        for (int q = 0; q < NS - 1; ++q)
+            if (q < n_my) issue(q, q);
+        // Score phase of step i after its data has landed; returns whether a row's exponent
+        // reference moves (uniform over the wave).  Every wave passes the barrier of every step.
+        auto scores = [&](int i, auto masked, WideStep<NTW, D>& ws) -> bool {
+            const int later = min(max(n_my - 1 - i, 0), NS - 2);  // steps issued after step i
+            if (later >= 2) wait_vmcnt<2 * LPW>();
+            else if (later == 1) wait_vmcnt<LPW>();
+            else wait_vmcnt<0>();
+            __syncthreads();
+            if (i + NS - 1 < n_my) issue(i + NS - 1, (i + NS - 1) % NS);
+            if (!decltype(masked)::value || i < n_my) {
+                const int t = t0 + i * TL;
+                const u32x4* kslot = ring + (i % NS) * SLOT16;
+                return wide_scores<NTW, MODE, decltype(masked)::value, D>(a, acc, ws, kslot, vlane_of(i), kofs, qv,
+                                                                           t * kWide, ri, mrow, sd.nc, lane);
+            }
+            return false;
+        };
+        auto finish = [&](int i, auto masked, const WideStep<NTW, D>& ws) {
+            if (!decltype(masked)::value || i < n_my) wide_pv<NTW, MODE, D>(a, acc, ws, vlane_of(i), lane);
+        };
+        int i = 0;
+        auto run = [&](int end, auto masked) {
+#pragma unroll 1
+            for (; i < end; ++i) {
+                WideStep<NTW, D> ws;
+                if (scores(i, masked, ws)) wide_rescale<NTW, MODE, D>(a, acc, ws);
+                finish(i, masked, ws);
+            }
+        };
+        run(n_plain, std::false_type{});
+        run(n_iter, std::true_type{});
+    }
+    acc_settle(acc.o);  // the asm MFMAs' results before the merge reads them
 
 #pragma unroll
     for (int n = 0; n < NTW; ++n) {

@@ -35,6 +35,71 @@ __device__ __forceinline__ f32x4 mfma16x16x16(f16x4 a, f16x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+// Accumulators carried across a step loop that also has a rare rescale (a VALU use of them).
+// With the builtin MFMA the register allocator either keeps a VGPR copy of every accumulator
+// and re-reads it each step, or splits the loop-carried value from the MFMA result and copies
+// it back each step.  These asm forms pin the accumulator in place in AGPRs (D = C).
+//
+// Inline asm is outside the hazard recognizer, so the wait states are explicit:
+//  - acc_mfma8 opens with more than the 2 that an MFMA read of a VGPR or AGPR just written by a
+//    VALU instruction needs (P converted to f16, V^T masked, a rescaled accumulator);
+//  - acc_settle8 stands between the last asm MFMA on a tile and any other read of it: more
+//    than the 11 an 8-pass MFMA result needs before a VALU or accvgpr read.  Being an asm
+//    statement on the tiles themselves, nothing that reads them can be scheduled before it.
+// o[t0 + t][n] += a[t0 + t] * b (v_mfma_f32_16x16x32_f16), t < 8: eight output tiles of row
+// tile n.
+template <int DT, int NT>
+__device__ __forceinline__ void acc_mfma8(f32x4 (&o)[DT][NT], int n, int t0, const u32x4 (&a)[DT], f16x8 b) {
+    asm("s_nop 2\n\t"
+        "v_mfma_f32_16x16x32_f16 %0, %8, %16, %0\n\t"
+        "v_mfma_f32_16x16x32_f16 %1, %9, %16, %1\n\t"
+        "v_mfma_f32_16x16x32_f16 %2, %10, %16, %2\n\t"
+        "v_mfma_f32_16x16x32_f16 %3, %11, %16, %3\n\t"
+        "v_mfma_f32_16x16x32_f16 %4, %12, %16, %4\n\t"
+        "v_mfma_f32_16x16x32_f16 %5, %13, %16, %5\n\t"
+        "v_mfma_f32_16x16x32_f16 %6, %14, %16, %6\n\t"
+        "v_mfma_f32_16x16x32_f16 %7, %15, %16, %7"
+        : "+a"(o[t0][n]), "+a"(o[t0 + 1][n]), "+a"(o[t0 + 2][n]), "+a"(o[t0 + 3][n]), "+a"(o[t0 + 4][n]),
+          "+a"(o[t0 + 5][n]), "+a"(o[t0 + 6][n]), "+a"(o[t0 + 7][n])
+        : "v"(a[t0]), "v"(a[t0 + 1]), "v"(a[t0 + 2]), "v"(a[t0 + 3]), "v"(a[t0 + 4]), "v"(a[t0 + 5]), "v"(a[t0 + 6]),
+          "v"(a[t0 + 7]), "v"(b));
+}
+// o += a * b as one asm MFMA.  b is passed as read-write (nothing changes it), so the MFMAs
+// of one row tile form a chain in program order and only the chain's first needs the wait
+// states after the VALU write of b (NOP); a written by a VALU instruction needs them too.
+template <bool NOP>
+__device__ __forceinline__ void acc_mfma1(f32x4& o, u32x4 a, f16x8& b) {
+    if constexpr (NOP)
+        asm("s_nop 2\n\tv_mfma_f32_16x16x32_f16 %0, %2, %1, %0" : "+a"(o), "+v"(b) : "v"(a));
+    else
+        asm("v_mfma_f32_16x16x32_f16 %0, %2, %1, %0" : "+a"(o), "+v"(b) : "v"(a));
+}
+// Keeps the accumulator tiles o[t0 .. t0+7][n] in AGPRs at this point (an empty asm on them):
+// placed after a VALU rescale of builtin-MFMA accumulators, so that the values meeting at the
+// end of the rare rescale branch are all in AGPRs and the common path copies nothing.
+template <int DT, int NT>
+__device__ __forceinline__ void acc_pin8(f32x4 (&o)[DT][NT], int n, int t0) {
+    asm volatile(""
+                 : "+a"(o[t0][n]), "+a"(o[t0 + 1][n]), "+a"(o[t0 + 2][n]), "+a"(o[t0 + 3][n]), "+a"(o[t0 + 4][n]),
+                   "+a"(o[t0 + 5][n]), "+a"(o[t0 + 6][n]), "+a"(o[t0 + 7][n]));
+}
+// Wait states after the asm MFMAs on the accumulator tiles o[t0 .. t0+7][n], before anything
+// else reads them.
+template <int DT, int NT>
+__device__ __forceinline__ void acc_settle8(f32x4 (&o)[DT][NT], int n, int t0) {
+    asm volatile("s_nop 7\n\ts_nop 7"
+                 : "+a"(o[t0][n]), "+a"(o[t0 + 1][n]), "+a"(o[t0 + 2][n]), "+a"(o[t0 + 3][n]), "+a"(o[t0 + 4][n]),
+                   "+a"(o[t0 + 5][n]), "+a"(o[t0 + 6][n]), "+a"(o[t0 + 7][n]));
+}
+// All tiles of an accumulator set.
+template <int DT, int NT>
+__device__ __forceinline__ void acc_settle(f32x4 (&o)[DT][NT]) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int t0 = 0; t0 < DT; t0 += 8) acc_settle8(o, n, t0);
+}
+
 // Raw buffer resource over [base, base + bytes): loads at offsets >= bytes return 0, so the
 // tail of a stream needs no clamping and can never fault.  Word 3 = 0x00020000 is the
 // gfx9-family raw-buffer format.
