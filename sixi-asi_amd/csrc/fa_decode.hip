@@ -56,7 +56,12 @@ constexpr int kQ8Dma = 9;           // dword LDS-DMA loads covering 16 q8_0 rows
 constexpr float kLazyLog2 = 8.0f;   // headroom (log2 units) before the exponent reference moves
 constexpr int kMaxPieces = 64;      // target bound on the pieces of one full-length segment
 
-enum { MODE_FAST = 0, MODE_GENERIC = 1 };
+// FAST: no mask beyond the lengths; MASK: an explicit ggml mask staged through LDS, no softcap
+// and no ALiBi (the drop-in's case); GENERIC: everything else (softcap, ALiBi, masks read from
+// global memory).  FAST and MASK keep scores as raw dot products and exponent references in
+// those units; GENERIC works with log2-domain logits.
+enum { MODE_FAST = 0, MODE_GENERIC = 1, MODE_MASK = 2 };
+template <int MODE> constexpr bool raw_units() { return MODE != MODE_GENERIC; }
 
 // Per-stream (rows, cached cells), kept in LDS so that a piece reads its extents there.
 struct StreamTable {
@@ -624,7 +629,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 #pragma unroll
     for (int n = 0; n < NTW; ++n) {
         acc.l[n] = sum4_rowgroups(acc.l[n]);
-        if (MODE == MODE_FAST && acc.m[n] != neg_inf()) acc.m[n] *= a.scale_log2;
+        if (raw_units<MODE>() && acc.m[n] != neg_inf()) acc.m[n] *= a.scale_log2;
     }
 
     __syncthreads();  // every wave is past its ring (each drained its own loads)
@@ -678,22 +683,22 @@ struct WideShape { static constexpr int groups_per_cu = 1; };
 // rows), which run one lane so that each wave keeps a SIMD and 512 registers.
 template <int RS, int D> constexpr int wide_lanes() { return (D == 256 && RS == 3) ? 1 : 2; }
 // Ring depth per lane (LDS: lanes x slots x SLOT): two steps in flight where it fits.
-// The software-pipelined step loop (128-dim heads) needs a four-slot ring.
-constexpr bool kWidePipelined = false;
-template <int D, int TL> constexpr int wide_slots() {
-    return (D == 128 && kWidePipelined) ? 4 : ((D == 128 || TL == 1) ? 3 : 2);
-}
+template <int D, int TL> constexpr int wide_slots() { return (D == 128 || TL == 1) ? 3 : 2; }
 struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
 constexpr WideSplit kWide64 = {2, 2};         // 64 rows
 constexpr WideSplit kWide96 = {3, 2};         // 96 rows
 
-// RS row groups (waves per lane) of NTW row tiles each.
-template <int NTW, int RS, int D>
+// Explicit masks: the mask rows j < 32 of a step's 32 cells (64 B per row, 2 KB) are staged
+// with the step's K and V, in a ring of their own.
+constexpr int kMaskTile = 32 * 64;
+// RS row groups (waves per lane) of NTW row tiles each; GEN: with the mask ring.
+template <int NTW, int RS, int D, bool GEN>
 struct alignas(256) WideLds {
     union {
         u32x4 ring[wide_lanes<RS, D>() * wide_slots<D, wide_lanes<RS, D>()>() * WideDim<D>::SLOT / 16];
         MergeBuf<NTW, (RS * wide_lanes<RS, D>() + 1) / 2, WideDim<D>::DT> mg;  // reused after the step loop
     };
+    u32x4 mring[GEN ? wide_lanes<RS, D>() * wide_slots<D, wide_lanes<RS, D>()>() * kMaskTile / 16 : 1];
     StreamTable st;
 };
 
@@ -765,6 +770,7 @@ struct WideStep {
     float sv[NT][8];              // scores (FAST: raw dot products; GENERIC: log2-domain logits)
     float mx[NT];                 // row maxima of the step
     bool need[NT];                // the row's exponent reference moves
+    bool mask_any;                // MASK: some mask value of the step is not 0 (wave-uniform)
     u32x4 vt[WideDim<D>::DT];     // V^T operands, when read ahead with the K operands
 };
 
@@ -775,7 +781,7 @@ __device__ __forceinline__ bool wide_scores(const FaArgs& a, const Acc<NT, WideD
                                             const u32x4* kslot, uint32_t vlane,
                                             const uint32_t (&kofs)[WideDim<D>::KS],
                                             const f16x8 (&qv)[NT][WideDim<D>::KS], int c0, const RowInfo<NT>& ri,
-                                            const char* mrow, int nc, int lane) {
+                                            const char* mrow, uint32_t mslot, int nc, int lane) {
     const int c = lane >> 4;
 
     // ---- S^T halves: lane (r, c) receives cells 16h + 4c + i of row r ----
@@ -806,6 +812,28 @@ __device__ __forceinline__ bool wide_scores(const FaArgs& a, const Acc<NT, WideD
                 st[h][n] = mfma16x16x32(kk, qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
         }
 
+    // explicit mask values of the lane's cells 16h + 4c .. +3 for each row tile (staged: from
+    // the step's LDS tile, row j at 64 j)
+    u32x2 mstage[NT][2];
+    if ((MODE == MODE_GENERIC && a.mask && a.mask_stage) || MODE == MODE_MASK) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                mstage[n][h] = lds_ld8(mslot + 64u * (uint32_t)ri.j[n] + 2u * (uint32_t)(16 * h + 4 * c));
+    }
+
+    // MASK: a step whose mask values are all 0 (+-0) for every row of the wave adds nothing;
+    // only the other steps (for a causal mask: those on the diagonal) add them per cell
+    ws.mask_any = false;
+    if constexpr (MODE == MODE_MASK) {
+        uint32_t bits = 0;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) bits |= mstage[n][0][0] | mstage[n][0][1] | mstage[n][1][0] | mstage[n][1][1];
+        ws.mask_any = __builtin_amdgcn_ballot_w64((bits & 0x7fff7fffu) != 0) != 0;
+    }
+    const float inv_scale = 1.0f / a.scale;
+
     // ---- scores and row maxima ----
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
@@ -813,10 +841,25 @@ __device__ __forceinline__ bool wide_scores(const FaArgs& a, const Acc<NT, WideD
         for (int e = 0; e < 8; ++e) {
             const int cell = c0 + 16 * (e >> 2) + 4 * c + (e & 3);
             float x = st[e >> 2][n][e & 3];
-            if (MODE == MODE_GENERIC) {
+            if (MODE == MODE_MASK) {
+                // raw units: s = dot + mask/scale; -inf (or a cell past the stream) skips the
+                // cell whatever its K holds
+                if (ws.mask_any) {
+                    const uint32_t w = mstage[n][e >> 2][(e & 3) >> 1];
+                    const float mv = half_bits_to_float((uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu)));
+                    x = (mv == neg_inf() || (MASKED && cell >= nc)) ? neg_inf() : fmaf(mv, inv_scale, x);
+                } else if (MASKED && cell >= nc) {
+                    x = neg_inf();
+                }
+            } else if (MODE == MODE_GENERIC) {
                 x *= a.scale;
                 if (a.softcap != 0.0f) x = a.softcap * tanhf(x);
-                if (a.mask) {
+                if (a.mask && a.mask_stage) {
+                    const uint32_t w = mstage[n][e >> 2][(e & 3) >> 1];
+                    const uint16_t bits = (uint16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
+                    const float mv = cell < nc ? ri.slope[n] * half_bits_to_float(bits) : neg_inf();
+                    x = (mv == neg_inf()) ? neg_inf() : x + mv;
+                } else if (a.mask) {
                     float mv = neg_inf();
                     if (cell < nc) {
                         const uint16_t bits = *reinterpret_cast<const uint16_t*>(
@@ -838,7 +881,7 @@ __device__ __forceinline__ bool wide_scores(const FaArgs& a, const Acc<NT, WideD
     }
 
     // ---- lazy exponent reference: it moves only when the step's max exceeds it by 2^8 ----
-    const float thr = (MODE == MODE_FAST) ? kLazyLog2 / a.scale_log2 : kLazyLog2;
+    const float thr = raw_units<MODE>() ? kLazyLog2 / a.scale_log2 : kLazyLog2;
     bool need_any = false;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
@@ -856,7 +899,7 @@ __device__ __forceinline__ void wide_rescale(const FaArgs& a, Acc<NT, WideDim<D>
     for (int n = 0; n < NT; ++n) {
         float alpha = 1.0f;
         if (ws.need[n]) {
-            alpha = fast_exp2((MODE == MODE_FAST) ? (acc.m[n] - ws.mx[n]) * c2 : acc.m[n] - ws.mx[n]);
+            alpha = fast_exp2(raw_units<MODE>() ? (acc.m[n] - ws.mx[n]) * c2 : acc.m[n] - ws.mx[n]);
             acc.m[n] = ws.mx[n];
         }
         acc.l[n] *= alpha;
@@ -876,19 +919,21 @@ __device__ __forceinline__ void wide_pv(const FaArgs& a, Acc<NT, WideDim<D>::DT>
     const int c = lane >> 4;
     const float c2 = a.scale_log2;
     f16x8 pt[NT];
+    const bool use_keep = (MODE == MODE_GENERIC && a.mask) || (MODE == MODE_MASK && ws.mask_any);
     u32x4 keep[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
+        keep[n] = u32x4{~0u, ~0u, ~0u, ~0u};
         const float ref = acc.m[n];
-        const float mc = (ref == neg_inf()) ? 0.0f : ((MODE == MODE_FAST) ? ref * c2 : ref);
+        const float mc = (ref == neg_inf()) ? 0.0f : (raw_units<MODE>() ? ref * c2 : ref);
         float ps[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            ps[e] = fast_exp2((MODE == MODE_FAST) ? fmaf(ws.sv[n][e], c2, -mc) : ws.sv[n][e] - mc);
+            ps[e] = fast_exp2(raw_units<MODE>() ? fmaf(ws.sv[n][e], c2, -mc) : ws.sv[n][e] - mc);
             pt[n][e] = (_Float16)ps[e];
         }
         acc.l[n] += ((ps[0] + ps[1]) + (ps[2] + ps[3])) + ((ps[4] + ps[5]) + (ps[6] + ps[7]));
-        if (MODE == MODE_GENERIC && a.mask) {
+        if (use_keep) {
             // explicit masks: a cell that none of these 16 rows sees may hold NaN bits, so
             // its V^T column is zeroed for them (0 * NaN must not reach the accumulator)
 #pragma unroll
@@ -901,43 +946,26 @@ __device__ __forceinline__ void wide_pv(const FaArgs& a, Acc<NT, WideDim<D>::DT>
         }
     }
 
-    // ---- O^T += V^T P^T (asm MFMAs, the accumulators pinned in place) ----
-    u32x4 vv[W::DT];
+    // ---- O^T += V^T P^T (asm MFMAs, the accumulators pinned in place), eight V^T operands
+    // at a time.  Only the operands depend on the mask (all-ones keep masks otherwise): two
+    // asm paths joining would make the compiler copy the accumulators right behind the
+    // MFMAs, unaware of the asm's results still being in flight. ----
 #pragma unroll
-    for (int t = 0; t < W::DT; ++t) vv[t] = PF ? ws.vt[t] : wide_vread<D>(vlane, t);
+    for (int t0 = 0; t0 < W::DT; t0 += 8) {
+        u32x4 vv[8];
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-        if (MODE == MODE_GENERIC && a.mask) {
-            u32x4 vm[W::DT];
+        for (int t = 0; t < 8; ++t) vv[t] = PF ? ws.vt[t0 + t] : wide_vread<D>(vlane, t0 + t);
 #pragma unroll
-            for (int t = 0; t < W::DT; ++t) vm[t] = vv[t] & keep[n];
+        for (int n = 0; n < NT; ++n) {
+            if (MODE != MODE_FAST) {
+                u32x4 vm[8];
 #pragma unroll
-            for (int t0 = 0; t0 < W::DT; t0 += 8) acc_mfma8(acc.o, n, t0, vm, pt[n]);
-        } else {
-#pragma unroll
-            for (int t0 = 0; t0 < W::DT; t0 += 8) acc_mfma8(acc.o, n, t0, vv, pt[n]);
+                for (int t = 0; t < 8; ++t) vm[t] = vv[t] & keep[n];
+                acc_mfma8(acc.o, n, t0, vm, pt[n]);
+            } else {
+                acc_mfma8(acc.o, n, t0, vv, pt[n]);
+            }
         }
-    }
-}
-
-// Instruction order of the pipelined step body, which holds the next step's K reads, QK^T
-// MFMAs and row maxima and this step's probabilities, V^T reads and PV MFMAs: each QK^T MFMA
-// is followed by four VALU instructions (the probabilities), each PV MFMA by two (the row
-// maxima), so the MFMA pipe and the VALU work side by side.  Sched-group barriers: DS read
-// 0x100, MFMA 0x008, VALU 0x002.
-template <int NT>
-__device__ __forceinline__ void wide_pipeline_order() {
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int k = 0; k < 8 * NT; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
-#pragma unroll
-    for (int k = 0; k < 8 * NT; ++k) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
     }
 }
 
@@ -986,11 +1014,10 @@ __device__ __forceinline__ void write_partial_wide(float* slot, int rows_slot, i
 
 // One piece of the 32-cell kernel: steps [tb, te) of segment (s, g).
 template <int NTW, int RS, int MODE, int D>
-__device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, RS, D>& sh, int causal,
-                                                  const Piece& pc) {
+__device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, RS, D, MODE != MODE_FAST>& sh,
+                                                  int causal, const Piece& pc) {
     using W = WideDim<D>;
     constexpr int TL = wide_lanes<RS, D>();
-    constexpr int NS = wide_slots<D, TL>();
     constexpr int SLOT16 = W::SLOT / 16;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1020,10 +1047,11 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
         ri.vis[n] = (valid && causal) ? sd.kl + j + 1 : sd.nc;
         ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, hb + (valid ? row % G : 0)) : 1.0f;
     }
-    // steps below t_full see no masked cell for any row
-    const int t_full = (MODE == MODE_GENERIC) ? 0 : (causal ? (sd.kl + 1) / kWide : sd.nc / kWide);
+    // steps below t_full need no per-row visibility test (MASK: no test for the stream's end;
+    // its explicit mask is applied on every step)
+    const int t_full = (MODE == MODE_GENERIC) ? 0 : ((causal && MODE == MODE_FAST) ? (sd.kl + 1) / kWide : sd.nc / kWide);
     const char* mrow = nullptr;
-    if (MODE == MODE_GENERIC && a.mask) mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3;
+    if (MODE != MODE_FAST && a.mask) mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3;
 
     Acc<NTW, W::DT> acc;
     acc_clear(acc);
@@ -1054,13 +1082,30 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     const int t0 = tb + tl;
     const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
     const int n_iter = (te - tb + TL - 1) / TL;
-    u32x4* ring = sh.ring + (size_t)tl * NS * SLOT16;
+    u32x4* ring = sh.ring + (size_t)tl * wide_slots<D, TL>() * SLOT16;
     const uint32_t ring_base = lds_addr(ring);
 
+    // explicit masks: rows j < 32 of a stream's mask; an empty resource (every load returns 0)
+    // when the mask is read from global memory instead, so that every issue has the same loads
+    constexpr bool GEN = MODE != MODE_FAST;
+    const buf_rsrc mrs = make_rsrc_uniform(mrow, GEN && a.mask_stage ? a.m_bytes : 0u);
+    const uint32_t mring_base = lds_addr(sh.mring) + (uint32_t)tl * wide_slots<D, TL>() * kMaskTile;
     auto issue = [&](int i, int slot) {
         const uint32_t c0 = (uint32_t)(t0 + i * TL) * kWide;
         const uint32_t base = ring_base + (uint32_t)slot * W::SLOT;
         const uint32_t pos = (uint32_t)lane % W::CPR;  // 16-byte position in the row
+        if constexpr (GEN) {
+            // mask rows 16*half + lane/4, cells c0 + 8*(lane%4) .. +7: 1 KB per load, laid out
+            // [row][32 cells] (64 B per row) in the slot's tile
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                if (RS == 1 || rg == half) {
+                    const uint32_t j = 16u * half + (uint32_t)lane / 4;
+                    dma16x1_to_lds(mrs, j * (uint32_t)a.m_nb1 + (c0 + 8u * (lane & 3)) * 2u,
+                                   mring_base + (uint32_t)slot * kMaskTile + 1024u * half);
+                }
+            }
+        }
 #pragma unroll
         for (int b8 = 0; b8 < W::LOADS / 8; ++b8) {
             uint32_t o8[8];
@@ -1082,89 +1127,23 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             }
         }
     };
-    // loads one issue puts in flight for each wave (the wave of a single row group stages K and V)
-    constexpr int LPW = (RS == 1 ? 2 : 1) * W::LOADS;
+    // loads one issue puts in flight for each wave (the wave of a single row group stages K and
+    // V, and both halves of an explicit mask's tile)
+    constexpr int LPW = (RS == 1 ? 2 : 1) * (W::LOADS + (GEN ? 1 : 0));
     // V^T read address of slot sl for this lane (the V area is 256-byte aligned, so ^ 32t
     // only moves bits 5..7 of vrow)
-    auto vlane_of = [&](int i) { return ring_base + (uint32_t)(i % NS) * W::SLOT + 32 * W::ROW + vrow; };
+    auto vlane_at = [&](int slot) { return ring_base + (uint32_t)slot * W::SLOT + 32 * W::ROW + vrow; };
     // Steps that every lane has and that lie below t_full for every lane run the unmasked
     // score phase, the rest the masked one.  (One loop choosing the body per step makes the
     // compiler merge two accumulator sets every step: register copies and spills.)
     const int n_plain = min(max((t_full - tb) / TL, 0), (te - tb) / TL);
-    if constexpr (D == 128 && kWidePipelined) {
-        // Software-pipelined: iteration i scores step i+1 (QK^T MFMAs, row maxima) and
-        // finishes step i (probabilities, PV MFMAs).  The two halves are independent, so in
-        // one basic block the MFMAs of one overlap the VALU work of the other.
-        // Ring of four slots, step j in slot j % 4: during iteration i slot i is read for V
-        // and slot i+1 for K while steps i+2 and i+3 are in flight.  The barrier of step j
-        // (in iteration j-1) comes after every wave's V reads of step j-2 (iteration j-2), so
-        // step j+2 is issued into that slot there.  Each issue is one batch of LPW loads per
-        // wave, the ring loads are a wave's only loads in the step loop, so vmcnt counts the
-        // batches issued after step j.
-        static_assert(NS == 4, "pipelined ring");
-        const int n_both = (te - tb) / TL;  // steps that every lane has
-        if (0 < n_my) issue(0, 0);
-        if (1 < n_my) issue(1, 1);
-        auto barrier_step = [&](int j) {
-            if (j + 1 < n_my) wait_vmcnt<LPW>();
-            else wait_vmcnt<0>();
-            __syncthreads();
-            if (j + 2 < n_my) issue(j + 2, (j + 2) % NS);
-        };
-        auto qk = [&](int j, auto masked, WideStep<NTW, D>& ws) -> bool {
-            const u32x4* kslot = ring + (j % NS) * SLOT16;
-            return wide_scores<NTW, MODE, decltype(masked)::value, D, false>(a, acc, ws, kslot, vlane_of(j), kofs, qv,
-                                                                              (t0 + j * TL) * kWide, ri, mrow, sd.nc,
-                                                                              lane);
-        };
-        auto pv = [&](int j, const WideStep<NTW, D>& ws) { wide_pv<NTW, MODE, D, false>(a, acc, ws, vlane_of(j), lane); };
-        WideStep<NTW, D> cur, nxt;
-        bool need_cur = false, need_nxt = false;
-        barrier_step(0);
-        if (0 < n_my) {
-            if (n_plain > 0) need_cur = qk(0, std::false_type{}, cur);
-            else need_cur = qk(0, std::true_type{}, cur);
-        }
-        int i = 0;
-        // every lane has steps i and i+1; step i+1 unmasked
-#pragma unroll 1
-        for (; i < n_plain - 1; ++i) {
-            if (need_cur) wide_rescale<NTW, MODE, D>(a, acc, cur);
-            barrier_step(i + 1);
-            need_nxt = qk(i + 1, std::false_type{}, nxt);
-            pv(i, cur);
-            wide_pipeline_order<NTW>();
-            cur = nxt;
-            need_cur = need_nxt;
-        }
-        // every lane has steps i and i+1; step i+1 masked
-#pragma unroll 1
-        for (; i < n_both - 1; ++i) {
-            if (need_cur) wide_rescale<NTW, MODE, D>(a, acc, cur);
-            barrier_step(i + 1);
-            need_nxt = qk(i + 1, std::true_type{}, nxt);
-            pv(i, cur);
-            wide_pipeline_order<NTW>();
-            cur = nxt;
-            need_cur = need_nxt;
-        }
-        // the last steps, which some lane may not have
-#pragma unroll 1
-        for (; i < n_iter; ++i) {
-            if (i < n_my && need_cur) wide_rescale<NTW, MODE, D>(a, acc, cur);
-            if (i + 1 < n_iter) barrier_step(i + 1);
-            if (i + 1 < n_my) need_nxt = qk(i + 1, std::true_type{}, nxt);
-            if (i < n_my) pv(i, cur);
-            cur = nxt;
-            need_cur = need_nxt;
-        }
-    } else {
+    {
         // Step i reads slot i % NS.  After the barrier of step i every wave has left step i-1,
         // so step i+NS-1 goes into that step's slot while steps i+1 .. i+NS-2 are still in
         // flight.  Each issue is one batch of LPW loads per wave, and the ring loads are the
         // only loads a wave has in flight in the step loop, so vmcnt counts the batches issued
         // after step i.
-        static_assert(NS >= 2 && NS <= 3, "ring depth");
+        constexpr int NS = wide_slots<D, TL>();
 #pragma unroll
         for (int q = 0; q < NS - 1; ++q)
             if (q < n_my) issue(q, q);
@@ -1180,13 +1159,14 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             if (!decltype(masked)::value || i < n_my) {
                 const int t = t0 + i * TL;
                 const u32x4* kslot = ring + (i % NS) * SLOT16;
-                return wide_scores<NTW, MODE, decltype(masked)::value, D>(a, acc, ws, kslot, vlane_of(i), kofs, qv,
-                                                                           t * kWide, ri, mrow, sd.nc, lane);
+                return wide_scores<NTW, MODE, decltype(masked)::value, D>(
+                    a, acc, ws, kslot, vlane_at((i) % NS), kofs, qv, t * kWide, ri, mrow,
+                    mring_base + (uint32_t)(i % NS) * kMaskTile, sd.nc, lane);
             }
             return false;
         };
         auto finish = [&](int i, auto masked, const WideStep<NTW, D>& ws) {
-            if (!decltype(masked)::value || i < n_my) wide_pv<NTW, MODE, D>(a, acc, ws, vlane_of(i), lane);
+            if (!decltype(masked)::value || i < n_my) wide_pv<NTW, MODE, D>(a, acc, ws, vlane_at((i) % NS), lane);
         };
         int i = 0;
         auto run = [&](int end, auto masked) {
@@ -1205,7 +1185,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
 #pragma unroll
     for (int n = 0; n < NTW; ++n) {
         acc.l[n] = sum4_rowgroups(acc.l[n]);
-        if (MODE == MODE_FAST && acc.m[n] != neg_inf()) acc.m[n] *= a.scale_log2;
+        if (raw_units<MODE>() && acc.m[n] != neg_inf()) acc.m[n] *= a.scale_log2;
     }
 
     __syncthreads();  // every wave is past its ring (each drained its own loads)
@@ -1295,7 +1275,7 @@ decode_d128(FaArgs a, int causal) {
 template <int NTW, int RS, int MODE, int D>
 __global__ __launch_bounds__((RS * wide_lanes<RS, D>() * 64), (RS * wide_lanes<RS, D>() * WideShape::groups_per_cu + 3) / 4)
 void decode_wide(FaArgs a, int causal) {
-    __shared__ WideLds<NTW, RS, D> sh;
+    __shared__ WideLds<NTW, RS, D, MODE != MODE_FAST> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
     for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
@@ -1434,11 +1414,13 @@ inline bool slot_fits(const FaArgs& a, int rows, int D) {
 }
 
 template <int NTW, int RS, int D>
-hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
+hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream) {
     if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(RS * wide_lanes<RS, D>() * 64);
-    if (generic)
+    if (mode == MODE_GENERIC)
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_GENERIC, D>), grid, block, 0, stream, a, causal);
+    else if (mode == MODE_MASK)
+        hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_MASK, D>), grid, block, 0, stream, a, causal);
     else
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_FAST, D>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
@@ -1448,7 +1430,8 @@ hipError_t launch_wide(const FaArgs& a, bool generic, int causal, hipStream_t st
 }
 
 template <int NTW, int KV>
-hipError_t launch_nt(const FaArgs& a, bool generic, int causal, hipStream_t stream) {
+hipError_t launch_nt(const FaArgs& a, int mode, int causal, hipStream_t stream) {
+    const bool generic = mode != MODE_FAST;
     if (!slot_fits(a, NTW * 16, 128)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(Shape<KV>::waves * 64);
     if (generic)
@@ -1478,7 +1461,11 @@ int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
 
 hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream) {
-    const bool generic = mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f;
+    // the 32-cell kernel's MASK mode: a staged explicit mask, no softcap, no ALiBi
+    const int mode = (mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f)
+                         ? ((mask_mode == SIXI_MASK_EXPLICIT && a.softcap == 0.0f && a.alibi_nlog2 == 0 && a.mask_stage)
+                                ? MODE_MASK : MODE_GENERIC)
+                         : MODE_FAST;
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
     if (head_dim == 256) {
         // 256-dim heads: every row count runs the 32-cell kernel (one or two row groups)
@@ -1486,29 +1473,29 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
         // at most two row tiles per wave (three spill the 256-dim accumulators), so 33-48 rows
         // run as 64 (decode_row_tiles maps 3 to 4); 96 rows run as three row groups of one lane
         switch (row_tiles) {
-            case 1: return launch_wide<1, 1, 256>(a, generic, causal, stream);
-            case 2: return launch_wide<2, 1, 256>(a, generic, causal, stream);
-            case 4: return launch_wide<2, 2, 256>(a, generic, causal, stream);
-            case 6: return launch_wide<2, 3, 256>(a, generic, causal, stream);
+            case 1: return launch_wide<1, 1, 256>(a, mode, causal, stream);
+            case 2: return launch_wide<2, 1, 256>(a, mode, causal, stream);
+            case 4: return launch_wide<2, 2, 256>(a, mode, causal, stream);
+            case 6: return launch_wide<2, 3, 256>(a, mode, causal, stream);
             default: return hipErrorNotSupported;
         }
     }
     if (head_dim != 128) return hipErrorNotSupported;
     if (kv_type == SIXI_TYPE_F16) {
         switch (row_tiles) {
-            case 1: return launch_nt<1, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 2: return launch_nt<2, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 3: return launch_nt<3, SIXI_TYPE_F16>(a, generic, causal, stream);
-            case 4: return launch_wide<kWide64.ntw, kWide64.rs, 128>(a, generic, causal, stream);
-            case 6: return launch_wide<kWide96.ntw, kWide96.rs, 128>(a, generic, causal, stream);
+            case 1: return launch_nt<1, SIXI_TYPE_F16>(a, mode, causal, stream);
+            case 2: return launch_nt<2, SIXI_TYPE_F16>(a, mode, causal, stream);
+            case 3: return launch_nt<3, SIXI_TYPE_F16>(a, mode, causal, stream);
+            case 4: return launch_wide<kWide64.ntw, kWide64.rs, 128>(a, mode, causal, stream);
+            case 6: return launch_wide<kWide96.ntw, kWide96.rs, 128>(a, mode, causal, stream);
             default: return hipErrorNotSupported;
         }
     }
     if (kv_type == SIXI_TYPE_Q8_0) {
         switch (row_tiles) {
-            case 1: return launch_nt<1, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
-            case 2: return launch_nt<2, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
-            case 3: return launch_nt<3, SIXI_TYPE_Q8_0>(a, generic, causal, stream);
+            case 1: return launch_nt<1, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
+            case 2: return launch_nt<2, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
+            case 3: return launch_nt<3, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
             default: return hipErrorNotSupported;
         }
     }

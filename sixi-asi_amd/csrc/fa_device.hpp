@@ -46,10 +46,9 @@ __device__ __forceinline__ f32x4 mfma16x16x16(f16x4 a, f16x4 b, f32x4 c) {
 //  - acc_settle8 stands between the last asm MFMA on a tile and any other read of it: more
 //    than the 11 an 8-pass MFMA result needs before a VALU or accvgpr read.  Being an asm
 //    statement on the tiles themselves, nothing that reads them can be scheduled before it.
-// o[t0 + t][n] += a[t0 + t] * b (v_mfma_f32_16x16x32_f16), t < 8: eight output tiles of row
-// tile n.
+// o[t0 + t][n] += a[t] * b (v_mfma_f32_16x16x32_f16), t < 8: eight output tiles of row tile n.
 template <int DT, int NT>
-__device__ __forceinline__ void acc_mfma8(f32x4 (&o)[DT][NT], int n, int t0, const u32x4 (&a)[DT], f16x8 b) {
+__device__ __forceinline__ void acc_mfma8(f32x4 (&o)[DT][NT], int n, int t0, const u32x4 (&a)[8], f16x8 b) {
     asm("s_nop 2\n\t"
         "v_mfma_f32_16x16x32_f16 %0, %8, %16, %0\n\t"
         "v_mfma_f32_16x16x32_f16 %1, %9, %16, %1\n\t"
@@ -61,27 +60,7 @@ __device__ __forceinline__ void acc_mfma8(f32x4 (&o)[DT][NT], int n, int t0, con
         "v_mfma_f32_16x16x32_f16 %7, %15, %16, %7"
         : "+a"(o[t0][n]), "+a"(o[t0 + 1][n]), "+a"(o[t0 + 2][n]), "+a"(o[t0 + 3][n]), "+a"(o[t0 + 4][n]),
           "+a"(o[t0 + 5][n]), "+a"(o[t0 + 6][n]), "+a"(o[t0 + 7][n])
-        : "v"(a[t0]), "v"(a[t0 + 1]), "v"(a[t0 + 2]), "v"(a[t0 + 3]), "v"(a[t0 + 4]), "v"(a[t0 + 5]), "v"(a[t0 + 6]),
-          "v"(a[t0 + 7]), "v"(b));
-}
-// o += a * b as one asm MFMA.  b is passed as read-write (nothing changes it), so the MFMAs
-// of one row tile form a chain in program order and only the chain's first needs the wait
-// states after the VALU write of b (NOP); a written by a VALU instruction needs them too.
-template <bool NOP>
-__device__ __forceinline__ void acc_mfma1(f32x4& o, u32x4 a, f16x8& b) {
-    if constexpr (NOP)
-        asm("s_nop 2\n\tv_mfma_f32_16x16x32_f16 %0, %2, %1, %0" : "+a"(o), "+v"(b) : "v"(a));
-    else
-        asm("v_mfma_f32_16x16x32_f16 %0, %2, %1, %0" : "+a"(o), "+v"(b) : "v"(a));
-}
-// Keeps the accumulator tiles o[t0 .. t0+7][n] in AGPRs at this point (an empty asm on them):
-// placed after a VALU rescale of builtin-MFMA accumulators, so that the values meeting at the
-// end of the rare rescale branch are all in AGPRs and the common path copies nothing.
-template <int DT, int NT>
-__device__ __forceinline__ void acc_pin8(f32x4 (&o)[DT][NT], int n, int t0) {
-    asm volatile(""
-                 : "+a"(o[t0][n]), "+a"(o[t0 + 1][n]), "+a"(o[t0 + 2][n]), "+a"(o[t0 + 3][n]), "+a"(o[t0 + 4][n]),
-                   "+a"(o[t0 + 5][n]), "+a"(o[t0 + 6][n]), "+a"(o[t0 + 7][n]));
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]), "v"(b));
 }
 // Wait states after the asm MFMAs on the accumulator tiles o[t0 .. t0+7][n], before anything
 // else reads them.
@@ -189,6 +168,20 @@ __device__ __forceinline__ void dma16x8_to_lds(buf_rsrc rs, const uint32_t (&v)[
         : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "s"(rs)
         : "memory", "scc");
 }
+// One 16-byte-per-lane load (1 KB).
+__device__ __forceinline__ void dma16x1_to_lds(buf_rsrc rs, uint32_t v, uint32_t lds) {
+    int saved;
+    asm volatile(
+        "s_nop 4\n\t"
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v), "s"(rs)
+        : "memory", "scc");
+}
 // 4 bytes per lane, LDS stride 256: q8_0 rows, whose alignment is only 4 bytes.
 __device__ __forceinline__ void dma4x9_to_lds(buf_rsrc rs, const uint32_t (&v)[9], uint32_t lds) {
     int saved;
@@ -245,6 +238,12 @@ __device__ __forceinline__ u32x2 ld_tr16(const lds_char* p) {
 
 // LDS pointer from an LDS byte address.
 __device__ __forceinline__ const lds_char* lds_ptr(uint32_t addr) { return (const lds_char*)(size_t)addr; }
+
+// 8-byte LDS load at an LDS byte address (8-byte aligned).
+__device__ __forceinline__ u32x2 lds_ld8(uint32_t addr) {
+    typedef __attribute__((address_space(3))) const u32x2 lds_u32x2;
+    return *(lds_u32x2*)(size_t)addr;
+}
 
 // LDS byte address of a __shared__ object.
 template <typename T>

@@ -30,6 +30,9 @@ struct FaArgs {
     const char* mask;      // EXPLICIT: f16 at mask + c*2 + j*m_nb1 + (s % m_ne3)*m_nb3
     int64_t m_nb1, m_nb3;
     int32_t m_ne3;
+    int32_t mask_stage;    // EXPLICIT, rows j < 32 of a step staged through LDS (16-byte aligned
+                           // rows); 0: read per cell from global memory
+    uint32_t m_bytes;      // staged: bytes of a stream's mask rows the kernel may read
 
     int32_t S, H, Hkv, G;  // streams, q heads, kv heads, H / Hkv
     int32_t Gr, hoff;      // heads of each GQA group this launch covers: hoff .. hoff+Gr-1

@@ -154,6 +154,14 @@ int resolve(const sixi_attn_params* p, Plan* out) {
         a.mask = static_cast<const char*>(m.data);
         a.m_nb1 = m.nb[1]; a.m_nb3 = m.nb[3];
         a.m_ne3 = (int32_t)m.ne[3];
+        // the 32-cell kernel stages rows j < 32 of every step through LDS with 16-byte DMA
+        // loads: whole rows of 16-byte alignment, reachable with 32-bit offsets
+        const int64_t rows = std::min<int64_t>(n_q, 32);
+        const int64_t span = (rows - 1) * m.nb[1] + m.ne[0] * 2;
+        a.mask_stage = (n_q <= 32 && m.nb[1] % 16 == 0 && (m.ne[3] == 1 || m.nb[3] % 16 == 0) &&
+                        aligned(m.data, 16) && span < (int64_t)UINT32_MAX)
+                           ? 1 : 0;
+        a.m_bytes = a.mask_stage ? (uint32_t)span : 0u;
     } else {
         a.m_ne3 = 1;
     }
