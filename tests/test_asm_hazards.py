@@ -1,0 +1,148 @@
+"""Static check of the gfx950 code of the decode kernels: no instruction may touch the
+accumulators an inline-asm MFMA writes within the hazard window behind it.
+
+The compiler's hazard recognizer does not look inside inline asm, so a register copy or VALU
+op that the compiler places right behind an asm MFMA block (e.g. where two asm paths join)
+gets no wait states and can read stale accumulator values.  The asm blocks of the kernels
+end their own windows (acc_settle8) where they hand the accumulators to compiled code; this
+test compiles the kernel source to device assembly with the build's flags and walks every
+path (branches followed) from each asm MFMA for WAIT wait states.
+"""
+import importlib.util
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+BUILD = ROOT / "sixi-asi_amd" / "build.py"
+
+# v_mfma_f32_16x16x32_f16 is 8 passes: a VALU read of its result needs 11 wait states on
+# gfx950 and an overlapping SrcC read by a different-size MFMA up to 19; the window here is
+# wider than both.
+WAIT = 24
+
+_REG = re.compile(r"\ba\[(\d+)(?::(\d+))?\]|\ba(\d+)\b")
+
+
+def _agprs(text):
+    out = set()
+    for m in _REG.finditer(text):
+        if m.group(3) is not None:
+            out.add(int(m.group(3)))
+        else:
+            lo = int(m.group(1))
+            out.update(range(lo, int(m.group(2) or lo) + 1))
+    return out
+
+
+def _functions(asm):
+    for name in re.findall(r"\.type\s+(\S+),@function", asm):
+        i = asm.index(name + ":")
+        j = asm.find(".Lfunc_end", i)
+        yield name, asm[i:j].splitlines()
+
+
+def _parse(lines):
+    labels, ins, in_asm = {}, [], False
+    for raw in lines:
+        t = raw.strip()
+        if "ASMSTART" in t:
+            in_asm = True
+            continue
+        if "ASMEND" in t:
+            in_asm = False
+            continue
+        if t.startswith(";"):
+            continue
+        t = t.split(";")[0].strip()
+        if not t:
+            continue
+        if t.endswith(":"):
+            labels[t[:-1]] = len(ins)
+            continue
+        if t.startswith("."):
+            continue
+        ins.append((t, in_asm))
+    return labels, ins
+
+
+def hazards(asm, wait=WAIT):
+    """(function, asm MFMA, offending instruction) for every touch of an asm MFMA's result
+    registers within `wait` wait states on any path (s_nop N counts N + 1)."""
+    found = []
+    for name, lines in _functions(asm):
+        labels, ins = _parse(lines)
+        for k, (t, is_asm) in enumerate(ins):
+            if not (is_asm and t.startswith("v_mfma")):
+                continue
+            dst = _agprs(t.split(",")[0])
+            stack, seen = [(k + 1, 0)], set()
+            while stack:
+                p, w = stack.pop()
+                while p < len(ins) and w < wait and (p, w) not in seen:
+                    seen.add((p, w))
+                    u, u_asm = ins[p]
+                    op = u.split()[0]
+                    if op.startswith("v_mfma") and u_asm:
+                        # a later asm MFMA may accumulate into it (tied SrcC), not read it as A/B
+                        srcs = u.split(None, 1)[1].split(",")[1:3]
+                        if _agprs(",".join(srcs)) & dst:
+                            found.append((name, t, u))
+                    elif _agprs(u) & dst:
+                        found.append((name, t, u))
+                    w += int(u.split()[1], 0) + 1 if op == "s_nop" else 1
+                    if op == "s_endpgm":
+                        break
+                    if op == "s_branch":
+                        p = labels[u.split()[1]]
+                        continue
+                    if op.startswith("s_cbranch"):
+                        stack.append((labels[u.split()[1]], w))
+                    p += 1
+    return found
+
+
+_TOY = """
+\t.type\t_Zk,@function
+_Zk:
+\t;;#ASMSTART
+\ts_nop 2
+\tv_mfma_f32_16x16x32_f16 a[0:3], v[0:3], v[4:7], a[0:3]
+\t;;#ASMEND
+{between}
+\tv_accvgpr_read_b32 v8, a2
+\ts_endpgm
+.Lfunc_end0:
+"""
+
+
+def test_checker_finds_a_planted_hazard():
+    assert len(hazards(_TOY.format(between=""))) == 1
+    # a branch to a block that reads the result is followed
+    branchy = _TOY.format(between="\ts_cbranch_scc1 .LBB0_2\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n"
+                                   "\ts_endpgm\n.LBB0_2:")
+    assert len(hazards(branchy)) == 1
+    # other registers, and reads past the window, are fine
+    assert hazards(_TOY.format(between="").replace("a2", "a4")) == []
+    assert hazards(_TOY.format(between="\ts_nop 7\n\ts_nop 7\n\ts_nop 7")) == []
+
+
+def test_decode_kernels_have_no_asm_mfma_hazards(tmp_path):
+    spec = importlib.util.spec_from_file_location("sixi_build", BUILD)
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    try:
+        hipcc = build._hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    flags = [f for f in build.HIP_FLAGS if f != "-fPIC"]
+    out = tmp_path / "fa_decode.s"
+    proc = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", str(out), str(build.CSRC / "fa_decode.hip")],
+                          stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert proc.returncode == 0, proc.stdout[-2000:]
+    asm = out.read_text()
+    assert asm.count("v_mfma_f32_16x16x32_f16 a[") > 0, "no asm MFMAs found: the check would be vacuous"
+    bad = hazards(asm)
+    assert not bad, f"{len(bad)} hazards, first: {bad[:3]}"
