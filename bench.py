@@ -8,7 +8,9 @@ plus its merge kernel, timed with HIP events on the stream the library launches 
 resident in HBM.
 
 Prints one JSON line: value = algorithmic HBM GB/s of the verify call (K/V of every attended
-cell + Q + O, counted once); roofline = that rate against the 8 TB/s HBM peak; the other
+cell + Q + O, counted once) at the median per-call time (p10/p90 beside it); roofline = that
+rate against the 8 TB/s HBM peak; verify_explicit_mask = the same call with the mask handed
+over as a ggml KQ mask (the drop-in path); the other
 configurations (single-stream decode and verify, long q8_0 decode/verify, chunked prefill)
 are reported beside it when their kernels are built; cpu_baseline = the oracle (a
 restatement of ggml's CPU flash_attn_ext, f16 V accumulator as upstream) on the host cores,
@@ -42,8 +44,9 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_calls(fa, w, dev, steps: int, warmup: int, out=None):
-    """Per-call GPU times (ms) with events on the stream the library launches on."""
+def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None):
+    """Per-call GPU times (ms) with events on the stream the library launches on.  With `mask`
+    (a ggml f16 KQ mask) the calls take the explicit-mask path instead of w.mask_mode."""
     import torch
 
     import sixi_attn as sa
@@ -52,9 +55,11 @@ def time_calls(fa, w, dev, steps: int, warmup: int, out=None):
         out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
 
+    mode = w.mask_mode if mask is None else sa.MASK_EXPLICIT
+
     def call():
         fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
-           mask_mode=w.mask_mode, stream=stream.cuda_stream)
+           mask_mode=mode, mask=mask, stream=stream.cuda_stream)
 
     for _ in range(warmup):
         call()
@@ -70,35 +75,76 @@ def time_calls(fa, w, dev, steps: int, warmup: int, out=None):
     return total / steps, per
 
 
+def ws_bytes(fa, w, dev, mask=None) -> int:
+    """sixi_attn_workspace_bytes of a call of workload w (q8_0 prefill-sized blocks and
+    256-dim q8_0 calls include the f16 staging of the cache)."""
+    import torch
+
+    import sixi_attn as sa
+
+    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    p = fa.params(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
+                  mask_mode=w.mask_mode if mask is None else sa.MASK_EXPLICIT, mask=mask)
+    return int(fa.workspace_bytes(p))
+
+
 def summarize(w, ms: float, per) -> dict:
+    """Mean (`us`, over the bracketed calls), median and p10/p90 of the per-call times; the
+    rates are taken at the median."""
     per_sorted = sorted(per)
     n = len(per_sorted)
+    med = statistics.median(per_sorted)
     return {
         "us": round(ms * 1e3, 2),
+        "us_median": round(med * 1e3, 2),
         "us_p10_p50_p90": [round(per_sorted[n // 10] * 1e3, 2), round(per_sorted[n // 2] * 1e3, 2),
                            round(per_sorted[(9 * n) // 10] * 1e3, 2)],
-        "GBps": round(w.bytes() / (ms * 1e-3) / 1e9, 1),
-        "TFLOPs": round(w.flops() / (ms * 1e-3) / 1e12, 2),
+        "GBps": round(w.bytes() / (med * 1e-3) / 1e9, 1),
+        "TFLOPs": round(w.flops() / (med * 1e-3) / 1e12, 2),
+        "GBps_mean": round(w.bytes() / (ms * 1e-3) / 1e9, 1),
         "bytes": w.bytes(),
         "flops": w.flops(),
     }
 
 
-def cpu_baseline(w, host, repeats: int = 5) -> dict:
+def _cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as "Model name")."""
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(w, host, gpu_out=None, repeats: int = 5) -> dict:
     """The oracle on the host cores: the whole verify workload (all 32 streams) on every
-    core of the process affinity, median of `repeats` runs after one warm-up, plus one
-    stream on one thread."""
+    core of the process affinity, median of `repeats` runs after one warm-up, with the f16 V
+    accumulator of ggml's CPU kernel (upstream) and, beside it, with an f32 accumulator; plus
+    one stream on one thread.  With `gpu_out` (the GPU's output of the same workload,
+    [S, n_q, H, D]) the distances of the GPU result from both CPU modes are reported over the
+    valid rows (mean-abs, RMSE, KL, ... as compute_diff_metrics)."""
     sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
+
     import oracle
 
     threads = oracle.cpu_threads()
     oracle.attention_for_workload(host, w.kv_type, [0], v_acc_f16=True, n_threads=threads)
-    runs = []
-    for _ in range(repeats):
-        t0 = time.perf_counter()
-        oracle.attention_for_workload(host, w.kv_type, None, v_acc_f16=True, n_threads=threads)
-        runs.append(time.perf_counter() - t0)
-    dt = statistics.median(runs)
+
+    def timed(acc16):
+        runs, out = [], None
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            out = oracle.attention_for_workload(host, w.kv_type, None, v_acc_f16=acc16, n_threads=threads)
+            runs.append(time.perf_counter() - t0)
+        return statistics.median(runs), out
+
+    dt, ref16 = timed(True)
+    dt32, ref32 = timed(False)
     # one stream near the mean length on one thread
     lens = [abs(x - sum(w.kv_len) / w.S) for x in w.kv_len]
     s1 = lens.index(min(lens))
@@ -107,18 +153,34 @@ def cpu_baseline(w, host, repeats: int = 5) -> dict:
     dt1 = time.perf_counter() - t0
     sub = type(w)(w.name, w.seed, 1, [w.kv_len[s1]], [w.q_len[s1]], H=w.H, Hkv=w.Hkv, D=w.D,
                   kv_type=w.kv_type, q_type=w.q_type)
-    return {
+    res = {
         "value": round(w.bytes() / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": _cpu_model(),
         "sample": f"the whole workload ({w.S} streams, {sum(w.kv_len)} cached cells, {sum(w.q_len)} rows), "
                   f"f16 V accumulator as ggml's CPU kernel, median of {repeats} runs: {dt * 1e3:.1f} ms/call",
         "us_per_call": round(dt * 1e6, 1),
+        "f32_accumulator": {"value": round(w.bytes() / dt32 / 1e9, 3), "unit": "GB/s",
+                            "us_per_call": round(dt32 * 1e6, 1),
+                            "sample": f"same workload, f32 V accumulator, median of {repeats} runs"},
         "one_thread": {"value": round(sub.bytes() / dt1 / 1e9, 3), "unit": "GB/s",
                        "sample": f"stream {s1} ({w.kv_len[s1]} cached cells, {w.q_len[s1]} rows), "
                                  f"{dt1 * 1e3:.1f} ms"},
     }
+    if gpu_out is not None:
+        ql = host["q_len"]
+
+        def rows(x):
+            return np.concatenate([x[s, :ql[s]].ravel() for s in range(w.S)]).astype(np.float64)
+
+        g = rows(gpu_out)
+        res["gpu_vs_cpu"] = {}
+        for name, ref in (("f16_accumulator_upstream", ref16), ("f32_accumulator", ref32)):
+            m = oracle.diff_metrics(rows(ref), g)
+            res["gpu_vs_cpu"][name] = {k: (float(f"{v:.4g}") if isinstance(v, float) else v) for k, v in m.items()}
+    return res
 
 
 def traffic_from_profile():
@@ -159,11 +221,11 @@ def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None):
             wp = dataclasses.replace(wp, D=head_dim)
         dp = wl.to_device(wl.make_host(wp))
         msp, _ = time_calls(fa, wp, dp, steps, warmup)
-        pre.append((wp, msp))
+        pre.append((wp, msp, ws_bytes(fa, wp, dp)))
         del dp
-    flops = sum(wp.flops() for wp, _ in pre)
-    t = sum(msp for _, msp in pre)
-    return flops / (t * 1e-3) / 1e12, t * 1e3
+    flops = sum(wp.flops() for wp, _, _ in pre)
+    t = sum(msp for _, msp, _ in pre)
+    return flops / (t * 1e-3) / 1e12, t * 1e3, max(b for _, _, b in pre)
 
 
 def time_kv_store(w, dev, steps: int, warmup: int) -> dict:
@@ -355,7 +417,7 @@ def prefill_only(steps: int, warmup: int) -> int:
     import sixi_attn as sa
 
     fa = sa.FlashAttnExt()
-    tf, us = time_prefill(fa, max(1, steps), warmup)
+    tf, us, _ = time_prefill(fa, max(1, steps), warmup)
     print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks", "us_two_chunks": round(us, 2),
                       "TFLOPs": round(tf, 2)}), flush=True)
     return 0
@@ -402,10 +464,12 @@ def main() -> int:
     host = wl.make_host(w)
     dev = wl.to_device(host)
     _log(f"timing {args.steps} steps after {args.warmup} warm-up")
-    ms, per = time_calls(fa, w, dev, args.steps, args.warmup)
+    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    ms, per = time_calls(fa, w, dev, args.steps, args.warmup, out=out)
     head = summarize(w, ms, per)
     gbs = head["GBps"]
-    _log(f"verify: {head['us']} us/call, {gbs} GB/s, {head['TFLOPs']} TFLOP/s")
+    _log(f"verify: median {head['us_median']} us/call (mean {head['us']}), {gbs} GB/s, {head['TFLOPs']} TFLOP/s")
+    gpu_out = out.cpu().numpy()
 
     traffic = traffic_from_profile()
     result = {
@@ -427,8 +491,12 @@ def main() -> int:
             "streams": w.S, "rows_per_stream": 16, "mean_cached_len": round(sum(w.kv_len) / w.S, 1),
             "bytes_per_call": w.bytes(), "flops_per_call": w.flops(),
         },
-        "us_per_layer": head["us"],
+        "value_stat": "median of the per-call times (HIP events between consecutive calls); "
+                      "ms_per_step is the mean over the bracketed steps",
+        "us_per_layer": head["us_median"],
+        "us_per_layer_mean": head["us"],
         "us_per_layer_p10_p50_p90": head["us_p10_p50_p90"],
+        "workspace_bytes": ws_bytes(fa, w, dev),
         "verify_tflops": head["TFLOPs"],
         "roofline": {
             "bound": "hbm",
@@ -439,8 +507,19 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": f"{TRAFFIC_PROFILE.relative_to(ROOT)} (FETCH_SIZE + WRITE_SIZE of a separate "
+                              "rocprofv3 --pmc run of this command, scaled by the copy calibration)",
         },
     }
+
+    # the same verify with the block-causal mask handed over as an explicit ggml KQ mask (the
+    # ggml FLASH_ATTN_EXT drop-in path)
+    mask = torch.from_numpy(wl.kq_mask(dev["k"].shape[1], w.n_q, w.kv_len, w.q_len)).view(torch.float16).cuda()
+    msm, perm = time_calls(fa, w, dev, max(20, args.steps // 2), max(5, args.warmup // 2), mask=mask)
+    result["verify_explicit_mask"] = summarize(w, msm, perm)
+    result["verify_explicit_mask"]["workspace_bytes"] = ws_bytes(fa, w, dev, mask=mask)
+    _log(f"verify, explicit mask: {result['verify_explicit_mask']}")
+    del mask
 
     if not args.no_extra:
         extra = {}
@@ -451,6 +530,7 @@ def main() -> int:
                 de = wl.to_device(he)
                 mse, pere = time_calls(fa, we, de, max(20, args.steps // 2), max(5, args.warmup // 2))
                 extra[name] = summarize(we, mse, pere)
+                extra[name]["workspace_bytes"] = ws_bytes(fa, we, de)
                 # the eager figure includes the host's issue time when a call is shorter than it
                 # (decode); GPU time per call from HIP-graph replays of the same call
                 oute = torch.empty((we.S, we.n_q, we.H, we.D), dtype=torch.float32, device="cuda")
@@ -484,17 +564,20 @@ def main() -> int:
 
         # chunked causal prefill (2 chunks of 2048 rows on a 2048-cell cache)
         try:
-            tf, us = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4))
+            tf, us, wsb = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4))
+            result["prefill_workspace_bytes"] = wsb
             result["prefill_tflops"] = round(tf, 2)
             result["prefill_us_two_chunks"] = round(us, 2)
             result["prefill_roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": F16_PEAK_TFLOPS,
                                           "unit": "TFLOP/s", "frac": round(tf / F16_PEAK_TFLOPS, 4)}
             _log(f"prefill: {us:.1f} us for 2 chunks, {tf:.1f} TFLOP/s")
-            tq, uq = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0)
-            result["configs"]["prefill_q8_0"] = {"us_two_chunks": round(uq, 2), "TFLOPs": round(tq, 2)}
+            tq, uq, wsq = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0)
+            result["configs"]["prefill_q8_0"] = {"us_two_chunks": round(uq, 2), "TFLOPs": round(tq, 2),
+                                                 "workspace_bytes": wsq}
             _log(f"prefill q8_0 KV: {uq:.1f} us for 2 chunks, {tq:.1f} TFLOP/s")
-            td, ud = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), head_dim=256)
-            result["configs"]["prefill_d256"] = {"us_two_chunks": round(ud, 2), "TFLOPs": round(td, 2)}
+            td, ud, wsd = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), head_dim=256)
+            result["configs"]["prefill_d256"] = {"us_two_chunks": round(ud, 2), "TFLOPs": round(td, 2),
+                                                 "workspace_bytes": wsd}
             _log(f"prefill 256-dim heads: {ud:.1f} us for 2 chunks, {td:.1f} TFLOP/s")
         except sa.SixiAttnError as e:
             result["prefill_tflops"] = None
@@ -503,7 +586,7 @@ def main() -> int:
 
     if not args.no_cpu:
         _log("CPU baseline (oracle on host cores)")
-        result["cpu_baseline"] = cpu_baseline(w, host)
+        result["cpu_baseline"] = cpu_baseline(w, host, gpu_out)
     print(json.dumps(result), flush=True)
     return 0
 

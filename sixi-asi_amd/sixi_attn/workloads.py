@@ -130,6 +130,23 @@ class Workload:
         return 4 * self.D * self.H * vis
 
 
+def kq_mask(n_kv: int, n_q_pad: int, kv_len, q_len, causal: bool = True) -> np.ndarray:
+    """The llama-style f16 KQ mask of a stream-major block, [S, 1, n_q_pad, n_kv] as f16 bits
+    (uint16): row j of stream s sees cell i when j < q_len[s], i < kv_len[s] + q_len[s] and
+    (causal) i <= kv_len[s] + j -- positions N_s + j, one sequence per stream
+    (src/core/core_execution.cpp:2047-2062) -- 0 there and -inf elsewhere."""
+    kl = np.asarray(kv_len, dtype=np.int64)[:, None, None]
+    ql = np.asarray(q_len, dtype=np.int64)[:, None, None]
+    if np.any(kl + ql > n_kv) or np.any(ql > n_q_pad) or np.any(kl < 0) or np.any(ql < 0):
+        raise ValueError("stream cells exceed the mask")
+    j = np.arange(n_q_pad, dtype=np.int64)[None, :, None]
+    i = np.arange(n_kv, dtype=np.int64)[None, None, :]
+    vis = (j < ql) & (i < kl + ql)
+    if causal:
+        vis &= i <= kl + j
+    return np.where(vis, np.uint16(0), np.uint16(0xFC00)).astype(np.uint16)[:, None]
+
+
 def config(name: str) -> Workload:
     """The five configurations of the attention path (decode, verify, batched verify,
     chunked prefill, long q8_0 decode/verify)."""

@@ -147,6 +147,21 @@ def test_mask_builder_semantics():
     assert np.isfinite(nc[0, 0, 0]).sum() == 5 and np.isfinite(nc[0, 0, 1]).sum() == 5
 
 
+def test_workload_mask_builder_matches_the_oracle():
+    """The package's numpy mask (used by bench.py's explicit-mask timing) equals the oracle's,
+    bit for bit, on ragged streams, empty blocks and both mask kinds."""
+    from sixi_attn import workloads as wl
+
+    for kl, ql, n_kv, n_q in (([3, 0], [2, 4], 12, 4), ([700, 5, 0, 31], [16, 1, 0, 16], 768, 16), ([0], [1], 1, 1)):
+        for causal in (True, False):
+            want = oracle.build_kq_mask(n_kv, n_q, kl, ql, causal)
+            got = wl.kq_mask(n_kv, n_q, kl, ql, causal)
+            assert got.shape == want.shape and got.dtype == np.uint16
+            assert np.array_equal(got, want)
+    with pytest.raises(ValueError):
+        wl.kq_mask(10, 4, [8], [3])
+
+
 def test_poisoned_cells_past_the_length_are_never_used():
     q, k, v, kl, ql = _case()
     a = _run(q, k, v, kl, ql)
