@@ -34,7 +34,10 @@
 extern "C" {
 #endif
 
-#define SIXI_ATTN_ABI_VERSION 1
+#define SIXI_ATTN_ABI_VERSION 2
+
+/* Cells per page of a paged KV cache (include/sixi_asi/manifest.hpp:124 page_size_tokens). */
+#define SIXI_KV_PAGE_CELLS 256
 
 /* ggml type ids (include/sixi_asi/common.hpp:170-180 QuantType: F32 0, F16 1, Q8_0 8) */
 enum {
@@ -82,8 +85,11 @@ typedef struct sixi_view {
 typedef struct sixi_attn_params {
     sixi_view q;            /* [D, n_q, H, S]    f32 or f16                                */
     sixi_view k;            /* [D, n_kv, Hkv, S] f16 or q8_0; nb[1] cell, nb[2] head,
-                               nb[3] stream (a 256-cell page multiple in the engine)      */
-    sixi_view v;            /* [D, n_kv, Hkv, S] f16 or q8_0, same D as k                 */
+                               nb[3] stream (a 256-cell page multiple in the engine);
+                               paged (page_table != NULL): the page pool
+                               [D, SIXI_KV_PAGE_CELLS, Hkv, n_pages], nb[3] = page stride  */
+    sixi_view v;            /* [D, n_kv, Hkv, S] f16 or q8_0, same D as k (paged: the same
+                               pool shape as k)                                            */
     sixi_view out;          /* [D, H, n_q, S]    f32 (ggml's permuted output)             */
     const int32_t* kv_len;  /* device [S]: cells cached before the block, or NULL          */
     const int32_t* q_len;   /* device [S]: rows of stream s (<= n_q), or NULL (= n_q)      */
@@ -98,6 +104,14 @@ typedef struct sixi_attn_params {
                                256-byte aligned; its contents need no initialisation       */
     size_t workspace_bytes;
     void* stream;           /* hipStream_t; NULL = the null stream                         */
+    /* Paged KV (optional).  NULL: k and v hold each stream's cells as one range.  Otherwise
+     * cell c of stream s is cell c % SIXI_KV_PAGE_CELLS of page
+     * page_table[s * page_table_stride + c / SIXI_KV_PAGE_CELLS] of the k and v pools, and a
+     * stream has n_kv = page_table_stride * SIXI_KV_PAGE_CELLS cells.  Device memory, int32,
+     * 4-byte aligned; only the entries of cells a row can see are read, each clamped to
+     * [0, n_pages) on the device.  Streams may share pages (sixi_kv_pool_seq_cp). */
+    const int32_t* page_table;
+    int64_t page_table_stride;
 } sixi_attn_params;
 
 /* Launches the attention for every stream, head and row.  Rows j >= q_len[s] are not

@@ -37,6 +37,7 @@ HIP_FLAGS = [
     f"-I{CSRC}",
 ]
 HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "fa_q8_stage.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
+               "sixi_kv_pool.cpp",
                "sixi_plan.cpp", "layer_prologue.hip", "sixi_layer_abi.cpp",
                "gdn_verify.hip", "sixi_gdn_abi.cpp"]
 

@@ -544,13 +544,10 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
     Acc<NTW> acc;
     acc_clear(acc);
 
-    // K/V of this (stream, kv-head) through range-checked buffer resources: cells >= nc read
-    // as zeros (and are masked), so the tail tile needs no clamping and cannot fault.
+    // K/V of this (stream, kv-head), per tile through range-checked buffer resources based at
+    // the tile's first cell (in its page, for paged caches): cells >= nc read as zeros (and are
+    // masked), so the tail tile needs no clamping and cannot fault.
     const int64_t rowb = (KV == SIXI_TYPE_F16) ? 128 * 2 : kQ8Row;
-    const buf_rsrc krs = make_rsrc(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
-                                     (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + rowb));
-    const buf_rsrc vrs = make_rsrc(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
-                                     (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + rowb));
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
 
     // tiles of this lane: tb + tl + TL*i, i < n_my
@@ -574,11 +571,15 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 
     // Stage tile i of this lane into slot i % NSLOT.
     auto issue = [&](int i) {
-        const uint32_t c0 = (uint32_t)(t0 + i * TL) * kTile;
+        const int c0 = (t0 + i * TL) * kTile;
         const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * KvTile<KV>::slot_bytes;
+        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, c0, sd.nc, rowb);
+        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, c0, sd.nc, rowb);
+        const buf_rsrc krs = make_rsrc_uniform(ksp.p, ksp.bytes);
+        const buf_rsrc vrs = make_rsrc_uniform(vsp.p, vsp.bytes);
         if constexpr (KV == SIXI_TYPE_F16) {
-            const uint32_t off = (c0 + r) * knb + c * 16;
-            const uint32_t vo = (c0 + 4 * c) * vnb + r * 16;
+            const uint32_t off = r * knb + c * 16;
+            const uint32_t vo = (4 * c) * vnb + r * 16;
             uint32_t ko4[4], vo4[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -592,8 +593,8 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
             uint32_t ko[kQ8Dma], vo[kQ8Dma];
 #pragma unroll
             for (int u = 0; u < kQ8Dma; ++u) {
-                ko[u] = (c0 + q8_cell[u]) * knb + q8_dw[u] * 4;
-                vo[u] = (c0 + q8_cell[u]) * vnb + q8_dw[u] * 4;
+                ko[u] = q8_cell[u] * knb + q8_dw[u] * 4;
+                vo[u] = q8_cell[u] * vnb + q8_dw[u] * 4;
             }
             dma4x9_to_lds(krs, ko, base);
             dma4x9_to_lds(vrs, vo, base + kQ8Dma * 256);
@@ -1056,11 +1057,8 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     Acc<NTW, W::DT> acc;
     acc_clear(acc);
 
-    // cells >= nc read as zeros through the range-checked resources (and are masked)
-    const buf_rsrc krs = make_rsrc_uniform(a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2,
-                                           (uint32_t)((int64_t)(sd.nc - 1) * a.k_nb1 + W::ROW));
-    const buf_rsrc vrs = make_rsrc_uniform(a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2,
-                                           (uint32_t)((int64_t)(sd.nc - 1) * a.v_nb1 + W::ROW));
+    // K/V per step through range-checked resources based at the step's first cell (in its page,
+    // for paged caches): cells >= nc read as zeros (and are masked)
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
     // LDS-DMA source offsets from a step's first cell; every load copies the ROW-byte rows of
     // CPL cells (1 KB, whole cache lines).  K (row group 0), load u: lane t fills LDS row
@@ -1093,6 +1091,10 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     auto issue = [&](int i, int slot) {
         const uint32_t c0 = (uint32_t)(t0 + i * TL) * kWide;
         const uint32_t base = ring_base + (uint32_t)slot * W::SLOT;
+        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, (int)c0, sd.nc, W::ROW);
+        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, (int)c0, sd.nc, W::ROW);
+        const buf_rsrc krs = make_rsrc_uniform(ksp.p, ksp.bytes);
+        const buf_rsrc vrs = make_rsrc_uniform(vsp.p, vsp.bytes);
         const uint32_t pos = (uint32_t)lane % W::CPR;  // 16-byte position in the row
         if constexpr (GEN) {
             // mask rows 16*half + lane/4, cells c0 + 8*(lane%4) .. +7: 1 KB per load, laid out
@@ -1113,7 +1115,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const uint32_t cell = W::CPL * (8 * b8 + u) + (uint32_t)lane / W::CPR;
-                    o8[u] = (c0 + cell) * knb + 16u * (pos ^ (cell & 15u));
+                    o8[u] = cell * knb + 16u * (pos ^ (cell & 15u));
                 }
                 dma16x8_to_lds(krs, o8, base + 8192u * b8);
             }
@@ -1121,7 +1123,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const uint32_t cell = W::CPL * (8 * b8 + u) + (uint32_t)lane / W::CPR;
-                    o8[u] = (c0 + cell) * vnb + 32u * ((pos >> 1) ^ (cell & 7u)) + 16u * (pos & 1u);
+                    o8[u] = cell * vnb + 32u * ((pos >> 1) ^ (cell & 7u)) + 16u * (pos & 1u);
                 }
                 dma16x8_to_lds(vrs, o8, base + 32 * W::ROW + 8192u * b8);
             }

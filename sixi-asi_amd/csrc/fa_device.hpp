@@ -317,6 +317,32 @@ __device__ __forceinline__ StreamDims stream_dims(const FaArgs& a, int s) {
     return stream_dims_from(a, q_raw, kv_raw);
 }
 
+// K or V rows of (stream s, kv-head g) from cell c0 on, for a range-checked buffer resource:
+// the address of cell c0's row, and the bytes from there to the end of the last row a load may
+// use -- rows up to cell nc - 1 that lie in c0's page (paged caches) or in the stream
+// (contiguous).  Offsets from the address are (c - c0) * nb1.  0 bytes when c0 >= nc (the page
+// table is then not read).  Every tile of the kernels lies in one page: tiles of 16, 32 and 64
+// cells start at multiples of their size, and pages hold 256 cells.
+struct KvSpan {
+    const char* p;
+    uint32_t bytes;
+};
+__device__ __forceinline__ KvSpan kv_span(const FaArgs& a, const char* kv, int64_t nb1, int64_t nb2, int64_t nb3, int s,
+                                          int g, int c0, int nc, int64_t rowb) {
+    if (c0 >= nc) return {kv, 0u};
+    int64_t off;
+    int last = nc;
+    if (a.pt) {
+        const int idx = __builtin_amdgcn_readfirstlane((int)((int64_t)s * a.pt_stride + (c0 >> 8)));
+        const int page = min(max(a.pt[idx], 0), a.n_pages - 1);
+        off = (int64_t)page * nb3 + (int64_t)(c0 & (kPageCells - 1)) * nb1;
+        last = min(nc, (c0 | (kPageCells - 1)) + 1);
+    } else {
+        off = (int64_t)s * nb3 + (int64_t)c0 * nb1;
+    }
+    return {kv + off + (int64_t)g * nb2, (uint32_t)((int64_t)(last - 1 - c0) * nb1 + rowb)};
+}
+
 // ALiBi slope of q-head h (ggml's rule); 1 when ALiBi is off.
 __device__ __forceinline__ float alibi_slope(const FaArgs& a, int h) {
     if (a.alibi_nlog2 == 0) return 1.0f;

@@ -17,9 +17,13 @@ struct FaArgs {
     int32_t q_f16;
 
     const char* k;         // cell c of head g of stream s at k + c*k_nb1 + g*k_nb2 + s*k_nb3
-    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;  // (paged: k_nb3 is the page stride, see pt)
     const char* v;
     int64_t v_nb1, v_nb2, v_nb3;
+    const int32_t* pt;     // paged KV: cell c of stream s in cell c % 256 of page
+                           // pt[s*pt_stride + c/256] (clamped to [0, n_pages)); null: contiguous
+    int64_t pt_stride;
+    int32_t n_pages;
 
     char* out;             // row (d, h, j, s) at out + d*4 + h*o_nb1 + j*o_nb2 + s*o_nb3
     int64_t o_nb1, o_nb2, o_nb3;
@@ -64,6 +68,9 @@ struct Q8StageArgs {
     int64_t k_nb1, k_nb2, k_nb3;
     const char* v;
     int64_t v_nb1, v_nb2, v_nb3;
+    const int32_t* pt;     // paged source cache (as FaArgs::pt), or null
+    int64_t pt_stride;
+    int32_t n_pages;
     const int32_t* kv_len;
     const int32_t* q_len;
     int32_t S, H, Hkv, n_q, D;
@@ -83,6 +90,8 @@ constexpr int kDecodeTile = 16;        // KV cells per wave step of the decode k
 constexpr int kDecodeTileWide = 32;    // KV cells per step of the f16 kernel for 49..96 rows
 constexpr int kDecodeMaxRowTiles = 6;  // 16-row MFMA tiles per (stream, kv-head): G*q_len <= 96
 constexpr int kMaxStreams = 512;       // LDS prefix table bound
+constexpr int kPageCells = SIXI_KV_PAGE_CELLS;  // paged KV: cells per page (a multiple of every tile)
+static_assert(kPageCells == 256, "page arithmetic below uses c >> 8 and c & 255");
 constexpr int kMaxSplitGroups = 2048;  // work-groups of a split-K launch (workspace bound)
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
 int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles);

@@ -138,12 +138,9 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     }
 
     // K/V of (stream, kv-head): every tile gets its own range-checked buffer resource whose
-    // base is the tile's first cell, so cells >= nc read as zero and no load can fault
+    // base is the tile's first cell (in its page, for paged caches), so cells >= nc read as
+    // zero and no load can fault
     const int64_t rowb = P::ROW;
-    const char* kbase = a.k + (int64_t)s * a.k_nb3 + (int64_t)g * a.k_nb2;
-    const char* vbase = a.v + (int64_t)s * a.v_nb3 + (int64_t)g * a.v_nb2;
-    const int64_t kbytes = (int64_t)(sd.nc - 1) * a.k_nb1 + rowb;
-    const int64_t vbytes = (int64_t)(sd.nc - 1) * a.v_nb1 + rowb;
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
 
     // ---- per-lane LDS byte offsets, fixed for the whole loop ----
@@ -187,10 +184,10 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     }
 
     auto issue_kv = [&](int t, int buf) {
-        const int64_t ko = (int64_t)t * kBN * knb;
-        const buf_rsrc krs = make_rsrc(kbase + ko, (uint32_t)(kbytes > ko ? kbytes - ko : 0));
-        const int64_t vo = (int64_t)t * kBN * vnb;
-        const buf_rsrc vrs = make_rsrc(vbase + vo, (uint32_t)(vbytes > vo ? vbytes - vo : 0));
+        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, t * kBN, sd.nc, rowb);
+        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, t * kBN, sd.nc, rowb);
+        const buf_rsrc krs = make_rsrc_uniform(ksp.p, ksp.bytes);
+        const buf_rsrc vrs = make_rsrc_uniform(vsp.p, vsp.bytes);
         if constexpr (P::LW == 4) {
             dma16x4_to_lds(krs, kdo, lds0 + buf * kKBytes + 4 * w * 1024);
             dma16x4_to_lds(vrs, vdo, lds0 + kVBase + buf * kVBytes + 4 * w * 1024);

@@ -49,8 +49,16 @@ __global__ __launch_bounds__(256) void q8_kv_to_f16(Q8StageArgs a, int which) {
         nc = ql > 0 ? kl + ql : 0;
     }
     if (cell >= nc) return;
+    // the cell's row: in its stream's range, or (paged) in its page
+    int64_t row_off;
+    if (a.pt) {
+        const int page = min(max(a.pt[(int64_t)s * a.pt_stride + (cell >> 8)], 0), a.n_pages - 1);
+        row_off = (int64_t)page * nb3 + (cell & (kPageCells - 1)) * nb1;
+    } else {
+        row_off = (int64_t)s * nb3 + cell * nb1;
+    }
     // a q8_0 block is 34 bytes: the f16 scale, then 32 int8 quants (2-byte aligned)
-    const uint16_t* blk = reinterpret_cast<const uint16_t*>(src + cell * nb1 + (int64_t)h * nb2 + (int64_t)s * nb3 + b * 34);
+    const uint16_t* blk = reinterpret_cast<const uint16_t*>(src + row_off + (int64_t)h * nb2 + b * 34);
     const float d = (float)__builtin_bit_cast(_Float16, blk[0]);
     u32x4* o = reinterpret_cast<u32x4*>(dst + ((((int64_t)s * a.n_kv + cell) * a.Hkv + h) * a.D + b * 32) * 2);
 #pragma unroll

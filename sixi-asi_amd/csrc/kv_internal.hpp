@@ -22,6 +22,10 @@ struct KvWriteArgs {
     int64_t n_cells;
     const int32_t* kv_len;  // may be null: row j -> cell j
     const int32_t* q_len;   // may be null: every row
+    const int32_t* pt;      // paged cache: cell c of stream s -> cell c % 256 of page
+                            // pt[s*pt_stride + c/256] (d_nb3 the page stride); null: contiguous
+    int64_t pt_stride;
+    int n_pages;
 };
 
 // Cells [src_cell, src_cell + n_cells) of stream src_stream -> [dst_cell, ...) of

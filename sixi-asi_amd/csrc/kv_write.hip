@@ -71,7 +71,14 @@ __global__ __launch_bounds__(256) void kv_write_kernel(KvWriteArgs a) {
     float x[32];
     load_block(a.src + (int64_t)j * a.s_nb1 + (int64_t)h * a.s_nb2 + (int64_t)s * a.s_nb3 + (int64_t)b * 32 * a.s_es,
                a.src_f16 != 0, x);
-    char* row = a.dst + cell * a.d_nb1 + (int64_t)h * a.d_nb2 + (int64_t)s * a.d_nb3;
+    int64_t row_off;
+    if (a.pt) {
+        const int page = min(max(a.pt[(int64_t)s * a.pt_stride + (cell >> 8)], 0), a.n_pages - 1);
+        row_off = (int64_t)page * a.d_nb3 + (cell & 255) * a.d_nb1;
+    } else {
+        row_off = cell * a.d_nb1 + (int64_t)s * a.d_nb3;
+    }
+    char* row = a.dst + row_off + (int64_t)h * a.d_nb2;
     if (!a.dst_q8) {
         u32x4* o = reinterpret_cast<u32x4*>(row + (int64_t)b * 64);
 #pragma unroll

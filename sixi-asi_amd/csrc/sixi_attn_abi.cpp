@@ -83,9 +83,22 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     for (int d = 0; d < 4; ++d)
         if (q.ne[d] <= 0 || k.ne[d] <= 0 || v.ne[d] <= 0 || o.ne[d] <= 0) return SIXI_E_INVALID_ARGUMENT;
     const int64_t D = q.ne[0], n_q = q.ne[1], H = q.ne[2], S = q.ne[3];
-    const int64_t n_kv = k.ne[1], Hkv = k.ne[2];
+    const int64_t Hkv = k.ne[2];
+    // paged: k and v are pools of 256-cell pages, a stream spans page_table_stride pages
+    const bool paged = p->page_table != nullptr;
+    int64_t n_kv = k.ne[1];
     if (k.ne[0] != D || v.ne[0] != D) return SIXI_E_INVALID_ARGUMENT;
-    if (v.ne[1] != n_kv || v.ne[2] != Hkv || k.ne[3] != S || v.ne[3] != S) return SIXI_E_INVALID_ARGUMENT;
+    if (paged) {
+        if (k.ne[1] != SIXI_KV_PAGE_CELLS || v.ne[1] != SIXI_KV_PAGE_CELLS || v.ne[2] != Hkv || v.ne[3] != k.ne[3])
+            return SIXI_E_INVALID_ARGUMENT;
+        if (p->page_table_stride <= 0 || p->page_table_stride > ((int64_t)1 << 26) / SIXI_KV_PAGE_CELLS)
+            return SIXI_E_INVALID_ARGUMENT;
+        if (k.ne[3] > INT32_MAX) return SIXI_E_UNSUPPORTED;
+        if (!aligned(p->page_table, 4)) return SIXI_E_ALIGNMENT;
+        n_kv = p->page_table_stride * SIXI_KV_PAGE_CELLS;
+    } else if (v.ne[1] != n_kv || v.ne[2] != Hkv || k.ne[3] != S || v.ne[3] != S) {
+        return SIXI_E_INVALID_ARGUMENT;
+    }
     if (H % Hkv != 0) return SIXI_E_INVALID_ARGUMENT;
     if (o.ne[0] != D || o.ne[1] != H || o.ne[2] != n_q || o.ne[3] != S) return SIXI_E_INVALID_ARGUMENT;
     if (S > sixi::kMaxStreams || H > 4096 || n_q > (1 << 20) || n_kv > (1 << 26)) return SIXI_E_UNSUPPORTED;
@@ -107,9 +120,11 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     const int64_t kvrow = row_bytes(k.type, D);
     if (k.nb[1] < kvrow || v.nb[1] < kvrow) return SIXI_E_INVALID_ARGUMENT;  // rows must not overlap
     if (o.nb[1] < D * 4 || q.nb[1] < D * qes) return SIXI_E_INVALID_ARGUMENT;
-    // one stream's cells (plus one tile of read-ahead) are addressed with 32-bit offsets
+    // the cells a buffer resource covers -- the rest of a stream (plus one tile of read-ahead),
+    // or of a page -- are addressed with 32-bit offsets
+    const int64_t span_cells = (paged ? SIXI_KV_PAGE_CELLS : n_kv) + sixi::kDecodeTileWide;
     int64_t kspan = 0, vspan = 0;
-    if (!mul_ok(n_kv + sixi::kDecodeTileWide, k.nb[1], &kspan) || !mul_ok(n_kv + sixi::kDecodeTileWide, v.nb[1], &vspan) ||
+    if (!mul_ok(span_cells, k.nb[1], &kspan) || !mul_ok(span_cells, v.nb[1], &vspan) ||
         kspan >= (int64_t)UINT32_MAX || vspan >= (int64_t)UINT32_MAX)
         return SIXI_E_UNSUPPORTED;
     if (view_span(q, D * qes) < 0 || view_span(k, kvrow) < 0 || view_span(v, kvrow) < 0 ||
@@ -146,6 +161,11 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     a.k_nb1 = k.nb[1]; a.k_nb2 = k.nb[2]; a.k_nb3 = k.nb[3];
     a.v = static_cast<const char*>(v.data);
     a.v_nb1 = v.nb[1]; a.v_nb2 = v.nb[2]; a.v_nb3 = v.nb[3];
+    if (paged) {
+        a.pt = p->page_table;
+        a.pt_stride = p->page_table_stride;
+        a.n_pages = (int32_t)k.ne[3];
+    }
     a.out = static_cast<char*>(const_cast<void*>(o.data));
     a.o_nb1 = o.nb[1]; a.o_nb2 = o.nb[2]; a.o_nb3 = o.nb[3];
     a.kv_len = p->kv_len;
@@ -264,6 +284,7 @@ int run(Plan& pl, char* ws, hipStream_t stream) {
         st.q_es = a.q_es; st.q_f16 = a.q_f16;
         st.k = a.k; st.k_nb1 = a.k_nb1; st.k_nb2 = a.k_nb2; st.k_nb3 = a.k_nb3;
         st.v = a.v; st.v_nb1 = a.v_nb1; st.v_nb2 = a.v_nb2; st.v_nb3 = a.v_nb3;
+        st.pt = a.pt; st.pt_stride = a.pt_stride; st.n_pages = a.n_pages;
         st.kv_len = a.kv_len; st.q_len = a.q_len;
         st.S = a.S; st.H = a.H; st.Hkv = a.Hkv; st.n_q = a.n_q; st.n_kv = a.n_kv; st.D = pl.D;
         st.k16 = ws + pl.stage_k; st.v16 = ws + pl.stage_v; st.q16 = ws + pl.stage_q;
@@ -274,6 +295,7 @@ int run(Plan& pl, char* ws, hipStream_t stream) {
         a.q_es = 2; a.q_f16 = 1;
         a.k = st.k16; a.k_nb2 = row; a.k_nb1 = (int64_t)a.Hkv * row; a.k_nb3 = (int64_t)a.n_kv * a.Hkv * row;
         a.v = st.v16; a.v_nb2 = row; a.v_nb1 = a.k_nb1; a.v_nb3 = a.k_nb3;
+        a.pt = nullptr;  // the staged rows are one range per stream
         ws += pl.stage_bytes;
     }
     a.part = reinterpret_cast<float*>(ws);

@@ -28,7 +28,14 @@ int resolve_write(const sixi_kv_write_params* p, sixi::KvWriteArgs* out) {
         if (s.ne[i] < 0 || d.ne[i] < 0 || s.nb[i] < 0 || d.nb[i] < 0) return SIXI_E_INVALID_ARGUMENT;
     const int64_t D = s.ne[0];
     if (D <= 0 || D % 32 != 0 || d.ne[0] != D) return SIXI_E_INVALID_ARGUMENT;
-    if (d.ne[2] != s.ne[2] || d.ne[3] != s.ne[3]) return SIXI_E_INVALID_ARGUMENT;
+    const bool paged = p->page_table != nullptr;
+    if (d.ne[2] != s.ne[2] || (!paged && d.ne[3] != s.ne[3])) return SIXI_E_INVALID_ARGUMENT;
+    if (paged) {
+        if (d.ne[1] != SIXI_KV_PAGE_CELLS || d.ne[3] <= 0 || d.ne[3] > INT32_MAX) return SIXI_E_INVALID_ARGUMENT;
+        if (p->page_table_stride <= 0 || p->page_table_stride > ((int64_t)1 << 26) / SIXI_KV_PAGE_CELLS)
+            return SIXI_E_INVALID_ARGUMENT;
+        if (!aligned(p->page_table, 4)) return SIXI_E_ALIGNMENT;
+    }
     if (s.ne[1] > INT32_MAX || s.ne[2] > INT32_MAX || s.ne[3] > INT32_MAX || D > INT32_MAX)
         return SIXI_E_INTEGER_OVERFLOW;
     // rows must be contiguous: the kernel reads 16-byte vectors of consecutive elements
@@ -60,9 +67,14 @@ int resolve_write(const sixi_kv_write_params* p, sixi::KvWriteArgs* out) {
     a.n_rows = (int)s.ne[1];
     a.Hkv = (int)s.ne[2];
     a.S = (int)s.ne[3];
-    a.n_cells = d.ne[1];
+    a.n_cells = paged ? p->page_table_stride * SIXI_KV_PAGE_CELLS : d.ne[1];
     a.kv_len = p->kv_len;
     a.q_len = p->q_len;
+    if (paged) {
+        a.pt = p->page_table;
+        a.pt_stride = p->page_table_stride;
+        a.n_pages = (int)d.ne[3];
+    }
     *out = a;
     return SIXI_OK;
 }

@@ -46,6 +46,17 @@ EXPORTED_SYMBOLS = (
     "sixi_kv_write",
     "sixi_kv_write_validate",
     "sixi_kv_copy",
+    "sixi_kv_pool_create",
+    "sixi_kv_pool_destroy",
+    "sixi_kv_pool_attach",
+    "sixi_kv_pool_prepare_write",
+    "sixi_kv_pool_seq_rm",
+    "sixi_kv_pool_seq_cp",
+    "sixi_kv_pool_page_table",
+    "sixi_kv_pool_upload",
+    "sixi_kv_pool_free_pages",
+    "sixi_kv_pool_stream_pages",
+    "sixi_kv_pool_page_refs",
     "sixi_verify_plan",
     "sixi_qk_prologue",
     "sixi_attn_gate",
@@ -91,6 +102,8 @@ class SixiAttnParams(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("stream", ctypes.c_void_p),
+        ("page_table", ctypes.c_void_p),
+        ("page_table_stride", ctypes.c_int64),
     ]
 
 
@@ -103,6 +116,8 @@ class SixiKvWriteParams(ctypes.Structure):
         ("flags", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
         ("stream", ctypes.c_void_p),
+        ("page_table", ctypes.c_void_p),
+        ("page_table_stride", ctypes.c_int64),
     ]
 
 
@@ -214,6 +229,22 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     lib.sixi_kv_write_validate.restype = ctypes.c_int
     lib.sixi_kv_copy.argtypes = [ctypes.POINTER(SixiKvCopyParams)]
     lib.sixi_kv_copy.restype = ctypes.c_int
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    for name, args, res in (
+            ("sixi_kv_pool_create", [i32, i32, i32, ctypes.POINTER(vp)], ctypes.c_int),
+            ("sixi_kv_pool_destroy", [vp], None),
+            ("sixi_kv_pool_attach", [vp, ctypes.POINTER(SixiView)], ctypes.c_int),
+            ("sixi_kv_pool_prepare_write", [vp, i32, i64, i64, vp], ctypes.c_int),
+            ("sixi_kv_pool_seq_rm", [vp, i32, i64], ctypes.c_int),
+            ("sixi_kv_pool_seq_cp", [vp, i32, i32, i64], ctypes.c_int),
+            ("sixi_kv_pool_page_table", [vp, vp], ctypes.c_int),
+            ("sixi_kv_pool_upload", [vp, vp, vp], ctypes.c_int),
+            ("sixi_kv_pool_free_pages", [vp], i32),
+            ("sixi_kv_pool_stream_pages", [vp, i32], i32),
+            ("sixi_kv_pool_page_refs", [vp, i32], i32)):
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
     lib.sixi_verify_plan.argtypes = [ctypes.POINTER(SixiVerifyStream), ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                      ctypes.POINTER(SixiVerifySlot), ctypes.POINTER(ctypes.c_int32)]
     lib.sixi_verify_plan.restype = ctypes.c_int
@@ -289,7 +320,10 @@ class FlashAttnExt:
         self._retired = []  # superseded workspaces: graphs captured before a regrowth still use them
 
     def params(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
-               scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None) -> SixiAttnParams:
+               scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None,
+               page_table=None) -> SixiAttnParams:
+        """``page_table`` (an int32 device tensor [S, pages per stream]): k and v are page pools
+        ``[n_pages, 256, Hkv, D]`` (uint8 q8_0 blocks as for a cache) read through it."""
         import torch
 
         D = q.shape[-1]
@@ -310,6 +344,9 @@ class FlashAttnExt:
         p.max_bias = max_bias
         p.logit_softcap = logit_softcap
         p.stream = stream
+        if page_table is not None:
+            p.page_table = page_table.data_ptr()
+            p.page_table_stride = page_table.stride(0)
         return p
 
     def workspace_bytes(self, p: SixiAttnParams) -> int:
@@ -330,13 +367,13 @@ class FlashAttnExt:
 
     def __call__(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
                  scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None, check=True,
-                 workspace=None, noalloc=False) -> int:
+                 workspace=None, noalloc=False, page_table=None) -> int:
         """One call.  ``noalloc=True`` runs sixi_attn_forward_noalloc (the library's fixed
-        device scratch, no workspace)."""
+        device scratch, no workspace); ``page_table`` reads k and v as page pools."""
         import torch
 
         p = self.params(q, k, v, out, kv_len, q_len, mask_mode, mask, scale, max_bias, logit_softcap,
-                        kv_type, stream)
+                        kv_type, stream, page_table)
         if p.stream is None:
             p.stream = torch.cuda.current_stream(self.device).cuda_stream
         if noalloc:
@@ -364,9 +401,11 @@ def _cache_view(cache, head_dim):
     return view_of(cache)
 
 
-def kv_write_params(src, cache, kv_len=None, q_len=None, stream=None) -> SixiKvWriteParams:
+def kv_write_params(src, cache, kv_len=None, q_len=None, stream=None, page_table=None) -> SixiKvWriteParams:
     """Parameters of ``sixi_kv_write`` for torch tensors: ``src[S, n_rows, Hkv, D]`` f32 or
-    f16, ``cache[S, n_cells, Hkv, D]`` f16 (or uint8 q8_0 blocks ``[..., D/32*34]``)."""
+    f16, ``cache[S, n_cells, Hkv, D]`` f16 (or uint8 q8_0 blocks ``[..., D/32*34]``); with
+    ``page_table`` (int32 device [S, pages per stream]) the cache is a page pool
+    ``[n_pages, 256, Hkv, D]``."""
     p = SixiKvWriteParams()
     p.src = view_of(src)
     p.dst = _cache_view(cache, src.shape[-1])
@@ -374,10 +413,13 @@ def kv_write_params(src, cache, kv_len=None, q_len=None, stream=None) -> SixiKvW
     p.q_len = q_len.data_ptr() if q_len is not None else None
     p.flags = 0
     p.stream = stream
+    if page_table is not None:
+        p.page_table = page_table.data_ptr()
+        p.page_table_stride = page_table.stride(0)
     return p
 
 
-def kv_write(src, cache, kv_len=None, q_len=None, stream=None, check=True) -> int:
+def kv_write(src, cache, kv_len=None, q_len=None, stream=None, check=True, page_table=None) -> int:
     """Stores the new K (or V) rows of each stream in its cache cells.
 
     Row j < q_len[s] of stream s goes to cell kv_len[s] + j, converted to the cache type with
@@ -389,7 +431,7 @@ def kv_write(src, cache, kv_len=None, q_len=None, stream=None, check=True) -> in
     import torch
 
     lib = load_library()
-    p = kv_write_params(src, cache, kv_len, q_len, stream)
+    p = kv_write_params(src, cache, kv_len, q_len, stream, page_table)
     if p.stream is None:
         p.stream = torch.cuda.current_stream(src.device).cuda_stream
     rc = lib.sixi_kv_write(ctypes.byref(p))
@@ -421,6 +463,99 @@ def kv_copy(cache, src_stream: int, dst_stream: int, n_cells: int, src_cell: int
     if check and rc != OK:
         raise SixiAttnError(rc, strerror(rc))
     return rc
+
+
+PAGE_CELLS = 256  # SIXI_KV_PAGE_CELLS
+
+
+class KvPool:
+    """A page pool over 256-cell pages (include/sixi_kv.h ``sixi_kv_pool_*``): which pages of
+    the K/V page pools (tensors ``[n_pages, 256, Hkv, D]``) hold each stream's cells.
+
+    ``seq_cp`` shares pages (llama_memory_seq_cp, src/core/core_execution.cpp:3215-3216,
+    :3245-3246) and ``seq_rm`` releases them (llama_memory_seq_rm, :4021-4062); no cell data
+    moves.  ``prepare_write`` gives a stream the pages a write needs, copying a page it shares
+    with another stream first (every attached pool tensor, on the current stream)."""
+
+    def __init__(self, n_pages: int, n_streams: int, max_pages: int):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        self._check(self.lib.sixi_kv_pool_create(int(n_pages), int(n_streams), int(max_pages), ctypes.byref(h)))
+        self.h = h
+        self.n_pages, self.n_streams, self.max_pages = int(n_pages), int(n_streams), int(max_pages)
+        self._views = []  # attached tensors stay alive with the pool
+
+    @staticmethod
+    def _check(rc: int) -> int:
+        if rc != OK:
+            raise SixiAttnError(rc, strerror(rc))
+        return rc
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.sixi_kv_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def attach(self, pages, head_dim: Optional[int] = None) -> None:
+        """Registers a page pool tensor ``[n_pages, 256, Hkv, D]`` f16 (or uint8 q8_0 blocks with
+        ``head_dim``) whose pages copy-on-write duplicates."""
+        v = _cache_view(pages, head_dim if head_dim is not None else pages.shape[-1])
+        self._check(self.lib.sixi_kv_pool_attach(self.h, ctypes.byref(v)))
+        self._views.append(pages)
+
+    def prepare_write(self, s: int, first: int, n: int, stream=None) -> None:
+        """Pages for stream s's cells [first, first + n), shared pages in that range copied."""
+        st = stream
+        if st is None and self._views:
+            import torch
+
+            st = torch.cuda.current_stream().cuda_stream
+        self._check(self.lib.sixi_kv_pool_prepare_write(self.h, int(s), int(first), int(n), st))
+
+    def seq_rm(self, s: int, p0: int) -> None:
+        self._check(self.lib.sixi_kv_pool_seq_rm(self.h, int(s), int(p0)))
+
+    def seq_cp(self, src: int, dst: int, n: int = -1) -> None:
+        self._check(self.lib.sixi_kv_pool_seq_cp(self.h, int(src), int(dst), int(n)))
+
+    def page_table(self):
+        """The page table as a numpy int32 array [n_streams, max_pages] (-1: no page)."""
+        import numpy as np
+
+        t = np.empty((self.n_streams, self.max_pages), dtype=np.int32)
+        self._check(self.lib.sixi_kv_pool_page_table(self.h, t.ctypes.data))
+        return t
+
+    def upload(self, dst=None, stream=None):
+        """The page table in an int32 device tensor [n_streams, max_pages] (``dst`` or new)."""
+        import torch
+
+        if dst is None:
+            dst = torch.empty((self.n_streams, self.max_pages), dtype=torch.int32, device="cuda")
+        st = stream if stream is not None else torch.cuda.current_stream(dst.device).cuda_stream
+        self._check(self.lib.sixi_kv_pool_upload(self.h, dst.data_ptr(), st))
+        return dst
+
+    def free_pages(self) -> int:
+        return self._count(self.lib.sixi_kv_pool_free_pages(self.h))
+
+    def stream_pages(self, s: int) -> int:
+        return self._count(self.lib.sixi_kv_pool_stream_pages(self.h, int(s)))
+
+    def page_refs(self, page: int) -> int:
+        return self._count(self.lib.sixi_kv_pool_page_refs(self.h, int(page)))
+
+    @staticmethod
+    def _count(n: int) -> int:
+        if n < 0:
+            raise SixiAttnError(n, strerror(n))
+        return n
 
 
 def plan_verify(streams, n_ctx_seq: int = 0, pad_mode: int = PAD_REFERENCE):

@@ -15,7 +15,7 @@ HEADERS = sorted((ROOT / "include").glob("*.h"))
 def _declared():
     names = set()
     for h in HEADERS:
-        names |= set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(sixi_\w+)\(", h.read_text(), re.M))
+        names |= set(re.findall(r"^\s*(?:int|int32_t|void|const char\*|size_t)\s+(sixi_\w+)\(", h.read_text(), re.M))
     return sorted(names)
 
 
@@ -25,7 +25,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert declared == sorted(sa.EXPORTED_SYMBOLS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.sixi_attn_abi_version() == 1
+    assert lib.sixi_attn_abi_version() == 2
 
 
 def test_status_strings():
