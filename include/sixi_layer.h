@@ -39,9 +39,14 @@ typedef struct sixi_qk_prologue_params {
     const int32_t* kv_len;  /* device [S]: cells cached before the block = position of row 0       */
     const int32_t* q_len;   /* device [S]: rows of stream s (<= n_rows), or NULL (= n_rows)        */
     sixi_view q_out;        /* [D, n_rows, H, S] f32: the attention's Q (sixi_attn_params.q)       */
-    sixi_view k_cache;      /* [D, n_cells, Hkv, S] f16 or q8_0                                    */
+    sixi_view k_cache;      /* [D, n_cells, Hkv, S] f16 or q8_0; paged: the page pool
+                               [D, SIXI_KV_PAGE_CELLS, Hkv, n_pages], nb[3] = page stride           */
     sixi_view v_cache;      /* same shape and type as k_cache                                     */
     void* stream;
+    /* Paged caches (optional, as sixi_attn_params): cell c of stream s is cell c % 256 of page
+     * page_table[s * page_table_stride + c / 256]; n_cells = page_table_stride * 256. */
+    const int32_t* page_table;
+    int64_t page_table_stride;
 } sixi_qk_prologue_params;
 
 /* For row j < q_len[s] of stream s (position kv_len[s] + j): writes the normed, rotated query of

@@ -32,6 +32,10 @@ struct QkPrologueArgs {
     int cache_q8;
     int D, H, Hkv, n_rows, S;
     int64_t n_cells;
+    const int32_t* pt;               // paged caches: cell c of stream s -> cell c % 256 of page
+                                     // pt[s*pt_stride + c/256] (kc_nb3/vc_nb3 the page strides)
+    int64_t pt_stride;
+    int n_pages;
 };
 
 struct AttnGateArgs {

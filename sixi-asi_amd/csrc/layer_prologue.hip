@@ -203,8 +203,14 @@ __global__ __launch_bounds__(256) void qk_prologue(QkPrologueArgs a) {
     if (j >= (a.q_len ? a.q_len[s] : a.n_rows)) return;
     const bool in_cache = pos >= 0 && pos < a.n_cells;  // outside the stream's cells: not stored
     char* qo_row = a.q_out + (int64_t)j * a.qo_nb1 + (int64_t)s * a.qo_nb3;
-    char* kc_row = a.kc + pos * a.kc_nb1 + (int64_t)s * a.kc_nb3;
-    char* vc_row = a.vc + pos * a.vc_nb1 + (int64_t)s * a.vc_nb3;
+    // the cell's rows: in the stream's range, or (paged) in its page
+    int64_t page = s, cell = pos;
+    if (a.pt && in_cache) {
+        page = min(max(a.pt[(int64_t)s * a.pt_stride + (pos >> 8)], 0), a.n_pages - 1);
+        cell = pos & 255;
+    }
+    char* kc_row = a.kc + cell * a.kc_nb1 + page * a.kc_nb3;
+    char* vc_row = a.vc + cell * a.vc_nb1 + page * a.vc_nb3;
     // per batch: every row is computed before the first store, since a store in flight makes
     // the next load's wait a full drain (one counter covers loads and stores)
     for (int first = wave; first < slots; first += 4 * kBatch) {

@@ -41,12 +41,20 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     if (!f32_rows_ok(qg) || !f32_rows_ok(k) || !f32_rows_ok(v) || !f32_rows_ok(qo)) return SIXI_E_INVALID_ARGUMENT;
     const int64_t D = qo.ne[0];
     if (D != 128 && D != 256) return SIXI_E_UNSUPPORTED;
-    const int64_t H = qg.ne[1], n_rows = qg.ne[2], S = qg.ne[3], Hkv = k.ne[1], n_cells = kc.ne[1];
+    const int64_t H = qg.ne[1], n_rows = qg.ne[2], S = qg.ne[3], Hkv = k.ne[1];
+    const bool paged = p->page_table != nullptr;
+    if (paged && (p->page_table_stride <= 0 || p->page_table_stride > ((int64_t)1 << 26) / SIXI_KV_PAGE_CELLS))
+        return SIXI_E_INVALID_ARGUMENT;
+    if (paged && !aligned(p->page_table, 4)) return SIXI_E_ALIGNMENT;
+    const int64_t n_cells = paged ? p->page_table_stride * SIXI_KV_PAGE_CELLS : kc.ne[1];
+    // the cache views: [D, n_cells, Hkv, S], or (paged) pools [D, 256, Hkv, n_pages]
+    const int64_t c_ne1 = paged ? SIXI_KV_PAGE_CELLS : n_cells, c_ne3 = paged ? kc.ne[3] : S;
+    if (paged && (c_ne3 <= 0 || c_ne3 > INT32_MAX)) return SIXI_E_INVALID_ARGUMENT;
     if (qg.ne[0] != 2 * D || !dims_are(qo, D, n_rows, H, S)) return SIXI_E_INVALID_ARGUMENT;
     if (!dims_are(k, D, Hkv, n_rows, S) || !dims_are(v, D, Hkv, n_rows, S)) return SIXI_E_INVALID_ARGUMENT;
     if (kc.type != vc.type || (kc.type != SIXI_TYPE_F16 && kc.type != SIXI_TYPE_Q8_0)) return SIXI_E_INVALID_ARGUMENT;
     if (!kc.data || !vc.data) return SIXI_E_INVALID_ARGUMENT;
-    if (!dims_are(kc, D, n_cells, Hkv, S) || !dims_are(vc, D, n_cells, Hkv, S)) return SIXI_E_INVALID_ARGUMENT;
+    if (!dims_are(kc, D, c_ne1, Hkv, c_ne3) || !dims_are(vc, D, c_ne1, Hkv, c_ne3)) return SIXI_E_INVALID_ARGUMENT;
     const int64_t cnb0 = kc.type == SIXI_TYPE_F16 ? 2 : 34;
     if (kc.nb[0] != cnb0 || vc.nb[0] != cnb0) return SIXI_E_INVALID_ARGUMENT;
     if (p->n_rot < 0 || p->n_rot > D || p->n_rot % (D / 32) != 0) return SIXI_E_INVALID_ARGUMENT;
@@ -108,6 +116,11 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     a.n_rows = (int)n_rows;
     a.S = (int)S;
     a.n_cells = n_cells;
+    if (paged) {
+        a.pt = p->page_table;
+        a.pt_stride = p->page_table_stride;
+        a.n_pages = (int)c_ne3;
+    }
     *out = a;
     return SIXI_OK;
 }

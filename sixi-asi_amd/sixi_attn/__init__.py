@@ -150,6 +150,8 @@ class SixiQkPrologueParams(ctypes.Structure):
         ("k_cache", SixiView),
         ("v_cache", SixiView),
         ("stream", ctypes.c_void_p),
+        ("page_table", ctypes.c_void_p),
+        ("page_table_stride", ctypes.c_int64),
     ]
 
 
@@ -589,11 +591,12 @@ def part_lengths(streams, slots, part: int, pad_mode: int = PAD_REFERENCE):
 
 def qk_prologue_params(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len=None, q_len=None,
                        eps: float = 1e-6, rope_base: float = 1e7, n_rot: int = 64,
-                       stream=None) -> SixiQkPrologueParams:
+                       stream=None, page_table=None) -> SixiQkPrologueParams:
     """Parameters of ``sixi_qk_prologue`` for torch tensors: ``qg[S, n_rows, H, 2D]`` (per head
     the query, then its gate), ``k/v[S, n_rows, Hkv, D]`` f32, ``q_norm/k_norm[D]`` f32,
     ``q_out[S, n_rows, H, D]`` f32 (the attention's Q), caches ``[S, n_cells, Hkv, D]`` f16 or
-    uint8 q8_0 blocks."""
+    uint8 q8_0 blocks (with ``page_table``, int32 device [S, pages per stream]: page pools
+    ``[n_pages, 256, Hkv, D]``)."""
     D = q_out.shape[-1]
     p = SixiQkPrologueParams()
     p.qg = view_of(qg, tokens_heads=False)
@@ -611,11 +614,15 @@ def qk_prologue_params(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len
     p.k_cache = _cache_view(k_cache, D)
     p.v_cache = _cache_view(v_cache, D)
     p.stream = stream
+    if page_table is not None:
+        p.page_table = page_table.data_ptr()
+        p.page_table_stride = page_table.stride(0)
     return p
 
 
 def qk_prologue(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len=None, q_len=None,
-                eps: float = 1e-6, rope_base: float = 1e7, n_rot: int = 64, stream=None, check=True) -> int:
+                eps: float = 1e-6, rope_base: float = 1e7, n_rot: int = 64, stream=None, check=True,
+                page_table=None) -> int:
     """The Q/K prologue of a Qwen3.8 full-attention layer (include/sixi_layer.h) fused with the
     KV store: RMS norm times the attn_q_norm / attn_k_norm weight, NEOX RoPE on the first
     ``n_rot`` dims at position kv_len[s] + j, Q to ``q_out``, K and V into cell kv_len[s] + j of
@@ -624,7 +631,7 @@ def qk_prologue(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len=None, 
     import torch
 
     p = qk_prologue_params(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len, q_len, eps, rope_base,
-                           n_rot, stream)
+                           n_rot, stream, page_table)
     if p.stream is None:
         p.stream = torch.cuda.current_stream(q_out.device).cuda_stream
     rc = load_library().sixi_qk_prologue(ctypes.byref(p))

@@ -208,3 +208,46 @@ def test_pool_seq_cp_shares_and_writes_copy_on_write(fa, kv_type):
     gathered = kp[torch.tensor(t[1, :2], dtype=torch.long, device="cuda")].reshape(2 * P, Hkv, row)
     assert torch.equal(gathered, kc[0, :2 * P])
     pool.close()
+
+
+@pytest.mark.parametrize("q8", [False, True])
+def test_prologue_store_through_the_page_table(q8):
+    """The layer prologue's fused KV store (include/sixi_layer.h) into a paged cache writes the
+    same bytes, cell for cell, as into the contiguous cache; the pages the block does not touch
+    (and the cells of touched pages outside the block) keep their bytes."""
+    S, R, H, Hkv, D = 3, 16, 24, 4, 256
+    kv_len, q_len = [250, 1000, 0], [16, 9, 16]  # stream 0's block crosses a page boundary
+    per = 5
+    n_pages = S * per + 3
+    torch.manual_seed(11)
+    qg = torch.randn((S, R, H, 2 * D), device="cuda")
+    k = torch.randn((S, R, Hkv, D), device="cuda")
+    v = torch.randn((S, R, Hkv, D), device="cuda")
+    wq = torch.rand(D, device="cuda") + 0.5
+    wk = torch.rand(D, device="cuda") + 0.5
+    row = D // 32 * 34 if q8 else D
+    dt = torch.uint8 if q8 else torch.float16
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    kc = torch.randint(0, 255, (S, per * P, Hkv, row), dtype=torch.uint8, device="cuda", generator=gen)
+    if not q8:  # finite f16 values
+        kc = (kc.to(torch.float16) - 127.0) / 64.0
+    vc = kc.clone()
+    perm = np.random.default_rng(3).permutation(n_pages)
+    kp, table = _paginate(kc, perm, n_pages)
+    vp, _ = _paginate(vc, perm, n_pages)
+    kp0, vp0 = kp.clone(), vp.clone()
+    kl = torch.tensor(kv_len, dtype=torch.int32, device="cuda")
+    ql = torch.tensor(q_len, dtype=torch.int32, device="cuda")
+    qo_c = torch.full((S, R, H, D), float("nan"), device="cuda")
+    qo_p = torch.full_like(qo_c, float("nan"))
+    sa.qk_prologue(qg, k, v, wq, wk, qo_c, kc, vc, kl, ql)
+    sa.qk_prologue(qg, k, v, wq, wk, qo_p, kp, vp, kl, ql, page_table=table)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.nan_to_num(qo_c, 7.0), torch.nan_to_num(qo_p, 7.0))
+    idx = table.reshape(-1).long()
+    for name, pool, cont, before in (("K", kp, kc, kp0), ("V", vp, vc, vp0)):
+        gathered = pool[idx].reshape(S, per * P, Hkv, row)
+        assert torch.equal(gathered.view(torch.uint8), cont.view(torch.uint8)), name
+        unused = torch.ones(n_pages, dtype=torch.bool, device="cuda")
+        unused[idx] = False
+        assert torch.equal(pool[unused].view(torch.uint8), before[unused].view(torch.uint8)), name
