@@ -75,6 +75,49 @@ def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None):
     return total / steps, per
 
 
+def time_paged(fa, w, dev, steps: int, warmup: int) -> dict:
+    """The workload's call with K and V in a page pool (include/sixi_attn.h page_table): each
+    stream's 256-cell pages placed at shuffled pool pages (seeded), read through the table."""
+    import numpy as np
+    import torch
+
+    import sixi_attn as sa
+
+    S, cap = dev["k"].shape[0], dev["k"].shape[1]
+    per = cap // sa.PAGE_CELLS
+    n_pages = S * per
+    perm = np.random.default_rng(0x51A7).permutation(n_pages).astype(np.int32)
+    table = torch.from_numpy(perm.reshape(S, per)).cuda()
+    idx = table.reshape(-1).long()
+    pools = []
+    for name in ("k", "v"):
+        c = dev[name]
+        pool = torch.empty((n_pages, sa.PAGE_CELLS) + tuple(c.shape[2:]), dtype=c.dtype, device="cuda")
+        pool[idx] = c.reshape(n_pages, sa.PAGE_CELLS, *c.shape[2:])
+        pools.append(pool)
+    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def call():
+        fa(dev["q"], pools[0], pools[1], out, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=w.mask_mode,
+           stream=stream.cuda_stream, page_table=table)
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        call()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_call = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    res = summarize(w, ev[0].elapsed_time(ev[steps]) / steps, per_call)
+    res["pages"] = n_pages
+    del pools
+    return res
+
+
 def ws_bytes(fa, w, dev, mask=None) -> int:
     """sixi_attn_workspace_bytes of a call of workload w (q8_0 prefill-sized blocks and
     256-dim q8_0 calls include the f16 staging of the cache)."""
@@ -511,6 +554,10 @@ def main() -> int:
                               "rocprofv3 --pmc run of this command, scaled by the copy calibration)",
         },
     }
+
+    # the same verify over a paged cache: every stream's 256-cell pages shuffled over one pool
+    result["verify_paged"] = time_paged(fa, w, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
+    _log(f"verify, paged KV: {result['verify_paged']}")
 
     # the same verify with the block-causal mask handed over as an explicit ggml KQ mask (the
     # ggml FLASH_ATTN_EXT drop-in path)

@@ -570,11 +570,14 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
     }
 
     // Stage tile i of this lane into slot i % NSLOT.
+    PageIds pages = page_ids_load(a, s, (t0 * kTile) >> 8);
     auto issue = [&](int i) {
-        const int c0 = (t0 + i * TL) * kTile;
+        // uniform over the wave (the compiler cannot tell): scalar page and span arithmetic
+        const int c0 = __builtin_amdgcn_readfirstlane((t0 + i * TL) * kTile);
         const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * KvTile<KV>::slot_bytes;
-        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, c0, sd.nc, rowb);
-        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, c0, sd.nc, rowb);
+        const int page = c0 < sd.nc ? page_id(pages, a, s, c0 >> 8) : 0;
+        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, c0, sd.nc, rowb, page);
+        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, c0, sd.nc, rowb, page);
         const buf_rsrc krs = make_rsrc_uniform(ksp.p, ksp.bytes);
         const buf_rsrc vrs = make_rsrc_uniform(vsp.p, vsp.bytes);
         if constexpr (KV == SIXI_TYPE_F16) {
@@ -1088,11 +1091,14 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     constexpr bool GEN = MODE != MODE_FAST;
     const buf_rsrc mrs = make_rsrc_uniform(mrow, GEN && a.mask_stage ? a.m_bytes : 0u);
     const uint32_t mring_base = lds_addr(sh.mring) + (uint32_t)tl * wide_slots<D, TL>() * kMaskTile;
+    PageIds pages = page_ids_load(a, s, (t0 * kWide) >> 8);
     auto issue = [&](int i, int slot) {
+        // uniform over the wave (the compiler cannot tell): scalar page and span arithmetic
         const uint32_t c0 = (uint32_t)(t0 + i * TL) * kWide;
         const uint32_t base = ring_base + (uint32_t)slot * W::SLOT;
-        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, (int)c0, sd.nc, W::ROW);
-        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, (int)c0, sd.nc, W::ROW);
+        const int page = (int)c0 < sd.nc ? page_id(pages, a, s, (int)(c0 >> 8)) : 0;
+        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, (int)c0, sd.nc, W::ROW, page);
+        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, (int)c0, sd.nc, W::ROW, page);
         const buf_rsrc krs = make_rsrc_uniform(ksp.p, ksp.bytes);
         const buf_rsrc vrs = make_rsrc_uniform(vsp.p, vsp.bytes);
         const uint32_t pos = (uint32_t)lane % W::CPR;  // 16-byte position in the row
@@ -1149,6 +1155,13 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
 #pragma unroll
         for (int q = 0; q < NS - 1; ++q)
             if (q < n_my) issue(q, q);
+        // The Q^T operands' loads end here, once per piece: left for the loop, the compiler's
+        // wait for them lands in the step body (before an LDS read that reuses a register),
+        // where it would drain the ring's DMA loads every step.
+#pragma unroll
+        for (int n = 0; n < NTW; ++n)
+#pragma unroll
+            for (int ks = 0; ks < W::KS; ++ks) asm volatile("" ::"v"(qv[n][ks]));
         // Score phase of step i after its data has landed; returns whether a row's exponent
         // reference moves (uniform over the wave).  Every wave passes the barrier of every step.
         auto scores = [&](int i, auto masked, WideStep<NTW, D>& ws) -> bool {

@@ -317,24 +317,50 @@ __device__ __forceinline__ StreamDims stream_dims(const FaArgs& a, int s) {
     return stream_dims_from(a, q_raw, kv_raw);
 }
 
+// Page ids of a paged cache for one stream, 64 consecutive page indices at a time, one per
+// lane: a tile's page comes from a register (v_readlane) rather than a load per tile.  Ids
+// are clamped to [0, n_pages).  Unused for contiguous caches (pt null).
+struct PageIds {
+    int first;  // page index that lane 0 holds
+    int id;     // lane l: id of page index first + l
+};
+__device__ __forceinline__ PageIds page_ids_load(const FaArgs& a, int s, int first) {
+    PageIds p{__builtin_amdgcn_readfirstlane(first), 0};
+    first = p.first;
+    if (a.pt) {
+        const int64_t idx = (int64_t)first + (threadIdx.x & 63);
+        if (idx < a.pt_stride) p.id = min(max(a.pt[(int64_t)s * a.pt_stride + idx], 0), a.n_pages - 1);
+    }
+    return p;
+}
+// Id of page index `page` (uniform) of stream s; reloads the window when it moves past it.
+__device__ __forceinline__ int page_id(PageIds& p, const FaArgs& a, int s, int page) {
+    if (!a.pt) return 0;
+    if (page < p.first || page >= p.first + 64) {
+        p = page_ids_load(a, s, page);
+        // use the load on this (rare) path: a first use after the paths join would put the
+        // compiler's wait for it -- which also drains the ring's DMA loads -- on every step
+        asm volatile("" ::"v"(p.id));
+    }
+    return __builtin_amdgcn_readlane(p.id, page - p.first);
+}
+
 // K or V rows of (stream s, kv-head g) from cell c0 on, for a range-checked buffer resource:
 // the address of cell c0's row, and the bytes from there to the end of the last row a load may
-// use -- rows up to cell nc - 1 that lie in c0's page (paged caches) or in the stream
-// (contiguous).  Offsets from the address are (c - c0) * nb1.  0 bytes when c0 >= nc (the page
-// table is then not read).  Every tile of the kernels lies in one page: tiles of 16, 32 and 64
-// cells start at multiples of their size, and pages hold 256 cells.
+// use -- rows up to cell nc - 1 that lie in c0's page (paged caches, page id `page` of c0's
+// page) or in the stream (contiguous).  Offsets from the address are (c - c0) * nb1.  0 bytes
+// when c0 >= nc.  Every tile of the kernels lies in one page: tiles of 16, 32 and 64 cells
+// start at multiples of their size, and pages hold 256 cells.
 struct KvSpan {
     const char* p;
     uint32_t bytes;
 };
 __device__ __forceinline__ KvSpan kv_span(const FaArgs& a, const char* kv, int64_t nb1, int64_t nb2, int64_t nb3, int s,
-                                          int g, int c0, int nc, int64_t rowb) {
+                                          int g, int c0, int nc, int64_t rowb, int page) {
     if (c0 >= nc) return {kv, 0u};
     int64_t off;
     int last = nc;
     if (a.pt) {
-        const int idx = __builtin_amdgcn_readfirstlane((int)((int64_t)s * a.pt_stride + (c0 >> 8)));
-        const int page = min(max(a.pt[idx], 0), a.n_pages - 1);
         off = (int64_t)page * nb3 + (int64_t)(c0 & (kPageCells - 1)) * nb1;
         last = min(nc, (c0 | (kPageCells - 1)) + 1);
     } else {

@@ -183,9 +183,11 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
         for (int db = 0; db < P::DB; ++db) vtr[db] = lds0 + kVBase + (base ^ (64u * db));
     }
 
+    PageIds pages = page_ids_load(a, s, 0);
     auto issue_kv = [&](int t, int buf) {
-        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, t * kBN, sd.nc, rowb);
-        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, t * kBN, sd.nc, rowb);
+        const int page = t * kBN < sd.nc ? page_id(pages, a, s, (t * kBN) >> 8) : 0;
+        const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, t * kBN, sd.nc, rowb, page);
+        const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, t * kBN, sd.nc, rowb, page);
         const buf_rsrc krs = make_rsrc_uniform(ksp.p, ksp.bytes);
         const buf_rsrc vrs = make_rsrc_uniform(vsp.p, vsp.bytes);
         if constexpr (P::LW == 4) {
