@@ -7,6 +7,10 @@ gets no wait states and can read stale accumulator values.  The asm blocks of th
 end their own windows (acc_settle8) where they hand the accumulators to compiled code; this
 test compiles the kernel source to device assembly with the build's flags and walks every
 path (branches followed) from each asm MFMA for WAIT wait states.
+
+The same assembly is checked for the other blind spot of inline asm: the LDS-DMA loads of
+the 32-cell kernel's ring are invisible to the compiler's wait insertion, so a wait it places
+in the step loop for a load of its own drains the whole ring every step.
 """
 import importlib.util
 import pathlib
@@ -129,7 +133,9 @@ def test_checker_finds_a_planted_hazard():
     assert hazards(_TOY.format(between="\ts_nop 7\n\ts_nop 7\n\ts_nop 7")) == []
 
 
-def test_decode_kernels_have_no_asm_mfma_hazards(tmp_path):
+@pytest.fixture(scope="module")
+def decode_asm(tmp_path_factory):
+    """gfx950 assembly of fa_decode.hip, built with the library's flags."""
     spec = importlib.util.spec_from_file_location("sixi_build", BUILD)
     build = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(build)
@@ -138,11 +144,40 @@ def test_decode_kernels_have_no_asm_mfma_hazards(tmp_path):
     except RuntimeError:
         pytest.skip("hipcc not available")
     flags = [f for f in build.HIP_FLAGS if f != "-fPIC"]
-    out = tmp_path / "fa_decode.s"
+    out = tmp_path_factory.mktemp("asm") / "fa_decode.s"
     proc = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", str(out), str(build.CSRC / "fa_decode.hip")],
                           stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert proc.returncode == 0, proc.stdout[-2000:]
-    asm = out.read_text()
-    assert asm.count("v_mfma_f32_16x16x32_f16 a[") > 0, "no asm MFMAs found: the check would be vacuous"
-    bad = hazards(asm)
+    return out.read_text()
+
+
+def test_decode_kernels_have_no_asm_mfma_hazards(decode_asm):
+    assert decode_asm.count("v_mfma_f32_16x16x32_f16 a[") > 0, "no asm MFMAs found: the check would be vacuous"
+    bad = hazards(decode_asm)
     assert not bad, f"{len(bad)} hazards, first: {bad[:3]}"
+
+
+def drains_before_lds_reads(asm, kernel_pattern):
+    """Compiler-placed vmcnt waits right before an LDS read, per kernel matching the pattern.
+    In the 32-cell kernel every vector-memory load of the step loop is an LDS-DMA load issued by
+    inline asm, which the compiler does not see; a wait it places before an LDS read stands for
+    a load it believes pending (from before the loop) and, executed in the loop, drains the DMA
+    ring every step."""
+    out = {}
+    for name, lines in _functions(asm):
+        if not re.search(kernel_pattern, name):
+            continue
+        body = [l.strip() for l in lines]
+        n = sum(1 for k in range(1, len(body) - 1)
+                if re.match(r"s_waitcnt\b.*vmcnt", body[k]) and "ASMSTART" not in body[k - 1]
+                and body[k + 1].startswith("ds_read"))
+        out[name] = n
+    return out
+
+
+def test_wide_decode_step_loops_do_not_drain_the_dma_ring(decode_asm):
+    # fast (mode 0) and staged-mask (mode 2) variants of decode_wide<NTW, RS, MODE, D>
+    found = drains_before_lds_reads(decode_asm, r"decode_wideILi\d+ELi\d+ELi[02]ELi\d+E")
+    assert len(found) >= 8, found
+    bad = {k: v for k, v in found.items() if v}
+    assert not bad, bad
