@@ -85,8 +85,8 @@ template <> struct KvTile<SIXI_TYPE_Q8_0> { static constexpr int slot_bytes = 2 
 
 // Four independent tile lanes (one wave each) per work-group, two work-groups per CU.
 template <int KV> struct Shape;
-template <> struct Shape<SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 4, slots = 2, groups_per_cu = 2; };
-template <> struct Shape<SIXI_TYPE_Q8_0> { static constexpr int waves = 4, lanes = 4, slots = 3, groups_per_cu = 2; };
+template <> struct Shape<SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 4, slots = 2; };
+template <> struct Shape<SIXI_TYPE_Q8_0> { static constexpr int waves = 4, lanes = 4, slots = 3; };
 
 template <int NT, int NS, int DT = 8>
 struct MergeBuf {
@@ -1279,7 +1279,7 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
 }
 
 template <int NTW, int KV, int MODE>
-__global__ __launch_bounds__((Shape<KV>::waves * 64), (Shape<KV>::waves * Shape<KV>::groups_per_cu / 4)) void
+__global__ __launch_bounds__((Shape<KV>::waves * 64), (Shape<KV>::waves * d128_groups_per_cu(KV, NTW, MODE != MODE_FAST) / 4)) void
 decode_d128(FaArgs a, int causal) {
     __shared__ DecodeLds<NTW, KV> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
@@ -1428,7 +1428,9 @@ inline bool slot_fits(const FaArgs& a, int rows, int D) {
     return (int64_t)rows * (D / 2 + 2) <= a.slot_floats;
 }
 
-template <int NTW, int RS, int D>
+// FAST_BUILT: whether the launch shape has a fast-mode kernel (the 32-cell kernel takes f16
+// explicit-mask and softcap calls of up to 48 rows as well, whose fast calls run decode_d128).
+template <int NTW, int RS, int D, bool FAST_BUILT = true>
 hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream) {
     if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(RS * wide_lanes<RS, D>() * 64);
@@ -1436,8 +1438,10 @@ hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_GENERIC, D>), grid, block, 0, stream, a, causal);
     else if (mode == MODE_MASK)
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_MASK, D>), grid, block, 0, stream, a, causal);
-    else
+    else if constexpr (FAST_BUILT)
         hipLaunchKernelGGL((decode_wide<NTW, RS, MODE_FAST, D>), grid, block, 0, stream, a, causal);
+    else
+        return hipErrorNotSupported;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     launch_merge<D>(a, NTW * RS * 16, stream);
@@ -1446,13 +1450,16 @@ hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream
 
 template <int NTW, int KV>
 hipError_t launch_nt(const FaArgs& a, int mode, int causal, hipStream_t stream) {
-    const bool generic = mode != MODE_FAST;
     if (!slot_fits(a, NTW * 16, 128)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(Shape<KV>::waves * 64);
-    if (generic)
-        hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
-    else
+    if (mode == MODE_FAST) {
         hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_FAST>), grid, block, 0, stream, a, causal);
+    } else if constexpr (KV == SIXI_TYPE_Q8_0) {
+        // (f16 explicit-mask and softcap calls run the 32-cell kernel)
+        hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+    } else {
+        return hipErrorNotSupported;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     launch_merge<128>(a, NTW * 16, stream);
@@ -1461,9 +1468,8 @@ hipError_t launch_nt(const FaArgs& a, int mode, int causal, hipStream_t stream) 
 
 }  // namespace
 
-int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles) {
+int decode_num_groups(const FaArgs& a, int cu_count, int per_cu) {
     const int64_t tiles_max = (int64_t)a.S * a.Hkv * ((a.n_kv + a.tile_cells - 1) / a.tile_cells + a.seg_cost);
-    const int per_cu = a.tile_cells == kDecodeTile ? Shape<SIXI_TYPE_F16>::groups_per_cu : WideShape::groups_per_cu;
     int64_t P = (int64_t)(cu_count > 0 ? cu_count : 256) * per_cu;
     if (P > kMaxSplitGroups) P = kMaxSplitGroups;
     if (P > tiles_max) P = tiles_max;
@@ -1496,6 +1502,16 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
         }
     }
     if (head_dim != 128) return hipErrorNotSupported;
+    if (kv_type == SIXI_TYPE_F16 && mode != MODE_FAST && row_tiles <= 3) {
+        // explicit mask or softcap, up to 48 rows: the 32-cell kernel with one row group per lane
+        // (its per-cell mask work fits the 512 registers of one wave per SIMD)
+        switch (row_tiles) {
+            case 1: return launch_wide<1, 1, 128, false>(a, mode, causal, stream);
+            case 2: return launch_wide<2, 1, 128, false>(a, mode, causal, stream);
+            case 3: return launch_wide<3, 1, 128, false>(a, mode, causal, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
     if (kv_type == SIXI_TYPE_F16) {
         switch (row_tiles) {
             case 1: return launch_nt<1, SIXI_TYPE_F16>(a, mode, causal, stream);

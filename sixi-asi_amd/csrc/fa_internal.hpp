@@ -94,21 +94,31 @@ constexpr int kPageCells = SIXI_KV_PAGE_CELLS;  // paged KV: cells per page (a m
 static_assert(kPageCells == 256, "page arithmetic below uses c >> 8 and c & 255");
 constexpr int kMaxSplitGroups = 2048;  // work-groups of a split-K launch (workspace bound)
 constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-robin over 8 XCDs
-int decode_num_groups(const FaArgs& a, int cu_count, int row_tiles);
-// Whether the 32-cell kernel runs this launch: f16 KV with more than 48 rows, or 256-dim heads.
-inline bool decode_wide_kernel(int kv_type, int row_tiles, int head_dim) {
-    return kv_type == SIXI_TYPE_F16 && (row_tiles > 3 || head_dim == 256);
+int decode_num_groups(const FaArgs& a, int cu_count, int groups_per_cu);
+// Whether the 32-cell kernel runs this launch: f16 KV with more than 48 rows or 256-dim heads,
+// and f16 KV under an explicit mask or a softcap (`generic`: the per-cell work needs the
+// 512 registers per wave of that kernel).
+inline bool decode_wide_kernel(int kv_type, int row_tiles, int head_dim, bool generic) {
+    return kv_type == SIXI_TYPE_F16 && (row_tiles > 3 || head_dim == 256 || generic);
+}
+// Work-groups per CU of the 16-cell kernel: two (256 registers per wave).  One group per CU
+// removes the few spills of q8_0 at 48 rows and of q8_0 under a mask, but halves the waves that
+// hide the loads: the 8 x 64k q8_0 verify took 286 against 171 us.
+constexpr int d128_groups_per_cu(int /*kv_type*/, int /*row_tiles*/, bool /*generic*/) { return 2; }
+// Work-groups per CU of a decode launch (the 32-cell kernel runs one).
+inline int decode_groups_per_cu(int kv_type, int row_tiles, int head_dim, bool generic) {
+    return decode_wide_kernel(kv_type, row_tiles, head_dim, generic) ? 1 : d128_groups_per_cu(kv_type, row_tiles, generic);
 }
 // Cells per split tile of the decode launch.
-inline int decode_tile_cells(int kv_type, int row_tiles, int head_dim) {
-    return decode_wide_kernel(kv_type, row_tiles, head_dim) ? kDecodeTileWide : kDecodeTile;
+inline int decode_tile_cells(int kv_type, int row_tiles, int head_dim, bool generic) {
+    return decode_wide_kernel(kv_type, row_tiles, head_dim, generic) ? kDecodeTileWide : kDecodeTile;
 }
 // Fixed cost of starting a piece (loading Q, filling the ring, merging and writing the
 // rows), in tiles of the split: each segment weighs tiles + seg_cost, so a work-group whose
 // range enters a segment gets that many tiles less.
 constexpr int kWideSegCost = 12;
-inline int decode_seg_cost(int kv_type, int row_tiles, int head_dim) {
-    return decode_wide_kernel(kv_type, row_tiles, head_dim) ? kWideSegCost : 0;
+inline int decode_seg_cost(int kv_type, int row_tiles, int head_dim, bool generic) {
+    return decode_wide_kernel(kv_type, row_tiles, head_dim, generic) ? kWideSegCost : 0;
 }
 // Row tiles the decode kernel runs for `rows` = G * n_q rows, i.e. exactly the rows of the
 // launched kernel's partial slots (16 per tile): 128-dim heads run up to 3 per wave, beyond

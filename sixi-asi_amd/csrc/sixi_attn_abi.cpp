@@ -36,6 +36,7 @@ struct Plan {
     int mask_mode = 0;
     int D = 0;
     bool splitk = true;
+    bool generic = false;      // explicit mask or softcap: the decode kernels' per-cell mode
     size_t seg_offset = 0;  // split-K: byte offset of the per-segment piece table
     int row_tiles = 0;
     int heads_per_launch = 0;  // split-K: heads of each GQA group per launch (the group in parts)
@@ -202,6 +203,7 @@ int resolve(const sixi_attn_params* p, Plan* out) {
 
     pl.kv_type = k.type;
     pl.mask_mode = mode;
+    pl.generic = mode == SIXI_MASK_EXPLICIT || softcap != 0.0f;
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
@@ -232,8 +234,8 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     if (pl.splitk) {
         pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q, pl.D);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles, pl.D);
-        a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles, pl.D);
-        a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles, pl.D);
+        a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles, pl.D, pl.generic);
+        a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles, pl.D, pl.generic);
         // slot indices run up to S*Hkv + P - 2 for a launch of P <= kMaxSplitGroups work-groups
         splitk_layout(pl, S * Hkv + sixi::kMaxSplitGroups);
     } else {
@@ -271,7 +273,9 @@ char* scratch_base() {
 
 // Work-groups of the launch: the split-K grid, or (prefill) the CU count its order needs.
 int launch_groups(const Plan& pl) {
-    return pl.splitk ? sixi::decode_num_groups(pl.a, cu_count_cached(), pl.row_tiles) : cu_count_cached();
+    return pl.splitk ? sixi::decode_num_groups(pl.a, cu_count_cached(),
+                                               sixi::decode_groups_per_cu(pl.kv_type, pl.row_tiles, pl.D, pl.generic))
+                     : cu_count_cached();
 }
 
 // Launches a resolved call on `ws` (laid out as pl says).
