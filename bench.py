@@ -456,6 +456,28 @@ def time_gdn(steps: int, warmup: int) -> dict:
             "frac_of_fp32_peak": round(flops / (us * 1e-6) / 1e12 / FP32_PEAK_TFLOPS, 4)}
 
 
+def batched_verify_q8():
+    """The headline verify workload over a q8_0 cache (same seeds, lengths and heads)."""
+    import dataclasses
+
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    return dataclasses.replace(wl.config("batched_verify"), name="batched_verify_q8", kv_type=sa.TYPE_Q8_0)
+
+
+def verify_q8_only(steps: int, warmup: int) -> int:
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    fa = sa.FlashAttnExt()
+    w = batched_verify_q8()
+    dev = wl.to_device(wl.make_host(w))
+    ms, per = time_calls(fa, w, dev, max(1, steps), warmup)
+    print(json.dumps({"workload": "batched verify over a q8_0 cache", **summarize(w, ms, per)}), flush=True)
+    return 0
+
+
 def prefill_only(steps: int, warmup: int) -> int:
     import sixi_attn as sa
 
@@ -471,7 +493,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "layer", "gdn"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "layer", "gdn", "verify_q8"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -494,6 +516,8 @@ def main() -> int:
     if args.workload == "gdn":
         print(json.dumps(time_gdn(max(8, args.steps), args.warmup)), flush=True)
         return 0
+    if args.workload == "verify_q8":
+        return verify_q8_only(args.steps, args.warmup)
 
     import sixi_attn as sa
     from sixi_attn import workloads as wl
@@ -570,9 +594,10 @@ def main() -> int:
 
     if not args.no_extra:
         extra = {}
-        for name in ("decode", "verify", "long_q8_decode", "long_q8_verify", "decode_d256", "batched_verify_d256"):
+        for name in ("decode", "verify", "long_q8_decode", "long_q8_verify", "batched_verify_q8", "decode_d256",
+                     "batched_verify_d256"):
             try:
-                we = wl.config(name)
+                we = batched_verify_q8() if name == "batched_verify_q8" else wl.config(name)
                 he = wl.make_host(we)
                 de = wl.to_device(he)
                 mse, pere = time_calls(fa, we, de, max(20, args.steps // 2), max(5, args.warmup // 2))

@@ -709,8 +709,10 @@ struct alignas(256) WideLds {
 // Q^T B operands of row tiles n0 .. n0+NT-1 in registers: lane (r, c) gets row 16(n0+n) + r
 // at dims 32ks + 8c .. +7 as f16 (rows >= R are zero).  All loads are issued before any is
 // used -- padding rows read row 0, which every piece has -- so the piece start pays one
-// memory latency, not one per operand.
-template <int NT, int KS>
+// memory latency, not one per operand.  Q8: Q goes through ggml's conversion to the q8_0 dot
+// type first (per 32-dim block d = amax/127, q = round-half-away(x * 127/amax) clamped to
+// +-127, the MFMA taking f16(q * f16(d))); the block's four lanes (c = 0..3) are lanes r + 16c.
+template <int NT, int KS, bool Q8 = false>
 __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, int R, int n0, int lane,
                                                 f16x8 (&qv)[NT][KS]) {
     const int r = lane & 15, c = lane >> 4;
@@ -724,6 +726,25 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
         src[n] = a.q + (int64_t)(rr / a.Gr) * a.q_nb1 + (int64_t)(g * a.G + a.hoff + rr % a.Gr) * a.q_nb2 +
                  (int64_t)s * a.q_nb3 + (int64_t)(8 * c) * a.q_es;
     }
+    auto store = [&](int n, int ks, const float (&x)[8]) {
+        f16x8 hv;
+        if constexpr (Q8) {
+            float am = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(x[e]));
+            am = fmaxf(am, __shfl_xor(am, 16, 64));
+            am = fmaxf(am, __shfl_xor(am, 32, 64));
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 127.0f / am : 0.0f;
+            const float dh = (float)(_Float16)d;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = (_Float16)(fminf(fmaxf(roundf(x[e] * id), -127.0f), 127.0f) * dh);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = (_Float16)x[e];
+        }
+        qv[n][ks] = valid[n] ? hv : f16x8{};
+    };
     if (a.q_f16) {
         u32x4 raw[NT][KS];
 #pragma unroll
@@ -733,7 +754,16 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
 #pragma unroll
         for (int n = 0; n < NT; ++n)
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) qv[n][ks] = valid[n] ? as_f16x8(raw[n][ks]) : f16x8{};
+            for (int ks = 0; ks < KS; ++ks) {
+                if constexpr (Q8) {
+                    float x[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = (float)as_f16x8(raw[n][ks])[e];
+                    store(n, ks, x);
+                } else {
+                    qv[n][ks] = valid[n] ? as_f16x8(raw[n][ks]) : f16x8{};
+                }
+            }
     } else {
         f32x4 raw[NT][KS][2];
 #pragma unroll
@@ -747,13 +777,13 @@ __device__ __forceinline__ void load_q_operands(const FaArgs& a, int s, int g, i
         for (int n = 0; n < NT; ++n)
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                f16x8 hv;
+                float x[8];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    hv[e] = (_Float16)raw[n][ks][0][e];
-                    hv[4 + e] = (_Float16)raw[n][ks][1][e];
+                    x[e] = raw[n][ks][0][e];
+                    x[4 + e] = raw[n][ks][1][e];
                 }
-                qv[n][ks] = valid[n] ? hv : f16x8{};
+                store(n, ks, x);
             }
     }
 }
@@ -1213,6 +1243,244 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     __syncthreads();  // LDS (merge buffers, rings) is reused by the next piece
 }
 
+// ---------------------------------------------------------------------------------------
+// q8_0 KV, 49..96 rows per GQA group (128-dim heads): the 32-cell kernel over q8_0 steps.
+//
+// A step's q8_0 rows (32 cells x 136 B of K, the same of V) come in by dword LDS-DMA into a
+// ring of q8_0 slots.  During step i the lane's waves convert step i+1 into f16 rows laid out
+// exactly as the f16 kernel stages them (K 16-byte chunks swizzled by cell % 16, V 32-byte
+// chunks by cell % 8), in one of two f16 buffers, so the score and PV code of the f16 kernel
+// runs unchanged on them.  The conversion is f16(q * d), one rounding -- the operands the
+// q8_0 16-cell kernel and the f16 staging path use -- and Q goes through ggml's conversion to
+// the q8_0 dot type.  With two row groups, row group 0 stages and converts K, row group 1 V;
+// one row group does both.  K and V are read once for all 96 rows (the 16-cell q8_0 kernel
+// holds 48 rows, so such a block would take two launches, each reading the KV).
+constexpr int kQ8StepBytes = 32 * kQ8Row;       // 4352: one step's K (or V) rows
+constexpr int kQ8StepLoads = kQ8StepBytes / 256;  // 17 dword LDS-DMA loads
+static_assert(kQ8StepLoads * 256 == kQ8StepBytes, "a step is a whole number of dword loads");
+constexpr int kQ8Slot = 2 * kQ8StepBytes;       // K + V
+template <int RS> constexpr int q8_slots() { return RS == 1 ? 3 : 4; }  // vmcnt holds 2 x 2 x 18 at most
+template <int NTW, int RS, bool GEN>
+struct alignas(256) WideQ8Lds {
+    static constexpr int TL = 2;
+    union {
+        struct {
+            u32x4 f16buf[TL * 2 * WideDim<128>::SLOT / 16];   // two converted steps per lane
+            u32x4 q8ring[TL * q8_slots<RS>() * kQ8Slot / 16];
+        } t;
+        MergeBuf<NTW, (RS * TL + 1) / 2, WideDim<128>::DT> mg;
+    };
+    u32x4 mring[GEN ? TL * q8_slots<RS>() * kMaskTile / 16 : 1];
+    StreamTable st;
+};
+
+// Converts the q8_0 rows of one step (K or V, 32 cells) to f16 at `dst` in the f16 kernel's
+// LDS layout: this lane's blocks idx = lane + 64m (cell idx / 4, block idx % 4), m < M.
+template <int M, bool IS_V>
+__device__ __forceinline__ void q8_step_to_f16(const uint32_t* src, char* dst, int lane) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int idx = lane + 64 * m;
+        const int x = idx >> 2, b = idx & 3;
+        uint16_t d;
+        uint32_t w[8];
+        ld_q8_block(src, x * kQ8Row + 34 * b, d, w);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32x4 h = dequant_q8x8(w[2 * k], w[2 * k + 1], d);
+            const int j = 4 * b + k;  // 16-byte chunk: dims 8j .. 8j+7
+            const int pos = IS_V ? 32 * ((j >> 1) ^ (x & 7)) + 16 * (j & 1) : 16 * (j ^ (x & 15));
+            *reinterpret_cast<u32x4*>(dst + x * WideDim<128>::ROW + pos) = h;
+        }
+    }
+}
+
+template <int NTW, int RS, int MODE>
+__device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<NTW, RS, MODE != MODE_FAST>& sh,
+                                                     int causal, const Piece& pc) {
+    using W = WideDim<128>;
+    constexpr int TL = 2;
+    constexpr int NSQ = q8_slots<RS>();
+    constexpr bool GEN = MODE != MODE_FAST;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int w = tid >> 6;
+    const int rg = w / TL;
+    const int tl = w % TL;
+    const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
+    const StreamDims sd = table_dims(sh.st, s);
+    const int G = a.Gr;
+    const int hb = g * a.G + a.hoff;
+    const int R = G * sd.ql;
+    const int n0 = rg * NTW;
+    const int r = lane & 15;
+    const int c = lane >> 4;
+
+    f16x8 qv[NTW][W::KS];
+    load_q_operands<NTW, W::KS, true>(a, s, g, R, n0, lane, qv);
+
+    RowInfo<NTW> ri;
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) {
+        const int row = 16 * (n0 + n) + r;
+        const bool valid = row < R;
+        const int j = valid ? row / G : 0;
+        ri.j[n] = j;
+        ri.vis[n] = (valid && causal) ? sd.kl + j + 1 : sd.nc;
+        ri.slope[n] = (MODE == MODE_GENERIC) ? alibi_slope(a, hb + (valid ? row % G : 0)) : 1.0f;
+    }
+    const int t_full = (MODE == MODE_GENERIC) ? 0 : ((causal && MODE == MODE_FAST) ? (sd.kl + 1) / kWide : sd.nc / kWide);
+    const char* mrow = nullptr;
+    if (MODE != MODE_FAST && a.mask) mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3;
+
+    Acc<NTW, W::DT> acc;
+    acc_clear(acc);
+
+    const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
+    // K/V of the piece's steps (same form as the f16 kernel): read offsets t * kv_nb of the
+    // dword t = 64u + lane of a step's rows -- row t / 34, dword t % 34 -- relative to the
+    // step's first cell; row group 0 loads K, row group 1 V (one row group: both)
+    uint32_t ko[kQ8StepLoads], vo[kQ8StepLoads];
+#pragma unroll
+    for (int u = 0; u < kQ8StepLoads; ++u) {
+        const uint32_t t = 64u * u + (uint32_t)lane;
+        ko[u] = (t / (kQ8Row / 4)) * knb + (t % (kQ8Row / 4)) * 4u;
+        vo[u] = (t / (kQ8Row / 4)) * vnb + (t % (kQ8Row / 4)) * 4u;
+    }
+    uint32_t kofs[W::KS];
+#pragma unroll
+    for (int ks = 0; ks < W::KS; ++ks) kofs[ks] = (uint32_t)W::ROW * r + 16u * (uint32_t)((4 * ks + c) ^ r);
+    const uint32_t vrow = (uint32_t)(4 * c + (r >> 2)) * (uint32_t)W::ROW + 32u * (4 * (c & 1) + (r >> 2)) + 8u * (r & 3);
+
+    const int t0 = tb + tl;
+    const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
+    const int n_iter = (te - tb + TL - 1) / TL;
+    u32x4* f16buf = sh.t.f16buf + (size_t)tl * 2 * (W::SLOT / 16);
+    const uint32_t* q8ring = reinterpret_cast<const uint32_t*>(sh.t.q8ring + (size_t)tl * NSQ * (kQ8Slot / 16));
+    const uint32_t q8_base = lds_addr(sh.t.q8ring) + (uint32_t)tl * NSQ * kQ8Slot;
+
+    const buf_rsrc mrs = make_rsrc_uniform(mrow, GEN && a.mask_stage ? a.m_bytes : 0u);
+    const uint32_t mring_base = lds_addr(sh.mring) + (uint32_t)tl * NSQ * kMaskTile;
+    PageIds pages = page_ids_load(a, s, (t0 * kWide) >> 8);
+    auto issue = [&](int i) {
+        const int slot = i % NSQ;
+        const uint32_t c0 = (uint32_t)(t0 + i * TL) * kWide;
+        const uint32_t base = q8_base + (uint32_t)slot * kQ8Slot;
+        const int page = (int)c0 < sd.nc ? page_id(pages, a, s, (int)(c0 >> 8)) : 0;
+        if constexpr (GEN) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                if (RS == 1 || rg == half) {
+                    const uint32_t j = 16u * half + (uint32_t)lane / 4;
+                    dma16x1_to_lds(mrs, j * (uint32_t)a.m_nb1 + (c0 + 8u * (lane & 3)) * 2u,
+                                   mring_base + (uint32_t)slot * kMaskTile + 1024u * half);
+                }
+            }
+        }
+        if (rg == 0) {
+            const KvSpan sp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, (int)c0, sd.nc, kQ8Row, page);
+            const buf_rsrc rs = make_rsrc_uniform(sp.p, sp.bytes);
+            uint32_t o8[8], o9[9];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o8[u] = ko[u];
+#pragma unroll
+            for (int u = 0; u < 9; ++u) o9[u] = ko[8 + u];
+            dma4x8_to_lds(rs, o8, base);
+            dma4x9_to_lds(rs, o9, base + 8 * 256);
+        }
+        if (rg == (RS == 1 ? 0 : 1)) {
+            const KvSpan sp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, (int)c0, sd.nc, kQ8Row, page);
+            const buf_rsrc rs = make_rsrc_uniform(sp.p, sp.bytes);
+            uint32_t o8[8], o9[9];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o8[u] = vo[u];
+#pragma unroll
+            for (int u = 0; u < 9; ++u) o9[u] = vo[8 + u];
+            dma4x8_to_lds(rs, o8, base + kQ8StepBytes);
+            dma4x9_to_lds(rs, o9, base + kQ8StepBytes + 8 * 256);
+        }
+    };
+    // step i's q8_0 rows -> f16 buffer i % 2
+    auto convert = [&](int i) {
+        const uint32_t* src = q8ring + (size_t)(i % NSQ) * (kQ8Slot / 4);
+        char* dst = reinterpret_cast<char*>(f16buf + (size_t)(i & 1) * (W::SLOT / 16));
+        if (rg == 0) q8_step_to_f16<2, false>(src, dst, lane);
+        if (rg == (RS == 1 ? 0 : 1)) q8_step_to_f16<2, true>(src + kQ8StepBytes / 4, dst + 32 * W::ROW, lane);
+    };
+    constexpr int LPW = (RS == 1 ? 2 : 1) * (kQ8StepLoads + (GEN ? 1 : 0));
+    const int n_plain = min(max((t_full - tb) / TL, 0), (te - tb) / TL);
+    {
+        // Issue order: steps 0 .. NSQ-2 up front, then step i+NSQ-1 after the barrier of step i
+        // (into the slot of step i-1, converted during step i-2).  Before the barrier of step i
+        // each wave waits for step i+1's loads, which the conversion during step i reads; the
+        // batches issued after it may stay in flight.
+        // own loads of step j landed, with steps 0 .. issued-1 issued so far
+        auto wait_for = [&](int j, int issued) {
+            const int later = max(min(issued, n_my) - (j + 1), 0);
+            if (later >= 2) wait_vmcnt<2 * LPW>();
+            else if (later == 1) wait_vmcnt<LPW>();
+            else wait_vmcnt<0>();
+        };
+#pragma unroll
+        for (int q = 0; q < NSQ - 1; ++q)
+            if (q < n_my) issue(q);
+#pragma unroll
+        for (int n = 0; n < NTW; ++n)
+#pragma unroll
+            for (int ks = 0; ks < W::KS; ++ks) asm volatile("" ::"v"(qv[n][ks]));
+        if (n_my > 0) wait_for(0, NSQ - 1);
+        __syncthreads();
+        if (n_my > 0) convert(0);
+        auto scores = [&](int i, auto masked, WideStep<NTW, 128>& ws) -> bool {
+            if (i + 1 < n_my) wait_for(i + 1, i + NSQ - 1);
+            __syncthreads();
+            if (i + NSQ - 1 < n_my) issue(i + NSQ - 1);
+            if (i + 1 < n_my) convert(i + 1);
+            if (!decltype(masked)::value || i < n_my) {
+                const int t = t0 + i * TL;
+                const u32x4* kslot = f16buf + (size_t)(i & 1) * (W::SLOT / 16);
+                const uint32_t vlane = lds_addr(kslot) + 32 * W::ROW + vrow;
+                return wide_scores<NTW, MODE, decltype(masked)::value, 128>(
+                    a, acc, ws, kslot, vlane, kofs, qv, t * kWide, ri, mrow,
+                    mring_base + (uint32_t)(i % NSQ) * kMaskTile, sd.nc, lane);
+            }
+            return false;
+        };
+        auto finish = [&](int i, auto masked, const WideStep<NTW, 128>& ws) {
+            if (!decltype(masked)::value || i < n_my)
+                wide_pv<NTW, MODE, 128>(a, acc, ws, lds_addr(f16buf + (size_t)(i & 1) * (W::SLOT / 16)) + 32 * W::ROW + vrow,
+                                        lane);
+        };
+        int i = 0;
+        auto run = [&](int end, auto masked) {
+#pragma unroll 1
+            for (; i < end; ++i) {
+                WideStep<NTW, 128> ws;
+                if (scores(i, masked, ws)) wide_rescale<NTW, MODE, 128>(a, acc, ws);
+                finish(i, masked, ws);
+            }
+        };
+        run(n_plain, std::false_type{});
+        run(n_iter, std::true_type{});
+    }
+    acc_settle(acc.o);
+
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) {
+        acc.l[n] = sum4_rowgroups(acc.l[n]);
+        if (raw_units<MODE>() && acc.m[n] != neg_inf()) acc.m[n] *= a.scale_log2;
+    }
+
+    __syncthreads();
+    if (merge_lanes<NTW, TL>(sh.mg, acc, rg, tl, lane)) {
+        if (tb == 0 && te == pc.nt_seg)
+            write_rows_wide(a, acc, n0, s, g, R, lane);
+        else
+            write_partial_wide(a.part + pc.slot * a.slot_floats, NTW * RS * 16, n0, R, acc, lane);
+    }
+    __syncthreads();
+}
+
 // Work-group -> range of the cost line (segments laid end to end, each seg_cost units of
 // start-up followed by its tiles).  Returns false for a work-group without a range.
 struct Partition {
@@ -1294,6 +1562,15 @@ void decode_wide(FaArgs a, int causal) {
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
     for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
+}
+
+template <int NTW, int RS, int MODE>
+__global__ __launch_bounds__((RS * 2 * 64), (RS * 2 + 3) / 4)
+void decode_wide_q8(FaArgs a, int causal) {
+    __shared__ WideQ8Lds<NTW, RS, MODE != MODE_FAST> sh;
+    if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
+    __syncthreads();
+    for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide_q8<NTW, RS, MODE>(a, sh, causal, pc); });
 }
 
 // Combines the pieces of every segment that more than one work-group touched, for segments of
@@ -1448,6 +1725,22 @@ hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream
     return hipGetLastError();
 }
 
+template <int NTW, int RS>
+hipError_t launch_wide_q8(const FaArgs& a, int mode, int causal, hipStream_t stream) {
+    if (!slot_fits(a, NTW * RS * 16, 128)) return hipErrorInvalidValue;
+    const dim3 grid(a.P), block(RS * 2 * 64);
+    if (mode == MODE_GENERIC)
+        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+    else if (mode == MODE_MASK)
+        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_MASK>), grid, block, 0, stream, a, causal);
+    else
+        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_FAST>), grid, block, 0, stream, a, causal);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_merge<128>(a, NTW * RS * 16, stream);
+    return hipGetLastError();
+}
+
 template <int NTW, int KV>
 hipError_t launch_nt(const FaArgs& a, int mode, int causal, hipStream_t stream) {
     if (!slot_fits(a, NTW * 16, 128)) return hipErrorInvalidValue;
@@ -1527,6 +1820,8 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
             case 1: return launch_nt<1, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
             case 2: return launch_nt<2, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
             case 3: return launch_nt<3, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
+            case 4: return launch_wide_q8<kWide64.ntw, kWide64.rs>(a, mode, causal, stream);
+            case 6: return launch_wide_q8<kWide96.ntw, kWide96.rs>(a, mode, causal, stream);
             default: return hipErrorNotSupported;
         }
     }

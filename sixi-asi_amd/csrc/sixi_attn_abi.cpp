@@ -207,13 +207,12 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
-    // q8_0 KV runs the 16-cell split-K kernel, which holds up to 48 rows per kv-head group:
-    // a larger group is covered in launches over disjoint head subsets (each reads the KV).
+    // q8_0 KV at 128-dim heads runs the split-K kernels (up to 48 rows the 16-cell kernel,
+    // 49..96 the 32-cell kernel) in one launch that reads the KV once
     pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
-        // (the q8_0 split-K kernel holds 128-dim rows)
-        if (D == 128 && pl.splitk && n_q <= kQ8MaxRows) {
-            pl.heads_per_launch = (int)(kQ8MaxRows / n_q);
+        if (D == 128 && pl.splitk) {
+            // one launch of the 32-cell q8_0 kernel
         } else {
             // prefill-sized blocks, more than 48 rows of one head, or 256-dim heads: K, V and Q
             // are staged as f16 operands in the workspace (fa_q8_stage.hip) and the f16 kernels run

@@ -2,7 +2,8 @@
 (ALiBi-style distance terms), ALiBi slopes (max_bias), logit softcap, and masks that cannot
 be staged through LDS (rows not 16-byte aligned, more than 32 rows), at every decode shape
 that takes them -- f16 at 6, 24 and 48 rows per GQA group (32-cell kernel, one row group per
-lane), 64 and 96 rows, q8_0 (16-cell kernel), 256-dim heads -- and the prefill kernel.
+lane), 64 and 96 rows, q8_0 (16-cell kernel up to 48 rows, the 32-cell q8_0 kernel beyond),
+256-dim heads -- and the prefill kernel.
 Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output, as for the other parity tests."""
 import sys
 
@@ -56,6 +57,8 @@ CASES = [
     ("f16 64 rows, softcap", sa.TYPE_F16, 128, [1200], [8], 32, 4, 0.0, 0.0, 50.0, 0),
     ("q8_0 48 rows, alibi", sa.TYPE_Q8_0, 128, [1000, 200], [8, 8], 24, 4, 0.05, 8.0, 0.0, 0),
     ("q8_0 12 rows, softcap", sa.TYPE_Q8_0, 128, [1500], [2], 24, 4, 0.0, 0.0, 30.0, 0),
+    ("q8_0 96 rows, distance mask", sa.TYPE_Q8_0, 128, [900, 2000], [16, 11], 24, 4, 0.02, 0.0, 0.0, 0),
+    ("q8_0 72 rows, alibi + softcap", sa.TYPE_Q8_0, 128, [1300, 40], [12, 12], 24, 4, 0.03, 8.0, 20.0, 0),
     ("256-dim 96 rows, alibi", sa.TYPE_F16, 256, [600, 1100], [16, 4], 24, 4, 0.03, 8.0, 0.0, 0),
     ("256-dim 6 rows, softcap", sa.TYPE_F16, 256, [2000], [1], 24, 4, 0.0, 0.0, 30.0, 0),
     ("prefill rows, alibi + softcap", sa.TYPE_F16, 128, [200], [150], 24, 4, 0.02, 8.0, 25.0, 0),

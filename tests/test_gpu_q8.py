@@ -107,17 +107,18 @@ def test_q8_explicit_mask_and_invariance(fa):
 
 
 @pytest.mark.parametrize("kv_len,q_len,H,Hkv", [
-    ([2000, 0, 513], [16, 16, 9], 24, 4),        # 16-token verify at GQA 6:1: 96 rows, two launches of 3 heads
-    ([700, 4100], [12, 5], 20, 4),               # GQA 5:1, 60 rows: launches of 4 and 1 heads
+    ([2000, 0, 513], [16, 16, 9], 24, 4),        # 16-token verify at GQA 6:1: 96 rows
+    ([700, 4100], [12, 5], 20, 4),               # GQA 5:1, 60 rows (run as 64)
+    ([30000], [16], 24, 4),                      # one long stream: many pieces per segment
 ])
-def test_q8_group_in_head_parts(fa, kv_len, q_len, H, Hkv):
-    """More than 48 rows per kv-head group: covered by launches over disjoint head subsets."""
-    _say(f"q8 head parts kv_len={kv_len} q_len={q_len} H={H} Hkv={Hkv}")
+def test_q8_more_than_48_rows(fa, kv_len, q_len, H, Hkv):
+    """49..96 rows per kv-head group: the 32-cell q8_0 kernel, one launch reading the KV once."""
+    _say(f"q8 49..96 rows kv_len={kv_len} q_len={q_len} H={H} Hkv={Hkv}")
     w = wl.Workload("q8_parts", 0x51A7_7000 + sum(kv_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv,
                     kv_type=sa.TYPE_Q8_0)
     host = wl.make_host(w, poison=True)
     dev = wl.to_device(host)
-    _check(w, host, _run(fa, w, dev), list(range(w.S)), "q8 head parts")
+    _check(w, host, _run(fa, w, dev), list(range(w.S)), "q8 49..96 rows")
 
 
 @pytest.mark.parametrize("name,kv_len,q_len,H,Hkv", [
