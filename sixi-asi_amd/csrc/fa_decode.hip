@@ -1489,11 +1489,22 @@ struct Partition {
 };
 
 __device__ __forceinline__ bool partition(const FaArgs& a, const int* ps, int b, Partition& pt) {
-    pt.T = (int64_t)a.Hkv * ps[a.S];
-    pt.P = pt.T < a.P ? pt.T : a.P;  // active work-groups: every one owns >= 1 unit
     // logical index: with the remap, consecutive tile ranges land on one XCD (work-groups
     // are dealt round-robin over the XCDs)
     pt.p_log = a.xcd_remap ? (b % kXcds) * (a.P / kXcds) + b / kXcds : b;
+    if (a.head_split) {
+        // ranges over the streams' cost line, each taken by the Hkv work-groups Hkv*q .. +Hkv-1
+        pt.T = ps[a.S];
+        const int64_t Q = a.P / a.Hkv;
+        pt.P = pt.T < Q ? pt.T : Q;
+        const int64_t q = pt.p_log / a.Hkv;
+        if (q >= pt.P) return false;
+        pt.x0 = q * pt.T / pt.P;
+        pt.x1 = (q + 1) * pt.T / pt.P;
+        return true;
+    }
+    pt.T = (int64_t)a.Hkv * ps[a.S];
+    pt.P = pt.T < a.P ? pt.T : a.P;  // active work-groups: every one owns >= 1 unit
     if (pt.p_log >= pt.P) return false;
     pt.x0 = pt.p_log * pt.T / pt.P;
     pt.x1 = (pt.p_log + 1) * pt.T / pt.P;
@@ -1506,6 +1517,38 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
     Partition pt;
     if (!partition(a, ps, blockIdx.x, pt)) return;
     const int64_t Hkv = a.Hkv;
+    if (a.head_split) {
+        // this work-group's kv-head over the cells of its range of every stream it touches;
+        // piece q of segment k sits in slot k + q * Hkv
+        const int g = (int)(pt.p_log % Hkv);
+        const int64_t q = pt.p_log / Hkv;
+        int lo = 0, hi = a.S;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (ps[mid] <= pt.x0) lo = mid; else hi = mid - 1;
+        }
+        for (int s = lo; s < a.S && ps[s] < pt.x1; ++s) {
+            const int ct = ps[s + 1] - ps[s];
+            const int64_t t0 = (int64_t)ps[s] + a.seg_cost;
+            const int64_t xb = pt.x0 > t0 ? pt.x0 : t0;
+            const int64_t xe = pt.x1 < ps[s + 1] ? pt.x1 : ps[s + 1];
+            if (xb >= xe) continue;
+            Piece pc;
+            pc.s = __builtin_amdgcn_readfirstlane(s);
+            pc.g = __builtin_amdgcn_readfirstlane(g);
+            pc.tb = __builtin_amdgcn_readfirstlane((int)(xb - t0));
+            pc.te = __builtin_amdgcn_readfirstlane((int)(xe - t0));
+            pc.nt_seg = __builtin_amdgcn_readfirstlane(ct - a.seg_cost);
+            pc.slot = __builtin_amdgcn_readfirstlane((int)(((int64_t)s + q) * Hkv + g));
+            if (threadIdx.x == 0) {
+                const int64_t seg = (int64_t)s * Hkv + g;
+                if (pc.tb == 0) a.seg_pieces[2 * seg] = (int)q;
+                if (pc.te == pc.nt_seg) a.seg_pieces[2 * seg + 1] = (int)q;
+            }
+            fn(pc);
+        }
+        return;
+    }
 
     // stream holding unit x0: the largest s with Hkv*ps[s] <= x0
     int lo = 0, hi = a.S;
@@ -1608,7 +1651,7 @@ __global__ __launch_bounds__(256) void decode_merge_pieces(FaArgs a, int rows_sl
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int p = p0 + PG * u <= p_last ? p0 + PG * u : p_last;
-            const float* sl = base + (int64_t)p * a.slot_floats;
+            const float* sl = base + (int64_t)p * a.piece_stride * a.slot_floats;
             hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * (2 * D) + d0 * 2);
             mv[u] = sl[(int64_t)rows_slot * (D / 2) + row];
             lv[u] = sl[(int64_t)rows_slot * (D / 2 + 1) + row];
@@ -1667,7 +1710,7 @@ __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int p = p0 + u <= p_last ? p0 + u : p_last;
-            const float* sl = base + (int64_t)p * a.slot_floats;
+            const float* sl = base + (int64_t)p * a.piece_stride * a.slot_floats;
             hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * (2 * D) + d0 * 2);
             mv[u] = sl[(int64_t)rows_slot * (D / 2) + row];
             lv[u] = sl[(int64_t)rows_slot * (D / 2 + 1) + row];
@@ -1725,8 +1768,25 @@ hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream
     return hipGetLastError();
 }
 
+// q8_0 rows of one cell are 34*D/32 bytes per head, so neighbouring heads share L2 lines.
+// The kv-heads of a cell range go to Hkv work-groups of one XCD that start together, which
+// fetch each shared line from HBM once (split over (stream, head) segments, two XCDs' L2s
+// each fetch the shared lines); the grid becomes a multiple of 8 * Hkv.
+inline FaArgs head_split_args(const FaArgs& a) {
+    FaArgs b = a;
+    const int64_t unit = (int64_t)kXcds * a.Hkv;
+    if (a.P >= unit) {
+        b.P = (int)(a.P / unit * unit);
+        b.head_split = 1;
+        b.piece_stride = a.Hkv;
+        b.xcd_remap = 1;
+    }
+    return b;
+}
+
 template <int NTW, int RS>
-hipError_t launch_wide_q8(const FaArgs& a, int mode, int causal, hipStream_t stream) {
+hipError_t launch_wide_q8(const FaArgs& a_in, int mode, int causal, hipStream_t stream) {
+    const FaArgs a = head_split_args(a_in);
     if (!slot_fits(a, NTW * RS * 16, 128)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(RS * 2 * 64);
     if (mode == MODE_GENERIC)

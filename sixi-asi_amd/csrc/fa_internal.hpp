@@ -52,6 +52,9 @@ struct FaArgs {
     float* part;           // partial slots of slot_floats floats: O/l rows [rows][128] f16, then m, l
     int32_t P;             // work-groups of the split-K launch (prefill: CUs of the device)
     int32_t xcd_remap;     // 1: consecutive tile ranges go to work-groups of one XCD
+    int32_t head_split;    // 1: the cost line runs over streams, and each range is taken by Hkv
+                           // work-groups at once, one per kv-head (same cells, same start)
+    int32_t piece_stride;  // slot of piece p of segment k: k + p * piece_stride
     int32_t tile_cells;    // KV cells per split tile (decode_tile_cells)
     int32_t seg_cost;      // tiles' worth of work charged to each segment in the split
     int64_t slot_floats;   // floats per partial slot

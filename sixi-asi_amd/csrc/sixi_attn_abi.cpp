@@ -306,6 +306,8 @@ int run(Plan& pl, char* ws, hipStream_t stream) {
     a.P = launch_groups(pl);
     if (pl.splitk) {
         a.xcd_remap = 0;
+        a.head_split = 0;
+        a.piece_stride = 1;
         e = hipSuccess;
         // one launch pair per head subset, ordered on the stream (they share the workspace)
         for (int h0 = 0; h0 < a.G && e == hipSuccess; h0 += pl.heads_per_launch) {
