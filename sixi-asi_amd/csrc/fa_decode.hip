@@ -1275,24 +1275,29 @@ struct alignas(256) WideQ8Lds {
 };
 
 // Converts the q8_0 rows of one step (K or V, 32 cells) to f16 at `dst` in the f16 kernel's
-// LDS layout: this lane's blocks idx = lane + 64m (cell idx / 4, block idx % 4), m < M.
-template <int M, bool IS_V>
-__device__ __forceinline__ void q8_step_to_f16(const uint32_t* src, char* dst, int lane) {
+// LDS layout: lane (h, x) = (lane / 32, lane % 32) takes block b = 2h + m of cell x in pass
+// m.  Block b starts 34b bytes into a 136-byte row, so all lanes of a pass have the scale in
+// the same half of a dword (no divergent unpacking), and the 64 lanes' dword reads (row
+// stride 34 dwords, h offset 17) hit 64 distinct banks.
+template <bool IS_V, int M>
+__device__ __forceinline__ void q8_block_to_f16(const uint32_t* src, char* dst, int x, int h) {
+    const int b = 2 * h + M;
+    uint16_t d;
+    uint32_t w[8];
+    ld_q8_block<M == 1>(src, x * kQ8Row + 34 * b, d, w);
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        const int idx = lane + 64 * m;
-        const int x = idx >> 2, b = idx & 3;
-        uint16_t d;
-        uint32_t w[8];
-        ld_q8_block(src, x * kQ8Row + 34 * b, d, w);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const u32x4 h = dequant_q8x8(w[2 * k], w[2 * k + 1], d);
-            const int j = 4 * b + k;  // 16-byte chunk: dims 8j .. 8j+7
-            const int pos = IS_V ? 32 * ((j >> 1) ^ (x & 7)) + 16 * (j & 1) : 16 * (j ^ (x & 15));
-            *reinterpret_cast<u32x4*>(dst + x * WideDim<128>::ROW + pos) = h;
-        }
+    for (int k = 0; k < 4; ++k) {
+        const u32x4 f = dequant_q8x8(w[2 * k], w[2 * k + 1], d);
+        const int j = 4 * b + k;  // 16-byte chunk: dims 8j .. 8j+7
+        const int pos = IS_V ? 32 * ((j >> 1) ^ (x & 7)) + 16 * (j & 1) : 16 * (j ^ (x & 15));
+        *reinterpret_cast<u32x4*>(dst + x * WideDim<128>::ROW + pos) = f;
     }
+}
+
+template <bool IS_V>
+__device__ __forceinline__ void q8_step_to_f16(const uint32_t* src, char* dst, int lane) {
+    q8_block_to_f16<IS_V, 0>(src, dst, lane & 31, lane >> 5);
+    q8_block_to_f16<IS_V, 1>(src, dst, lane & 31, lane >> 5);
 }
 
 template <int NTW, int RS, int MODE>
@@ -1404,8 +1409,8 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
     auto convert = [&](int i) {
         const uint32_t* src = q8ring + (size_t)(i % NSQ) * (kQ8Slot / 4);
         char* dst = reinterpret_cast<char*>(f16buf + (size_t)(i & 1) * (W::SLOT / 16));
-        if (rg == 0) q8_step_to_f16<2, false>(src, dst, lane);
-        if (rg == (RS == 1 ? 0 : 1)) q8_step_to_f16<2, true>(src + kQ8StepBytes / 4, dst + 32 * W::ROW, lane);
+        if (rg == 0) q8_step_to_f16<false>(src, dst, lane);
+        if (rg == (RS == 1 ? 0 : 1)) q8_step_to_f16<true>(src + kQ8StepBytes / 4, dst + 32 * W::ROW, lane);
     };
     constexpr int LPW = (RS == 1 ? 2 : 1) * (kQ8StepLoads + (GEN ? 1 : 0));
     const int n_plain = min(max((t_full - tb) / TL, 0), (te - tb) / TL);

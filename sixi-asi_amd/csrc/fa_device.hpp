@@ -455,8 +455,9 @@ __device__ __forceinline__ uint16_t ld_half_at(const uint32_t* base, int a) {
 
 // One q8_0 block (34 bytes: f16 scale, 32 int8) at byte offset `a` (even) of a dword array:
 // the scale bits and the 32 quants as eight little-endian dwords.
+template <bool ODD2>  // a % 4 == 2
 __device__ __forceinline__ void ld_q8_block(const uint32_t* base, int a, uint16_t& d, uint32_t (&w)[8]) {
-    if (a & 2) {  // scale in the upper half of a dword, quants dword-aligned
+    if constexpr (ODD2) {  // scale in the upper half of a dword, quants dword-aligned
         d = (uint16_t)(base[(a - 2) >> 2] >> 16);
 #pragma unroll
         for (int i = 0; i < 8; ++i) w[i] = base[((a + 2) >> 2) + i];
