@@ -36,6 +36,16 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
+# Per-source flags.  fa_decode.hip: MFMA accumulators in VGPR form (the software-pipelined
+# step loop keeps O in the 256 VGPRs and its operands in AGPRs; in AGPR form the compiler
+# copies the 96 accumulator registers across every iteration).
+FILE_FLAGS = {"fa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+
+
+def flags_for(src: str) -> list[str]:
+    return [*HIP_FLAGS, *FILE_FLAGS.get(src, [])]
+
+
 HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "fa_q8_stage.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
                "sixi_kv_pool.cpp",
                "sixi_plan.cpp", "layer_prologue.hip", "sixi_layer_abi.cpp",
@@ -66,7 +76,7 @@ def build_attn(jobs: int | None = None) -> pathlib.Path:
         obj = OBJ / (src.replace(".", "_") + ".o")
         objs.append(obj)
         lang = ["-x", "hip"] if src.endswith(".cpp") else []
-        cmds.append([hipcc, *HIP_FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([hipcc, *flags_for(src), *lang, "-c", str(CSRC / src), "-o", str(obj)])
     with cf.ThreadPoolExecutor(max_workers=jobs or min(8, len(cmds))) as ex:
         list(ex.map(_run, cmds))
     out = LIB / "libsixi_attn.so"

@@ -688,6 +688,17 @@ struct WideShape { static constexpr int groups_per_cu = 1; };
 template <int RS, int D> constexpr int wide_lanes() { return (D == 256 && RS == 3) ? 1 : 2; }
 // Ring depth per lane (LDS: lanes x slots x SLOT): two steps in flight where it fits.
 template <int D, int TL> constexpr int wide_slots() { return (D == 128 || TL == 1) ? 3 : 2; }
+// The fast mode of 128-dim heads with two lanes runs the software-pipelined step loop.  It
+// reads K of the next step and V of the current one, so K and V have rings of their own
+// (8 KB slots; row group 0 stages K, row group 1 V), each as deep as LDS allows: while a
+// lane computes, 4 K and 3 V batches can be in flight (56 KB per lane).
+constexpr int kPipeK = 5, kPipeV = 4;
+template <int MODE, int D, int TL> constexpr bool wide_pipelined() { return MODE == MODE_FAST && D == 128 && TL == 2; }
+// Ring bytes of one lane.
+template <int D, int TL, bool GEN> constexpr int wide_lane_ring_bytes() {
+    return (!GEN && D == 128 && TL == 2) ? (kPipeK + kPipeV) * 32 * WideDim<D>::ROW
+                                         : wide_slots<D, TL>() * WideDim<D>::SLOT;
+}
 struct WideSplit { int ntw, rs; };            // row tiles per wave x waves per lane
 constexpr WideSplit kWide64 = {2, 2};         // 64 rows
 constexpr WideSplit kWide96 = {3, 2};         // 96 rows
@@ -699,7 +710,7 @@ constexpr int kMaskTile = 32 * 64;
 template <int NTW, int RS, int D, bool GEN>
 struct alignas(256) WideLds {
     union {
-        u32x4 ring[wide_lanes<RS, D>() * wide_slots<D, wide_lanes<RS, D>()>() * WideDim<D>::SLOT / 16];
+        u32x4 ring[wide_lanes<RS, D>() * wide_lane_ring_bytes<D, wide_lanes<RS, D>(), GEN>() / 16];
         MergeBuf<NTW, (RS * wide_lanes<RS, D>() + 1) / 2, WideDim<D>::DT> mg;  // reused after the step loop
     };
     u32x4 mring[GEN ? wide_lanes<RS, D>() * wide_slots<D, wide_lanes<RS, D>()>() * kMaskTile / 16 : 1];
@@ -1003,6 +1014,176 @@ __device__ __forceinline__ void wide_pv(const FaArgs& a, Acc<NT, WideDim<D>::DT>
     }
 }
 
+// ---- Software-pipelined fast step loop (128-dim heads, lengths only) ----
+// With one wave per SIMD nothing else hides a wave's VALU work behind its MFMAs.  Iteration
+// i of this loop therefore computes the scores of step i+1 and the PV product of step i in
+// one scheduling region: the score MFMAs issue between the exponentials of step i, the PV
+// MFMAs between the row maxima of step i+1 (MFMAs are builtins here, so that the compiler
+// interleaves them and inserts the wait states their results need).
+template <int NT>
+struct PipeState {
+    float sv[NT][8];  // raw scores of the step, masked cells -inf
+    float mx[NT];     // their row maxima
+};
+
+// S^T of a step: lane (r, c) receives cells 16h + 4c + i of row r.
+template <int NT>
+__device__ __forceinline__ void pipe_scores(const u32x4* kslot, const uint32_t (&kofs)[4], const f16x8 (&qv)[NT][4],
+                                            f32x4 (&st)[2][NT]) {
+    using W = WideDim<128>;
+    f16x8 kop[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            kop[h][ks] = as_f16x8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kslot) + kofs[ks] +
+                                                                  W::HALF * h));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int n = 0; n < NT; ++n)
+                st[h][n] = mfma16x16x32(kop[h][ks], qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
+}
+
+// Row maxima of a step's scores (cells at or past a row's visibility bound -inf when MASKED);
+// returns whether one of the lane's rows moves its exponent reference.
+template <int NT, bool MASKED>
+__device__ __forceinline__ bool pipe_max(const Acc<NT, 8>& acc, const f32x4 (&st)[2][NT], PipeState<NT>& ps, int c0,
+                                         const RowInfo<NT>& ri, float thr, int lane) {
+    const int c = lane >> 4;
+    bool need = false;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float x = st[e >> 2][n][e & 3];
+            if (MASKED && c0 + 16 * (e >> 2) + 4 * c + (e & 3) >= ri.vis[n]) x = neg_inf();
+            ps.sv[n][e] = x;
+        }
+        ps.mx[n] = max4_rowgroups(max3f(max3f(ps.sv[n][0], ps.sv[n][1], ps.sv[n][2]),
+                                        max3f(ps.sv[n][3], ps.sv[n][4], ps.sv[n][5]), max2f(ps.sv[n][6], ps.sv[n][7])));
+        need |= ps.mx[n] > acc.m[n] + thr;
+    }
+    return need;
+}
+
+// Moves the exponent reference of the rows whose step maximum exceeds it by thr, rescaling
+// their l and O (rare: only when the running maximum grows by 2^8 in exponent units).
+template <int NT>
+__device__ __forceinline__ void pipe_rescale(Acc<NT, 8>& acc, const PipeState<NT>& ps, float thr, float c2) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const bool move = ps.mx[n] > acc.m[n] + thr;
+        const float alpha = move ? fast_exp2((acc.m[n] - ps.mx[n]) * c2) : 1.0f;
+        acc.m[n] = move ? ps.mx[n] : acc.m[n];
+        acc.l[n] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc.o[t][n] *= alpha;
+    }
+}
+
+// Probabilities of a step against the (settled) reference, in f16, and their f32 row sums.
+template <int NT>
+__device__ __forceinline__ void pipe_probs(Acc<NT, 8>& acc, const PipeState<NT>& ps, float c2, f16x8 (&pt)[NT]) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+        const float ref = acc.m[n];
+        const float mc = (ref == neg_inf()) ? 0.0f : ref * c2;
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            p[e] = fast_exp2(fmaf(ps.sv[n][e], c2, -mc));
+            pt[n][e] = (_Float16)p[e];
+        }
+        acc.l[n] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    }
+}
+
+// O^T += V^T P^T, row tile by row tile.
+template <int NT>
+__device__ __forceinline__ void pipe_pv(Acc<NT, 8>& acc, const u32x4 (&vt)[8], const f16x8 (&pt)[NT]) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc.o[t][n] = mfma16x16x32(as_f16x8(vt[t]), pt[n], acc.o[t][n]);
+}
+
+// One pipelined iteration: scores of the next step (K at kslot) and the PV product of this one
+// (V^T at vlane).  The issue order is fixed by scheduling fences, slot by slot: first the LDS
+// reads, then 8*NT slots of one score MFMA and the exponential of one probability of this
+// step, then 8*NT slots of one PV MFMA and a piece of the next step's row maxima.  Returns
+// whether a row of the lane moves its exponent reference at the next step.
+template <int NT, bool MASKED>
+__device__ __forceinline__ bool pipe_iteration(Acc<NT, 8>& acc, PipeState<NT>& ps, const u32x4* kslot, uint32_t vlane,
+                                               const uint32_t (&kofs)[4], const f16x8 (&qv)[NT][4], int c0n,
+                                               const RowInfo<NT>& ri, float thr, float c2, int lane) {
+    using W = WideDim<128>;
+    const int c = lane >> 4;
+    f16x8 kop[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            kop[h][ks] = as_f16x8(*reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(kslot) + kofs[ks] +
+                                                                  W::HALF * h));
+    u32x4 vt[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) vt[t] = wide_vread<128>(vlane, t);
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 st[2][NT];
+    f16x8 pt[NT];
+    float pr[NT][8], mc[NT];
+#pragma unroll
+    for (int k = 0; k < 8 * NT; ++k) {
+        const int ks = k / (2 * NT), h = (k / NT) % 2, n = k % NT;
+        st[h][n] = mfma16x16x32(kop[h][ks], qv[n][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[h][n]);
+        const int np = k / 8, e = k % 8;
+        if (e == 0) mc[np] = (acc.m[np] == neg_inf()) ? 0.0f : acc.m[np] * c2;
+        pr[np][e] = fast_exp2(fmaf(ps.sv[np][e], c2, -mc[np]));
+        if (e & 1) {
+            pt[np][e - 1] = (_Float16)pr[np][e - 1];
+            pt[np][e] = (_Float16)pr[np][e];
+        }
+        if (e == 7)
+            acc.l[np] += ((pr[np][0] + pr[np][1]) + (pr[np][2] + pr[np][3])) +
+                         ((pr[np][4] + pr[np][5]) + (pr[np][6] + pr[np][7]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    bool need = false;
+    float m01[NT], m2[NT], mx[NT];
+#pragma unroll
+    for (int k = 0; k < 8 * NT; ++k) {
+        const int n = k / 8, t = k % 8;
+        acc.o[t][n] = mfma16x16x32(as_f16x8(vt[t]), pt[n], acc.o[t][n]);
+        if (t < 3) {
+            // cells e = 3t .. 3t+2 (t = 2: e = 6, 7) of row tile n
+#pragma unroll
+            for (int e = 3 * t; e < 3 * t + 3 && e < 8; ++e) {
+                float x = st[e >> 2][n][e & 3];
+                if (MASKED && c0n + 16 * (e >> 2) + 4 * c + (e & 3) >= ri.vis[n]) x = neg_inf();
+                ps.sv[n][e] = x;
+            }
+            if (t == 0) m01[n] = max3f(ps.sv[n][0], ps.sv[n][1], ps.sv[n][2]);
+            if (t == 1) m2[n] = max3f(ps.sv[n][3], ps.sv[n][4], ps.sv[n][5]);
+            if (t == 2) mx[n] = max3f(m01[n], m2[n], max2f(ps.sv[n][6], ps.sv[n][7]));
+        } else if (t == 3) {
+            auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx[n]), __float_as_uint(mx[n]), false, false);
+            mx[n] = max2f(__uint_as_float(a[0]), __uint_as_float(a[1]));
+        } else if (t == 4) {
+            auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx[n]), __float_as_uint(mx[n]), false, false);
+            ps.mx[n] = max2f(__uint_as_float(b[0]), __uint_as_float(b[1]));
+        } else if (t == 5) {
+            need |= ps.mx[n] > acc.m[n] + thr;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return need;
+}
+
 // Normalised rows (O layout of the 32-cell kernel).
 template <int NT, int DT>
 __device__ __forceinline__ void write_rows_wide(const FaArgs& a, const Acc<NT, DT>& acc, int n0, int s, int g, int R,
@@ -1055,7 +1236,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     constexpr int SLOT16 = W::SLOT / 16;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: row group and lane in SGPRs
     const int rg = w / TL;
     const int tl = w % TL;
     const int r = lane & 15;
@@ -1113,14 +1294,16 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
     const int t0 = tb + tl;
     const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
     const int n_iter = (te - tb + TL - 1) / TL;
-    u32x4* ring = sh.ring + (size_t)tl * wide_slots<D, TL>() * SLOT16;
+    constexpr bool GEN = MODE != MODE_FAST;
+    constexpr bool PIPE = wide_pipelined<MODE, D, TL>();
+    constexpr int NS = wide_slots<D, TL>();  // slots of the plain ring
+    u32x4* ring = sh.ring + (size_t)tl * (wide_lane_ring_bytes<D, TL, GEN>() / 16);
     const uint32_t ring_base = lds_addr(ring);
 
     // explicit masks: rows j < 32 of a stream's mask; an empty resource (every load returns 0)
     // when the mask is read from global memory instead, so that every issue has the same loads
-    constexpr bool GEN = MODE != MODE_FAST;
     const buf_rsrc mrs = make_rsrc_uniform(mrow, GEN && a.mask_stage ? a.m_bytes : 0u);
-    const uint32_t mring_base = lds_addr(sh.mring) + (uint32_t)tl * wide_slots<D, TL>() * kMaskTile;
+    const uint32_t mring_base = lds_addr(sh.mring) + (uint32_t)tl * NS * kMaskTile;
     PageIds pages = page_ids_load(a, s, (t0 * kWide) >> 8);
     auto issue = [&](int i, int slot) {
         // uniform over the wave (the compiler cannot tell): scalar page and span arithmetic
@@ -1181,10 +1364,53 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
         // flight.  Each issue is one batch of LPW loads per wave, and the ring loads are the
         // only loads a wave has in flight in the step loop, so vmcnt counts the batches issued
         // after step i.
-        constexpr int NS = wide_slots<D, TL>();
+        // (the pipelined loop's ring and its pre-loop loads are set up below)
+        constexpr int KB = 32 * W::ROW;  // bytes of one step's K (or V) rows
+        const uint32_t vring_base = ring_base + kPipeK * KB;
+        auto issue_k = [&](int j) {  // row group 0: K of step j into K slot j % kPipeK
+            const uint32_t c0 = (uint32_t)(t0 + j * TL) * kWide;
+            const int page = (int)c0 < sd.nc ? page_id(pages, a, s, (int)(c0 >> 8)) : 0;
+            const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, (int)c0, sd.nc, W::ROW, page);
+            const buf_rsrc krs = make_rsrc_uniform(ksp.p, ksp.bytes);
+            const uint32_t pos = (uint32_t)lane % W::CPR;
+            uint32_t o8[8];
 #pragma unroll
-        for (int q = 0; q < NS - 1; ++q)
-            if (q < n_my) issue(q, q);
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t cell = W::CPL * u + (uint32_t)lane / W::CPR;
+                o8[u] = cell * knb + 16u * (pos ^ (cell & 15u));
+            }
+            dma16x8_to_lds(krs, o8, ring_base + (uint32_t)(j % kPipeK) * KB);
+        };
+        auto issue_v = [&](int j) {  // row group 1: V of step j into V slot j % kPipeV
+            const uint32_t c0 = (uint32_t)(t0 + j * TL) * kWide;
+            const int page = (int)c0 < sd.nc ? page_id(pages, a, s, (int)(c0 >> 8)) : 0;
+            const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, (int)c0, sd.nc, W::ROW, page);
+            const buf_rsrc vrs = make_rsrc_uniform(vsp.p, vsp.bytes);
+            const uint32_t pos = (uint32_t)lane % W::CPR;
+            uint32_t o8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t cell = W::CPL * u + (uint32_t)lane / W::CPR;
+                o8[u] = cell * vnb + 32u * ((pos >> 1) ^ (cell & 7u)) + 16u * (pos & 1u);
+            }
+            dma16x8_to_lds(vrs, o8, vring_base + (uint32_t)(j % kPipeV) * KB);
+        };
+        if constexpr (PIPE) {
+            static_assert(RS == 2 && W::LOADS == 8, "the pipelined ring: one K and one V loader wave per lane");
+            if (rg == 0) {
+#pragma unroll
+                for (int q = 0; q < kPipeK; ++q)
+                    if (q < n_my) issue_k(q);
+            } else {
+#pragma unroll
+                for (int q = 0; q < kPipeV - 1; ++q)
+                    if (q < n_my) issue_v(q);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < NS - 1; ++q)
+                if (q < n_my) issue(q, q);
+        }
         // The Q^T operands' loads end here, once per piece: left for the loop, the compiler's
         // wait for them lands in the step body (before an LDS read that reuses a register),
         // where it would drain the ring's DMA loads every step.
@@ -1192,6 +1418,87 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
         for (int n = 0; n < NTW; ++n)
 #pragma unroll
             for (int ks = 0; ks < W::KS; ++ks) asm volatile("" ::"v"(qv[n][ks]));
+        if constexpr (PIPE) {
+            // Iteration i reads K of step i+1 and V of step i.  Row group 0 keeps K of steps
+            // up to i+kPipeK-1 issued and waits for K of step i+1 before the iteration's barrier,
+            // then issues step i+kPipeK into the slot of step i (read in iteration i-1); row
+            // group 1 keeps V up to step i+kPipeV-2 issued, waits for V of step i, then issues
+            // step i+kPipeV-1 into the slot of step i-1.  Each wave counts only its own loads.
+            auto wait_later = [&](int later) {  // own batches still in flight: `later`
+                if (later >= 4) wait_vmcnt<4 * LPW>();
+                else if (later == 3) wait_vmcnt<3 * LPW>();
+                else if (later == 2) wait_vmcnt<2 * LPW>();
+                else if (later == 1) wait_vmcnt<LPW>();
+                else wait_vmcnt<0>();
+            };
+            auto wait_k = [&](int j) { wait_later(max(min(j + kPipeK - 2, n_my - 1) - j, 0)); };  // K of step j
+            auto wait_v = [&](int j) { wait_later(max(min(j + kPipeV - 2, n_my - 1) - j, 0)); };  // V of step j
+            auto kslot = [&](int j) { return ring + (size_t)(j % kPipeK) * (KB / 16); };
+            auto vlane = [&](int j) { return vring_base + (uint32_t)(j % kPipeV) * KB + vrow; };
+            const float c2 = a.scale_log2;
+            const float thr = kLazyLog2 / a.scale_log2;
+            PipeState<NTW> ps;
+            bool need = false;
+            if (n_iter > 0) {
+                if (rg == 0 && n_my > 0) wait_later(max(min(kPipeK - 1, n_my - 1), 0));
+                __syncthreads();
+                if (n_my > 0) {
+                    f32x4 st[2][NTW];
+                    pipe_scores(kslot(0), kofs, qv, st);
+                    need = n_plain > 0 ? pipe_max<NTW, false>(acc, st, ps, t0 * kWide, ri, thr, lane)
+                                       : pipe_max<NTW, true>(acc, st, ps, t0 * kWide, ri, thr, lane);
+                }
+            }
+            auto head = [&](int i) {
+                if (rg == 0) {
+                    if (i + 1 < n_my) wait_k(i + 1);
+                } else if (i < n_my) {
+                    wait_v(i);
+                }
+                __syncthreads();
+                if (rg == 0) {
+                    if (i + kPipeK < n_my) issue_k(i + kPipeK);
+                } else if (i + kPipeV - 1 < n_my) {
+                    issue_v(i + kPipeV - 1);
+                }
+                if (i < n_my && __builtin_amdgcn_ballot_w64(need) != 0) pipe_rescale(acc, ps, thr, c2);
+            };
+            auto body = [&](int i, auto masked) {
+                need = pipe_iteration<NTW, decltype(masked)::value>(acc, ps, kslot(i + 1), vlane(i), kofs, qv,
+                                                                     (t0 + (i + 1) * TL) * kWide, ri, thr, c2, lane);
+            };
+            auto last = [&](int i) {  // PV of a step without a next one
+                u32x4 vt[8];
+                f16x8 pt[NTW];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) vt[t] = wide_vread<128>(vlane(i), t);
+                pipe_probs(acc, ps, c2, pt);
+                pipe_pv(acc, vt, pt);
+            };
+            int i = 0;
+            // next step unmasked (every lane has it)
+#pragma unroll 1
+            for (; i < n_plain - 1; ++i) {
+                head(i);
+                body(i, std::false_type{});
+            }
+#pragma unroll 1
+            for (; i < n_iter - 1; ++i) {
+                head(i);
+                if (i + 1 < n_my) body(i, std::true_type{});
+                else if (i < n_my) last(i);
+            }
+            if (n_iter > 0) {
+                // V of the last step (nothing is issued any more)
+                const int il = n_iter - 1;
+                if (rg == 1 && il < n_my) wait_v(il);
+                __syncthreads();
+                if (il < n_my) {
+                    if (__builtin_amdgcn_ballot_w64(need) != 0) pipe_rescale(acc, ps, thr, c2);
+                    last(il);
+                }
+            }
+        } else {
         // Score phase of step i after its data has landed; returns whether a row's exponent
         // reference moves (uniform over the wave).  Every wave passes the barrier of every step.
         auto scores = [&](int i, auto masked, WideStep<NTW, D>& ws) -> bool {
@@ -1224,6 +1531,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
         };
         run(n_plain, std::false_type{});
         run(n_iter, std::true_type{});
+        }
     }
     acc_settle(acc.o);  // the asm MFMAs' results before the merge reads them
 
@@ -1753,10 +2061,29 @@ inline bool slot_fits(const FaArgs& a, int rows, int D) {
     return (int64_t)rows * (D / 2 + 2) <= a.slot_floats;
 }
 
+// Head-aligned split: the kv-heads of a cell range go to Hkv work-groups of one XCD that start
+// together, so one XCD requests a cell's whole row (all heads) at about the same time.  For
+// q8_0 (34*D/32 bytes per head row) neighbouring heads share L2 lines, which are then fetched
+// from HBM once, not once per XCD; for f16 the four 256-byte slices of a row are requested
+// together (measured 2-3% faster on the 32 x 16 verify).  The grid becomes a multiple of 8 * Hkv.
+inline FaArgs head_split_args(const FaArgs& a) {
+    FaArgs b = a;
+    const int64_t unit = (int64_t)kXcds * a.Hkv;
+    if (a.P >= unit) {
+        b.P = (int)(a.P / unit * unit);
+        b.head_split = 1;
+        b.piece_stride = a.Hkv;
+        b.xcd_remap = 1;
+    }
+    return b;
+}
+
 // FAST_BUILT: whether the launch shape has a fast-mode kernel (the 32-cell kernel takes f16
 // explicit-mask and softcap calls of up to 48 rows as well, whose fast calls run decode_d128).
 template <int NTW, int RS, int D, bool FAST_BUILT = true>
-hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream) {
+hipError_t launch_wide(const FaArgs& a_in, int mode, int causal, hipStream_t stream) {
+    // the pipelined fast kernel (128-dim heads) with the head-aligned split
+    const FaArgs a = (D == 128 && mode == MODE_FAST) ? head_split_args(a_in) : a_in;
     if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(RS * wide_lanes<RS, D>() * 64);
     if (mode == MODE_GENERIC)
@@ -1771,22 +2098,6 @@ hipError_t launch_wide(const FaArgs& a, int mode, int causal, hipStream_t stream
     if (e != hipSuccess) return e;
     launch_merge<D>(a, NTW * RS * 16, stream);
     return hipGetLastError();
-}
-
-// q8_0 rows of one cell are 34*D/32 bytes per head, so neighbouring heads share L2 lines.
-// The kv-heads of a cell range go to Hkv work-groups of one XCD that start together, which
-// fetch each shared line from HBM once (split over (stream, head) segments, two XCDs' L2s
-// each fetch the shared lines); the grid becomes a multiple of 8 * Hkv.
-inline FaArgs head_split_args(const FaArgs& a) {
-    FaArgs b = a;
-    const int64_t unit = (int64_t)kXcds * a.Hkv;
-    if (a.P >= unit) {
-        b.P = (int)(a.P / unit * unit);
-        b.head_split = 1;
-        b.piece_stride = a.Hkv;
-        b.xcd_remap = 1;
-    }
-    return b;
 }
 
 template <int NTW, int RS>

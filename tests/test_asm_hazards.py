@@ -143,7 +143,7 @@ def decode_asm(tmp_path_factory):
         hipcc = build._hipcc()
     except RuntimeError:
         pytest.skip("hipcc not available")
-    flags = [f for f in build.HIP_FLAGS if f != "-fPIC"]
+    flags = [f for f in build.flags_for("fa_decode.hip") if f != "-fPIC"]
     out = tmp_path_factory.mktemp("asm") / "fa_decode.s"
     proc = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", str(out), str(build.CSRC / "fa_decode.hip")],
                           stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
