@@ -620,9 +620,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
 #pragma unroll 1
     for (int i = 0; i < n_my; ++i) {
         const int ahead = n_my - 1 - i;  // own tiles issued after tile i
-        if (NSLOT == 3 && ahead >= 2) wait_vmcnt<2 * DMA>();
-        else if (ahead >= 1) wait_vmcnt<DMA>();
-        else wait_vmcnt<0>();
+        wait_batches<DMA, NSLOT - 1>(ahead);
         step(i, [&] {
             wait_lgkmcnt0();
             if (i + NSLOT < n_my) issue(i + NSLOT);
@@ -1424,13 +1422,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
             // then issues step i+kPipeK into the slot of step i (read in iteration i-1); row
             // group 1 keeps V up to step i+kPipeV-2 issued, waits for V of step i, then issues
             // step i+kPipeV-1 into the slot of step i-1.  Each wave counts only its own loads.
-            auto wait_later = [&](int later) {  // own batches still in flight: `later`
-                if (later >= 4) wait_vmcnt<4 * LPW>();
-                else if (later == 3) wait_vmcnt<3 * LPW>();
-                else if (later == 2) wait_vmcnt<2 * LPW>();
-                else if (later == 1) wait_vmcnt<LPW>();
-                else wait_vmcnt<0>();
-            };
+            auto wait_later = [&](int later) { wait_batches<LPW, kPipeK - 1>(later); };  // own batches in flight
             auto wait_k = [&](int j) { wait_later(max(min(j + kPipeK - 2, n_my - 1) - j, 0)); };  // K of step j
             auto wait_v = [&](int j) { wait_later(max(min(j + kPipeV - 2, n_my - 1) - j, 0)); };  // V of step j
             auto kslot = [&](int j) { return ring + (size_t)(j % kPipeK) * (KB / 16); };
@@ -1502,10 +1494,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
         // Score phase of step i after its data has landed; returns whether a row's exponent
         // reference moves (uniform over the wave).  Every wave passes the barrier of every step.
         auto scores = [&](int i, auto masked, WideStep<NTW, D>& ws) -> bool {
-            const int later = min(max(n_my - 1 - i, 0), NS - 2);  // steps issued after step i
-            if (later >= 2) wait_vmcnt<2 * LPW>();
-            else if (later == 1) wait_vmcnt<LPW>();
-            else wait_vmcnt<0>();
+            wait_batches<LPW, NS - 2>(n_my - 1 - i);  // own batches of the steps issued after step i
             __syncthreads();
             if (i + NS - 1 < n_my) issue(i + NS - 1, (i + NS - 1) % NS);
             if (!decltype(masked)::value || i < n_my) {
@@ -1729,10 +1718,7 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
         // batches issued after it may stay in flight.
         // own loads of step j landed, with steps 0 .. issued-1 issued so far
         auto wait_for = [&](int j, int issued) {
-            const int later = max(min(issued, n_my) - (j + 1), 0);
-            if (later >= 2) wait_vmcnt<2 * LPW>();
-            else if (later == 1) wait_vmcnt<LPW>();
-            else wait_vmcnt<0>();
+            wait_batches<LPW, NSQ - 2>(min(issued, n_my) - (j + 1));
         };
 #pragma unroll
         for (int q = 0; q < NSQ - 1; ++q)
@@ -1801,11 +1787,14 @@ struct Partition {
     int p_log;
 };
 
+// HS: the kernel may run a head-aligned split (a.head_split); kernels launched without one
+// leave the branch out (it costs registers in the tile loop of the 16-cell kernel).
+template <bool HS>
 __device__ __forceinline__ bool partition(const FaArgs& a, const int* ps, int b, Partition& pt) {
     // logical index: with the remap, consecutive tile ranges land on one XCD (work-groups
     // are dealt round-robin over the XCDs)
     pt.p_log = a.xcd_remap ? (b % kXcds) * (a.P / kXcds) + b / kXcds : b;
-    if (a.head_split) {
+    if (HS && a.head_split) {
         // ranges over the streams' cost line, each taken by the Hkv work-groups Hkv*q .. +Hkv-1
         pt.T = ps[a.S];
         const int64_t Q = a.P / a.Hkv;
@@ -1825,12 +1814,12 @@ __device__ __forceinline__ bool partition(const FaArgs& a, const int* ps, int b,
 }
 
 // Runs fn(piece) for every piece of this work-group's tile range, in order.
-template <typename F>
+template <bool HS, typename F>
 __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F&& fn) {
     Partition pt;
-    if (!partition(a, ps, blockIdx.x, pt)) return;
+    if (!partition<HS>(a, ps, blockIdx.x, pt)) return;
     const int64_t Hkv = a.Hkv;
-    if (a.head_split) {
+    if (HS && a.head_split) {
         // this work-group's kv-head over the cells of its range of every stream it touches;
         // piece q of segment k sits in slot k + q * Hkv
         const int g = (int)(pt.p_log % Hkv);
@@ -1908,7 +1897,7 @@ decode_d128(FaArgs a, int causal) {
     __shared__ DecodeLds<NTW, KV> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
     __syncthreads();
-    for_each_piece(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, KV, MODE>(a, sh, causal, pc); });
+    for_each_piece<false>(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, KV, MODE>(a, sh, causal, pc); });
 }
 
 template <int NTW, int RS, int MODE, int D>
@@ -1917,7 +1906,7 @@ void decode_wide(FaArgs a, int causal) {
     __shared__ WideLds<NTW, RS, D, MODE != MODE_FAST> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
-    for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
+    for_each_piece<MODE == MODE_FAST && D == 128>(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
 }
 
 template <int NTW, int RS, int MODE>
@@ -1926,7 +1915,7 @@ void decode_wide_q8(FaArgs a, int causal) {
     __shared__ WideQ8Lds<NTW, RS, MODE != MODE_FAST> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
-    for_each_piece(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide_q8<NTW, RS, MODE>(a, sh, causal, pc); });
+    for_each_piece<true>(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide_q8<NTW, RS, MODE>(a, sh, causal, pc); });
 }
 
 // Combines the pieces of every segment that more than one work-group touched, for segments of
@@ -2123,8 +2112,9 @@ hipError_t launch_nt(const FaArgs& a, int mode, int causal, hipStream_t stream) 
     const dim3 grid(a.P), block(Shape<KV>::waves * 64);
     if (mode == MODE_FAST) {
         hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_FAST>), grid, block, 0, stream, a, causal);
-    } else if constexpr (KV == SIXI_TYPE_Q8_0) {
-        // (f16 explicit-mask and softcap calls run the 32-cell kernel)
+    } else if constexpr (KV == SIXI_TYPE_Q8_0 && NTW == 1) {
+        // (f16 explicit-mask and softcap calls, and q8_0 ones of more than 16 rows, run the
+        // 32-cell kernels)
         hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
     } else {
         return hipErrorNotSupported;
@@ -2194,8 +2184,10 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
     if (kv_type == SIXI_TYPE_Q8_0) {
         switch (row_tiles) {
             case 1: return launch_nt<1, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
-            case 2: return launch_nt<2, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
-            case 3: return launch_nt<3, SIXI_TYPE_Q8_0>(a, mode, causal, stream);
+            case 2: return mode == MODE_FAST ? launch_nt<2, SIXI_TYPE_Q8_0>(a, mode, causal, stream)
+                                             : launch_wide_q8<2, 1>(a, mode, causal, stream);
+            case 3: return mode == MODE_FAST ? launch_nt<3, SIXI_TYPE_Q8_0>(a, mode, causal, stream)
+                                             : launch_wide_q8<3, 1>(a, mode, causal, stream);
             case 4: return launch_wide_q8<kWide64.ntw, kWide64.rs>(a, mode, causal, stream);
             case 6: return launch_wide_q8<kWide96.ntw, kWide96.rs>(a, mode, causal, stream);
             default: return hipErrorNotSupported;

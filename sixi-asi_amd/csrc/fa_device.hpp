@@ -257,7 +257,27 @@ __device__ __forceinline__ void dma4x8_to_lds(buf_rsrc rs, const uint32_t (&v)[8
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 63, "vmcnt counts at most 63 loads");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Waits until at most min(later, KMAX) batches of PER loads each are in flight (a ring's own
+// loads issued after the one needed; KMAX: the most the ring can have).
+template <int PER, int KMAX>
+__device__ __forceinline__ void wait_batches(int later) {
+    static_assert(PER * KMAX <= 63, "vmcnt counts at most 63 loads");
+    if constexpr (KMAX >= 4) {
+        if (later >= 4) return wait_vmcnt<4 * PER>();
+    }
+    if constexpr (KMAX >= 3) {
+        if (later >= 3) return wait_vmcnt<3 * PER>();
+    }
+    if constexpr (KMAX >= 2) {
+        if (later >= 2) return wait_vmcnt<2 * PER>();
+    }
+    if constexpr (KMAX >= 1) {
+        if (later >= 1) return wait_vmcnt<PER>();
+    }
+    wait_vmcnt<0>();
 }
 __device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 

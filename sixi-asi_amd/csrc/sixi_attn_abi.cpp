@@ -207,8 +207,9 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
-    // q8_0 KV at 128-dim heads runs the split-K kernels (up to 48 rows the 16-cell kernel,
-    // 49..96 the 32-cell kernel) in one launch that reads the KV once
+    // q8_0 KV at 128-dim heads runs the split-K kernels in one launch that reads the KV once:
+    // the 16-cell kernel up to 48 rows (with a mask or softcap: up to 16), the 32-cell q8_0
+    // kernel beyond
     pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
         if (D == 128 && pl.splitk) {

@@ -10,7 +10,10 @@ path (branches followed) from each asm MFMA for WAIT wait states.
 
 The same assembly is checked for the other blind spot of inline asm: the LDS-DMA loads of
 the 32-cell kernel's ring are invisible to the compiler's wait insertion, so a wait it places
-in the step loop for a load of its own drains the whole ring every step.
+in the step loop for a load of its own drains the whole ring every step.  And for register
+spills: no kernel may touch scratch memory inside a step loop (the innermost loops that
+issue MFMAs); the one kernel with a spill (the q8_0 16-cell kernel at 48 rows, 36 bytes)
+keeps it in the piece's set-up and epilogue.
 """
 import importlib.util
 import pathlib
@@ -181,3 +184,36 @@ def test_wide_decode_step_loops_do_not_drain_the_dma_ring(decode_asm):
     assert len(found) >= 8, found
     bad = {k: v for k, v in found.items() if v}
     assert not bad, bad
+
+
+def scratch_in_step_loops(asm):
+    """(function, instruction) for every scratch access inside a step loop: a loop (label ..
+    backward branch) that issues MFMAs and contains no smaller loop that does."""
+    found = []
+    for name, lines in _functions(asm):
+        labels, ins = _parse(lines)
+        ops = [t for t, _ in ins]
+        loops = []
+        for k, t in enumerate(ops):
+            parts = t.split()
+            if (parts[0].startswith("s_cbranch") or parts[0] == "s_branch") and len(parts) > 1:
+                a = labels.get(parts[1])
+                if a is not None and a < k and any(u.startswith("v_mfma") for u in ops[a:k + 1]):
+                    loops.append((a, k))
+        steps = [(a, b) for a, b in loops
+                 if not any((c, d) != (a, b) and a <= c and d <= b for c, d in loops)]
+        for a, b in steps:
+            found += [(name, u) for u in ops[a:b + 1] if u.startswith("scratch_")]
+    return found
+
+
+def test_checker_finds_scratch_in_a_step_loop():
+    toy = ("\t.type\t_Zk,@function\n_Zk:\n.LBB0_1:\n\tv_mfma_f32_16x16x32_f16 v[0:3], v[4:7], v[8:11], v[0:3]\n"
+           "\t{mid}\n\ts_cbranch_scc1 .LBB0_1\n\tscratch_load_dword v1, off, off\n\ts_endpgm\n.Lfunc_end0:\n")
+    assert len(scratch_in_step_loops(toy.format(mid="scratch_store_dword off, v1, off"))) == 1
+    assert scratch_in_step_loops(toy.format(mid="v_mov_b32 v1, v2")) == []
+
+
+def test_decode_kernels_touch_no_scratch_in_step_loops(decode_asm):
+    bad = scratch_in_step_loops(decode_asm)
+    assert not bad, f"{len(bad)} scratch accesses in step loops, first: {bad[:3]}"
