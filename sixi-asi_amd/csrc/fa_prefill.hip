@@ -11,10 +11,12 @@
 //   K   [64 cells][16 chunks of 16 B], chunk q of cell c stored at slot q ^ (c & 15) (each
 //       lane fetches the global chunk that lands in its slot), read back conflict-free as
 //       MFMA A operands;
-//   V   [64 cells][8 chunks of 32 B], chunk q of cell c stored at position q ^ (c & 7); the
+//   V   [64 cells][8 chunks of 32 B], chunk q of cell c stored at position q ^ 2(c & 3); the
 //       V^T A operands come out of it with ds_read_b64_tr_b16 (within each 16-lane group,
 //       lane i receives element i%4 of the 8 bytes addressed by lane 4e + i/4), so no
-//       transpose runs through registers.
+//       transpose runs through registers.  The 32 lanes of a read pass address 4 cells
+//       (c & 3 = 0..3) x 2 chunks: the swizzle spreads them over all 8 positions of a row,
+//       i.e. 256 distinct bytes, conflict-free (with c & 7 they covered 4 positions).
 //   S^T = K Q^T on v_mfma_f32_32x32x16_f16: A = 32 cells x 16 dims from LDS, B = Q^T held in
 //       registers for the whole work-group (lane l: row l%32, dims 16ks + 8(l/32)..+7);
 //       lane l receives cells 8b + 4(l/32) + e (b, e < 4) of row l%32, so a row's 64 cells
@@ -161,24 +163,23 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     }
     // V staging: wave w's load u fills LDS row CPL(LW w + u) + t/CPR at 16-byte position
     // t%CPR, i.e. 32-byte chunk position (t%CPR)/2 of the row, which holds dims
-    // 16 * (position ^ (row % 8))
+    // 16 * (position ^ 2(row % 4))
     uint32_t vdo[P::LW];
 #pragma unroll
     for (int u = 0; u < P::LW; ++u) {
         const int cell = P::CPL * (P::LW * w + u) + lane / P::CPR;
         const int pos = lane % P::CPR;
-        vdo[u] = (uint32_t)cell * vnb + 32u * (uint32_t)((pos >> 1) ^ (cell & 7)) + 16u * (uint32_t)(pos & 1);
+        vdo[u] = (uint32_t)cell * vnb + 32u * (uint32_t)((pos >> 1) ^ (2 * (cell & 3))) + 16u * (uint32_t)(pos & 1);
     }
     // V^T A operand of (db, kk), half h: lane (G = l/16, q = l%16) addresses cell
-    // 16kk + 8h + 4(G/2) + q/4, dims 32db + 16(G%2) + 4(q%4) .. +3, which sits in chunk
-    // position (2db + G%2) ^ (4(G/2) + q/4).  The row offset has the bits that 64db touches
-    // clear, so the address is (row + 32*((G%2) ^ (4(G/2) + q/4)) + 8(q%4)) ^ 64db +
-    // (16kk + 8h)*ROW.
+    // 16kk + 8h + x, x = 4(G/2) + q/4, dims 32db + 16(G%2) + 4(q%4) .. +3, which sits in chunk
+    // position (2db + G%2) ^ 2(x % 4).  The row offset has the bits that 64db touches clear,
+    // so the address is (row + 32*((G%2) ^ 2(x % 4)) + 8(q%4)) ^ 64db + (16kk + 8h)*ROW.
     uint32_t vtr[P::DB];
     {
         const int G = lane >> 4, q = lane & 15;
         const int x = 4 * (G >> 1) + (q >> 2);
-        const uint32_t base = (uint32_t)x * (uint32_t)P::ROW + 32u * (uint32_t)((G & 1) ^ x) + 8u * (uint32_t)(q & 3);
+        const uint32_t base = (uint32_t)x * (uint32_t)P::ROW + 32u * (uint32_t)((G & 1) ^ (2 * (x & 3))) + 8u * (uint32_t)(q & 3);
 #pragma unroll
         for (int db = 0; db < P::DB; ++db) vtr[db] = lds0 + kVBase + (base ^ (64u * db));
     }
