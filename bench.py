@@ -248,10 +248,13 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
-def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None):
+def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None, explicit_mask=False):
     """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks).
-    kv_type q8_0 runs the same chunks over a q8_0 cache (staged as f16 operands per call)."""
+    kv_type q8_0 runs the same chunks over a q8_0 cache (staged as f16 operands per call);
+    explicit_mask hands the causal mask over as a ggml f16 KQ mask (the ggml hook's path)."""
     import dataclasses
+
+    import torch
 
     from sixi_attn import workloads as wl
 
@@ -263,7 +266,10 @@ def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None):
         if head_dim is not None:
             wp = dataclasses.replace(wp, D=head_dim)
         dp = wl.to_device(wl.make_host(wp))
-        msp, _ = time_calls(fa, wp, dp, steps, warmup)
+        mask = None
+        if explicit_mask:
+            mask = torch.from_numpy(wl.kq_mask(dp["k"].shape[1], wp.n_q, wp.kv_len, wp.q_len)).view(torch.float16).cuda()
+        msp, _ = time_calls(fa, wp, dp, steps, warmup, mask=mask)
         pre.append((wp, msp, ws_bytes(fa, wp, dp)))
         del dp
     flops = sum(wp.flops() for wp, _, _ in pre)
@@ -651,6 +657,10 @@ def main() -> int:
             result["configs"]["prefill_d256"] = {"us_two_chunks": round(ud, 2), "TFLOPs": round(td, 2),
                                                  "workspace_bytes": wsd}
             _log(f"prefill 256-dim heads: {ud:.1f} us for 2 chunks, {td:.1f} TFLOP/s")
+            tm, um, wsm = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), explicit_mask=True)
+            result["configs"]["prefill_explicit_mask"] = {"us_two_chunks": round(um, 2), "TFLOPs": round(tm, 2),
+                                                          "workspace_bytes": wsm}
+            _log(f"prefill with the causal mask as an explicit ggml mask: {um:.1f} us for 2 chunks, {tm:.1f} TFLOP/s")
         except sa.SixiAttnError as e:
             result["prefill_tflops"] = None
             result["prefill_note"] = f"prefill kernel unavailable: {e}"

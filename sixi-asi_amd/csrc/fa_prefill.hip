@@ -28,6 +28,12 @@
 //       reduction index k = 8(l/32) + e stands for cell 8(e/4) + 4(l/32) + e%4 of the step;
 //       the transposed V reads follow the same order.
 // Only tiles that reach past the first row's causal boundary (or the stream's end) mask.
+//
+// Explicit masks without softcap or ALiBi (the ggml hook: MODE_MASK) keep the fast mode's raw
+// units and read the mask from LDS: each wave stages its 32 rows x 64 cells of a tile (4 KB)
+// by LDS-DMA, the next tile's as soon as it has read the current one.  A wave whose 32 rows
+// see none of a tile's cells (a causal mask's upper triangle) skips the tile's MFMAs; a tile
+// whose mask is zero for all of them skips the per-cell work.
 #include <type_traits>
 
 #include "fa_device.hpp"
@@ -49,12 +55,15 @@ struct PfDim {
 };
 constexpr float kLazyLog2 = 8.0f;
 
-enum { MODE_FAST = 0, MODE_GENERIC = 1 };
+enum { MODE_FAST = 0, MODE_GENERIC = 1, MODE_MASK = 2 };
+constexpr int kMaskWave = 32 * kBN * 2;  // bytes of one wave's mask rows of a tile (f16)
 
-template <int D>
+// (128-dim heads with the mask: 80 KB, so two work-groups still share a CU's 160 KB)
+template <int D, bool MASK>
 struct PrefillLds {
     u32x4 k[2][PfDim<D>::TILE / 16];
     u32x4 v[2][PfDim<D>::TILE / 16];
+    u32x4 m[MASK ? 4 * kMaskWave / 16 : 1];  // MASK: wave w's rows at kMaskWave * w
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -68,7 +77,7 @@ template <int MODE, int D>
 __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs a, int causal, int nrb, int n_cu) {
     using P = PfDim<D>;
     constexpr int kKBytes = P::TILE, kVBytes = P::TILE;
-    __shared__ PrefillLds<D> sh;
+    __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -107,6 +116,8 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     const int vis_min = causal ? sd.kl + j0 + 1 : sd.nc;
     const int n_tiles = (vis_max + kBN - 1) / kBN;
     const int t_full = (MODE == MODE_GENERIC) ? 0 : vis_min / kBN;
+    constexpr bool RAW = MODE != MODE_GENERIC;  // scores in raw dot-product units
+    const int t_beg = 0, t_end = n_tiles;  // the tiles walked
 
     // ---- Q^T B operands in registers: lane l -> row j, dims 16ks + 8*hl .. +7 ----
     // (every load issued before any is used; rows past the block read its first row)
@@ -208,21 +219,79 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     float m_ref = neg_inf();  // raw score (FAST) or log2 units (GENERIC)
     float l_sum = 0.0f;
     const float c2 = a.scale_log2;
-    const float thr = (MODE == MODE_FAST) ? kLazyLog2 / c2 : kLazyLog2;
+    const float thr = RAW ? kLazyLog2 / c2 : kLazyLog2;
     const float slope = (MODE == MODE_GENERIC) ? alibi_slope(a, h) : 1.0f;
     const char* mrow = nullptr;
     if (MODE == MODE_GENERIC && a.mask)
         mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3 + (int64_t)min(j, j_last) * a.m_nb1;
     const f32x16 zero16 = {};
 
+    // MODE_MASK: the stream's mask rows through a range-checked resource (rows up to n_q);
+    // wave w's load u stages its rows 8u + l/8, the 16-byte piece at slot l%8 of a row
+    // holding cells 8((l%8) ^ ((row >> 1) & 7)) .. +7 of the tile, so that the 32 lanes of a
+    // read (one row each, same piece) spread over the banks
+    buf_rsrc mrs = make_rsrc(a.q, 0u);  // (empty unless MODE_MASK)
+    uint32_t mdo[4] = {0u, 0u, 0u, 0u};
+    const uint32_t m_lds = lds0 + 4 * kKBytes + (uint32_t)w * kMaskWave;
+    const float inv_scale = 1.0f / a.scale;
+    if constexpr (MODE == MODE_MASK) {
+        mrs = make_rsrc_uniform(a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3, (uint32_t)((int64_t)a.n_q * a.m_nb1));
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = 8 * u + lane / 8;
+            const int jr = min(j0 + 32 * w + r, j_last);
+            mdo[u] = (uint32_t)((int64_t)jr * a.m_nb1) + 16u * (uint32_t)((lane % 8) ^ ((r >> 1) & 7));
+        }
+    }
+    auto issue_mask = [&](int t) {
+        if constexpr (MODE == MODE_MASK) {
+            uint32_t o[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o[u] = mdo[u] + (uint32_t)(t * kBN) * 2u;
+            dma16x4_to_lds(mrs, o, m_lds);
+        }
+    };
+
     // One tile from LDS buffer BUF (compile-time, so every LDS offset is an immediate).
     auto tile = [&](int t, auto BUF, auto MASKED) {
         constexpr int buf = decltype(BUF)::value;
         constexpr bool masked = decltype(MASKED)::value;
-        const bool more = t + 1 < n_tiles;
+        const bool more = t + 1 < t_end;
         if (more) issue_kv(t + 1, buf ^ 1);
         const int c0 = t * kBN;
         const char* kt = lds + buf * kKBytes;
+
+        // MODE_MASK: this wave's mask values of the lane's 32 cells (row rl, cells
+        // 32cb + 8b + 4hl .. +3: piece 4cb + b, half hl), then the next tile's rows into the
+        // same place (once the reads have returned)
+        u32x2 mv[2][4];
+        bool mask_any = false, live = true;
+        if constexpr (MODE == MODE_MASK) {
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    mv[cb][b] = lds_ld8(m_lds + 128u * (uint32_t)rl +
+                                        16u * (uint32_t)((4 * cb + b) ^ ((rl >> 1) & 7)) + 8u * (uint32_t)hl);
+            uint32_t nz = 0, alive = 0;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        nz |= mv[cb][b][e] & 0x7fff7fffu;
+                        // a cell is seen unless its value is -inf (0xfc00) or it lies past the stream
+                        const int cell = c0 + 32 * cb + 8 * b + 4 * hl + 2 * e;
+                        alive |= ((mv[cb][b][e] & 0xffffu) != 0xfc00u && cell < sd.nc) ? 1u : 0u;
+                        alive |= ((mv[cb][b][e] >> 16) != 0xfc00u && cell + 1 < sd.nc) ? 1u : 0u;
+                    }
+            mask_any = __builtin_amdgcn_ballot_w64(nz != 0) != 0;
+            live = __builtin_amdgcn_ballot_w64(row_ok && alive != 0) != 0;
+            wait_lgkmcnt0();
+            if (t + 1 < t_end) issue_mask(t + 1);
+        }
+        if (live) {
 
         // ---- S^T = K Q^T: two 32-cell blocks ----
         // (the MFMA phases run at raised wave priority, so that the SIMD feeds the matrix core of
@@ -261,6 +330,15 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
                         x = neg_inf();
                     }
                     x *= kLog2e;
+                } else if (MODE == MODE_MASK) {
+                    // raw units: s = dot + mask / scale; -inf (or a cell past the stream) skips it
+                    if (mask_any) {
+                        const uint32_t wv = mv[cb][i >> 2][(i & 3) >> 1];
+                        const float m = half_bits_to_float((uint16_t)((i & 1) ? (wv >> 16) : (wv & 0xffffu)));
+                        x = (m == neg_inf() || (masked && cell >= sd.nc)) ? neg_inf() : fmaf(m, inv_scale, x);
+                    } else if (masked && cell >= sd.nc) {
+                        x = neg_inf();
+                    }
                 } else if (masked) {
                     if (cell >= vis) x = neg_inf();
                 }
@@ -281,7 +359,7 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
         if (__builtin_amdgcn_ballot_w64(need) != 0) {
             float alpha = 1.0f;
             if (need) {
-                alpha = fast_exp2((MODE == MODE_FAST) ? (m_ref - mx) * c2 : m_ref - mx);
+                alpha = fast_exp2(RAW ? (m_ref - mx) * c2 : m_ref - mx);
                 m_ref = mx;
             }
             l_sum *= alpha;
@@ -290,7 +368,7 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
         }
 
         // ---- probabilities ----
-        const float mc = (m_ref == neg_inf()) ? 0.0f : ((MODE == MODE_FAST) ? m_ref * c2 : m_ref);
+        const float mc = (m_ref == neg_inf()) ? 0.0f : (RAW ? m_ref * c2 : m_ref);
         // B operands of the four 16-cell steps (f16 pairs by packed RNE conversion) and the
         // row sum of exactly those f16 probabilities, two per v_dot2_f32_f16
         f16x8 pb[4];
@@ -303,7 +381,7 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
                 f32x2 pp;
 #pragma unroll
                 for (int e = 0; e < 2; ++e)
-                    pp[e] = fast_exp2((MODE == MODE_FAST) ? fmaf(st[cb][i + e], c2, -mc) : st[cb][i + e] - mc);
+                    pp[e] = fast_exp2(RAW ? fmaf(st[cb][i + e], c2, -mc) : st[cb][i + e] - mc);
                 const f16x2 ph = __builtin_convertvector(pp, f16x2);
                 pb[2 * cb + (i >> 3)][i & 7] = ph[0];
                 pb[2 * cb + (i >> 3)][(i & 7) + 1] = ph[1];
@@ -314,7 +392,8 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
         // Explicit masks: a cell that none of this wave's 32 rows sees may hold NaN bits, so
         // its V^T entries are zeroed in this wave's operands (0 * NaN must not reach O).
         uint32_t keep[4][4];
-        if (MODE == MODE_GENERIC && a.mask) {
+        const bool use_keep = (MODE == MODE_GENERIC && a.mask) || (MODE == MODE_MASK && mask_any);
+        if (use_keep) {
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
@@ -336,7 +415,7 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
                 const u32x2 lo = ld_tr16(vp);
                 const u32x2 hi = ld_tr16(vp + 8 * P::ROW);
                 u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
-                if (MODE == MODE_GENERIC && a.mask) {
+                if (use_keep) {
 #pragma unroll
                     for (int m2 = 0; m2 < 4; ++m2) vop[m2] &= keep[kk][m2];
                 }
@@ -345,39 +424,41 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
         }
 
         __builtin_amdgcn_s_setprio(0);
-        if (more) wait_vmcnt<0>();  // this wave's share of tile t+1 is in LDS
+        }  // live
+        if (more) wait_vmcnt<0>();  // this wave's share of tile t+1 (and, masked, its mask rows) is in LDS
         __syncthreads();
     };
     // (256-dim heads run every tail tile masked: two bodies per buffer in one loop would merge
     // their accumulator sets, and the registers are all taken; at most one tail tile is
     // unmasked, and the mask passes its cells)
     auto run_tile = [&](int t, auto BUF) {
-        if (D == 128 && MODE == MODE_FAST && t < t_full)
+        if (D == 128 && RAW && t < t_full)
             tile(t, BUF, std::integral_constant<bool, false>{});
         else
             tile(t, BUF, std::integral_constant<bool, true>{});
     };
 
-    // prologue: tile 0 into buffer 0
-    if (n_tiles > 0) {
-        issue_kv(0, 0);
+    // prologue: the first tile into buffer 0
+    if (t_beg < t_end) {
+        issue_kv(t_beg, 0);
+        issue_mask(t_beg);
         wait_vmcnt<0>();
     }
     __syncthreads();
 
     // the unmasked tiles in pairs (buffers 0, 1), then the tail with the masked tiles, so
     // each loop holds one copy of the tile body per buffer
-    const int t_fast = (MODE == MODE_FAST) ? min(t_full, n_tiles) : 0;
-    int t = 0;
+    const int t_fast = RAW ? min(t_full, t_end) : 0;
+    int t = t_beg;
 #pragma unroll 1
     for (; t + 2 <= t_fast; t += 2) {
         tile(t, std::integral_constant<int, 0>{}, std::integral_constant<bool, false>{});
         tile(t + 1, std::integral_constant<int, 1>{}, std::integral_constant<bool, false>{});
     }
 #pragma unroll 1
-    for (; t < n_tiles; t += 2) {
+    for (; t < t_end; t += 2) {
         run_tile(t, std::integral_constant<int, 0>{});
-        if (t + 1 < n_tiles) run_tile(t + 1, std::integral_constant<int, 1>{});
+        if (t + 1 < t_end) run_tile(t + 1, std::integral_constant<int, 1>{});
     }
 
     // ---- normalise and write: lane holds dims 32db + 8b + 4hl .. +3 of row j ----
@@ -405,7 +486,13 @@ hipError_t launch_prefill_d(const FaArgs& a, int mask_mode, hipStream_t stream) 
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
     const int nrb = (a.n_q + kBM - 1) / kBM;
     const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
-    if (generic)
+    // an explicit mask alone, with 16-byte aligned rows that one 32-bit range covers: LDS-staged
+    const bool mask_only = mask_mode == SIXI_MASK_EXPLICIT && a.mask && a.softcap == 0.0f && a.alibi_nlog2 == 0 &&
+                           reinterpret_cast<uintptr_t>(a.mask) % 16 == 0 && a.m_nb1 % 16 == 0 &&
+                           (a.m_ne3 == 1 || a.m_nb3 % 16 == 0) && (int64_t)a.n_q * a.m_nb1 < (int64_t)UINT32_MAX;
+    if (mask_only)
+        hipLaunchKernelGGL((prefill_f16<MODE_MASK, D>), grid, block, 0, stream, a, causal, nrb, a.P);
+    else if (generic)
         hipLaunchKernelGGL((prefill_f16<MODE_GENERIC, D>), grid, block, 0, stream, a, causal, nrb, a.P);
     else
         hipLaunchKernelGGL((prefill_f16<MODE_FAST, D>), grid, block, 0, stream, a, causal, nrb, a.P);

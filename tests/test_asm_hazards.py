@@ -217,3 +217,22 @@ def test_checker_finds_scratch_in_a_step_loop():
 def test_decode_kernels_touch_no_scratch_in_step_loops(decode_asm):
     bad = scratch_in_step_loops(decode_asm)
     assert not bad, f"{len(bad)} scratch accesses in step loops, first: {bad[:3]}"
+
+
+def test_prefill_kernels_touch_no_scratch_in_tile_loops(tmp_path_factory):
+    spec = importlib.util.spec_from_file_location("sixi_build", BUILD)
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    try:
+        hipcc = build._hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    flags = [f for f in build.flags_for("fa_prefill.hip") if f != "-fPIC"]
+    out = tmp_path_factory.mktemp("asm") / "fa_prefill.s"
+    proc = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", str(out), str(build.CSRC / "fa_prefill.hip")],
+                          stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert proc.returncode == 0, proc.stdout[-2000:]
+    asm = out.read_text()
+    assert asm.count("v_mfma") > 0
+    bad = scratch_in_step_loops(asm)
+    assert not bad, f"{len(bad)} scratch accesses in tile loops, first: {bad[:3]}"
