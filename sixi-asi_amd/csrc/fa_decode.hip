@@ -1552,61 +1552,73 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
 // the q8_0 dot type.  With two row groups, row group 0 stages and converts K, row group 1 V;
 // one row group does both.  K and V are read once for all 96 rows (the 16-cell q8_0 kernel
 // holds 48 rows, so such a block would take two launches, each reading the KV).
-constexpr int kQ8StepBytes = 32 * kQ8Row;       // 4352: one step's K (or V) rows
-constexpr int kQ8StepLoads = kQ8StepBytes / 256;  // 17 dword LDS-DMA loads
-static_assert(kQ8StepLoads * 256 == kQ8StepBytes, "a step is a whole number of dword loads");
-constexpr int kQ8Slot = 2 * kQ8StepBytes;       // K + V
+// Per head dim: ROW bytes of a q8_0 head row; a step's rows come in as LOADS LDS-DMA loads of
+// LB bytes per lane (128-dim rows are only 4-byte aligned: dword loads, 17 x 256 B = 4352 B
+// exactly; 256-dim rows are 16-byte aligned: 9 x 1 KB, the last half past the step's 8704 B);
+// TL lanes per work-group (256 dims: one, for LDS).
+template <int D> struct Q8Dim;
+template <> struct Q8Dim<128> { static constexpr int ROW = 136, LB = 4, LOADS = 17, TL = 2; };
+template <> struct Q8Dim<256> { static constexpr int ROW = 272, LB = 16, LOADS = 9, TL = 1; };
+template <int D> constexpr int q8_step_lds() { return Q8Dim<D>::LOADS * 64 * Q8Dim<D>::LB; }  // K (or V) of a step
+template <int D> constexpr int q8_slot_bytes() { return 2 * q8_step_lds<D>(); }              // K + V
+static_assert(q8_step_lds<128>() == 32 * 136 && q8_step_lds<256>() >= 32 * 272, "a step's rows fit its loads");
 template <int RS> constexpr int q8_slots() { return RS == 1 ? 3 : 4; }  // vmcnt holds 2 x 2 x 18 at most
-template <int NTW, int RS, bool GEN>
+template <int NTW, int RS, bool GEN, int D>
 struct alignas(256) WideQ8Lds {
-    static constexpr int TL = 2;
+    static constexpr int TL = Q8Dim<D>::TL;
     union {
         struct {
-            u32x4 f16buf[TL * 2 * WideDim<128>::SLOT / 16];   // two converted steps per lane
-            u32x4 q8ring[TL * q8_slots<RS>() * kQ8Slot / 16];
+            u32x4 f16buf[TL * 2 * WideDim<D>::SLOT / 16];   // two converted steps per lane
+            u32x4 q8ring[TL * q8_slots<RS>() * q8_slot_bytes<D>() / 16];
         } t;
-        MergeBuf<NTW, (RS * TL + 1) / 2, WideDim<128>::DT> mg;
+        MergeBuf<NTW, (RS * TL + 1) / 2, WideDim<D>::DT> mg;
     };
     u32x4 mring[GEN ? TL * q8_slots<RS>() * kMaskTile / 16 : 1];
     StreamTable st;
 };
 
 // Converts the q8_0 rows of one step (K or V, 32 cells) to f16 at `dst` in the f16 kernel's
-// LDS layout: lane (h, x) = (lane / 32, lane % 32) takes block b = 2h + m of cell x in pass
-// m.  Block b starts 34b bytes into a 136-byte row, so all lanes of a pass have the scale in
-// the same half of a dword (no divergent unpacking), and the 64 lanes' dword reads (row
-// stride 34 dwords, h offset 17) hit 64 distinct banks.
-template <bool IS_V, int M>
+// LDS layout: lane (h, x) = (lane / 32, lane % 32) takes block b = (D/64)h + m of cell x in
+// pass m < D/64.  Block b starts 34b bytes into the row (whose length is a multiple of 4), so
+// all lanes of a pass have the scale in the same half of a dword (no divergent unpacking);
+// at 128 dims the 64 lanes' dword reads (row stride 34 dwords, h offset 17) hit 64 banks.
+template <bool IS_V, int M, int D>
 __device__ __forceinline__ void q8_block_to_f16(const uint32_t* src, char* dst, int x, int h) {
-    const int b = 2 * h + M;
+    const int b = (D / 64) * h + M;
     uint16_t d;
     uint32_t w[8];
-    ld_q8_block<M == 1>(src, x * kQ8Row + 34 * b, d, w);
+    ld_q8_block<(M & 1) == 1>(src, x * Q8Dim<D>::ROW + 34 * b, d, w);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const u32x4 f = dequant_q8x8(w[2 * k], w[2 * k + 1], d);
         const int j = 4 * b + k;  // 16-byte chunk: dims 8j .. 8j+7
         const int pos = IS_V ? 32 * ((j >> 1) ^ (x & 7)) + 16 * (j & 1) : 16 * (j ^ (x & 15));
-        *reinterpret_cast<u32x4*>(dst + x * WideDim<128>::ROW + pos) = f;
+        *reinterpret_cast<u32x4*>(dst + x * WideDim<D>::ROW + pos) = f;
     }
 }
 
-template <bool IS_V>
+template <bool IS_V, int D>
 __device__ __forceinline__ void q8_step_to_f16(const uint32_t* src, char* dst, int lane) {
-    q8_block_to_f16<IS_V, 0>(src, dst, lane & 31, lane >> 5);
-    q8_block_to_f16<IS_V, 1>(src, dst, lane & 31, lane >> 5);
+    q8_block_to_f16<IS_V, 0, D>(src, dst, lane & 31, lane >> 5);
+    q8_block_to_f16<IS_V, 1, D>(src, dst, lane & 31, lane >> 5);
+    if constexpr (D == 256) {
+        q8_block_to_f16<IS_V, 2, D>(src, dst, lane & 31, lane >> 5);
+        q8_block_to_f16<IS_V, 3, D>(src, dst, lane & 31, lane >> 5);
+    }
 }
 
-template <int NTW, int RS, int MODE>
-__device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<NTW, RS, MODE != MODE_FAST>& sh,
+template <int NTW, int RS, int MODE, int D>
+__device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<NTW, RS, MODE != MODE_FAST, D>& sh,
                                                      int causal, const Piece& pc) {
-    using W = WideDim<128>;
-    constexpr int TL = 2;
+    using W = WideDim<D>;
+    using Q = Q8Dim<D>;
+    constexpr int TL = Q::TL;
+    constexpr int STEP = q8_step_lds<D>(), SLOTB = q8_slot_bytes<D>();
     constexpr int NSQ = q8_slots<RS>();
     constexpr bool GEN = MODE != MODE_FAST;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int w = tid >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rg = w / TL;
     const int tl = w % TL;
     const int s = pc.s, g = pc.g, tb = pc.tb, te = pc.te;
@@ -1639,15 +1651,16 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
     acc_clear(acc);
 
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
-    // K/V of the piece's steps (same form as the f16 kernel): read offsets t * kv_nb of the
-    // dword t = 64u + lane of a step's rows -- row t / 34, dword t % 34 -- relative to the
-    // step's first cell; row group 0 loads K, row group 1 V (one row group: both)
-    uint32_t ko[kQ8StepLoads], vo[kQ8StepLoads];
+    // K/V of the piece's steps: read offsets of the LB-byte piece t = 64u + lane of a step's
+    // rows -- row t / (ROW/LB), piece t % (ROW/LB) -- relative to the step's first cell; row
+    // group 0 loads K, row group 1 V (one row group: both)
+    constexpr uint32_t PER = Q::ROW / Q::LB;
+    uint32_t ko[Q::LOADS], vo[Q::LOADS];
 #pragma unroll
-    for (int u = 0; u < kQ8StepLoads; ++u) {
+    for (int u = 0; u < Q::LOADS; ++u) {
         const uint32_t t = 64u * u + (uint32_t)lane;
-        ko[u] = (t / (kQ8Row / 4)) * knb + (t % (kQ8Row / 4)) * 4u;
-        vo[u] = (t / (kQ8Row / 4)) * vnb + (t % (kQ8Row / 4)) * 4u;
+        ko[u] = (t / PER) * knb + (t % PER) * (uint32_t)Q::LB;
+        vo[u] = (t / PER) * vnb + (t % PER) * (uint32_t)Q::LB;
     }
     uint32_t kofs[W::KS];
 #pragma unroll
@@ -1658,8 +1671,8 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
     const int n_my = t0 < te ? (te - t0 + TL - 1) / TL : 0;
     const int n_iter = (te - tb + TL - 1) / TL;
     u32x4* f16buf = sh.t.f16buf + (size_t)tl * 2 * (W::SLOT / 16);
-    const uint32_t* q8ring = reinterpret_cast<const uint32_t*>(sh.t.q8ring + (size_t)tl * NSQ * (kQ8Slot / 16));
-    const uint32_t q8_base = lds_addr(sh.t.q8ring) + (uint32_t)tl * NSQ * kQ8Slot;
+    const uint32_t* q8ring = reinterpret_cast<const uint32_t*>(sh.t.q8ring + (size_t)tl * NSQ * (SLOTB / 16));
+    const uint32_t q8_base = lds_addr(sh.t.q8ring) + (uint32_t)tl * NSQ * SLOTB;
 
     const buf_rsrc mrs = make_rsrc_uniform(mrow, GEN && a.mask_stage ? a.m_bytes : 0u);
     const uint32_t mring_base = lds_addr(sh.mring) + (uint32_t)tl * NSQ * kMaskTile;
@@ -1667,7 +1680,7 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
     auto issue = [&](int i) {
         const int slot = i % NSQ;
         const uint32_t c0 = (uint32_t)(t0 + i * TL) * kWide;
-        const uint32_t base = q8_base + (uint32_t)slot * kQ8Slot;
+        const uint32_t base = q8_base + (uint32_t)slot * SLOTB;
         const int page = (int)c0 < sd.nc ? page_id(pages, a, s, (int)(c0 >> 8)) : 0;
         if constexpr (GEN) {
 #pragma unroll
@@ -1679,37 +1692,38 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
                 }
             }
         }
+        auto rows = [&](const buf_rsrc& rs, const uint32_t (&o)[Q::LOADS], uint32_t dst) {
+            uint32_t o8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o8[u] = o[u];
+            if constexpr (Q::LB == 4) {
+                uint32_t o9[9];
+#pragma unroll
+                for (int u = 0; u < 9; ++u) o9[u] = o[8 + u];
+                dma4x8_to_lds(rs, o8, dst);
+                dma4x9_to_lds(rs, o9, dst + 8 * 256);
+            } else {
+                dma16x8_to_lds(rs, o8, dst);
+                dma16x1_to_lds(rs, o[8], dst + 8 * 1024);
+            }
+        };
         if (rg == 0) {
-            const KvSpan sp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, (int)c0, sd.nc, kQ8Row, page);
-            const buf_rsrc rs = make_rsrc_uniform(sp.p, sp.bytes);
-            uint32_t o8[8], o9[9];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) o8[u] = ko[u];
-#pragma unroll
-            for (int u = 0; u < 9; ++u) o9[u] = ko[8 + u];
-            dma4x8_to_lds(rs, o8, base);
-            dma4x9_to_lds(rs, o9, base + 8 * 256);
+            const KvSpan sp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, (int)c0, sd.nc, Q::ROW, page);
+            rows(make_rsrc_uniform(sp.p, sp.bytes), ko, base);
         }
         if (rg == (RS == 1 ? 0 : 1)) {
-            const KvSpan sp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, (int)c0, sd.nc, kQ8Row, page);
-            const buf_rsrc rs = make_rsrc_uniform(sp.p, sp.bytes);
-            uint32_t o8[8], o9[9];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) o8[u] = vo[u];
-#pragma unroll
-            for (int u = 0; u < 9; ++u) o9[u] = vo[8 + u];
-            dma4x8_to_lds(rs, o8, base + kQ8StepBytes);
-            dma4x9_to_lds(rs, o9, base + kQ8StepBytes + 8 * 256);
+            const KvSpan sp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, (int)c0, sd.nc, Q::ROW, page);
+            rows(make_rsrc_uniform(sp.p, sp.bytes), vo, base + STEP);
         }
     };
     // step i's q8_0 rows -> f16 buffer i % 2
     auto convert = [&](int i) {
-        const uint32_t* src = q8ring + (size_t)(i % NSQ) * (kQ8Slot / 4);
+        const uint32_t* src = q8ring + (size_t)(i % NSQ) * (SLOTB / 4);
         char* dst = reinterpret_cast<char*>(f16buf + (size_t)(i & 1) * (W::SLOT / 16));
-        if (rg == 0) q8_step_to_f16<false>(src, dst, lane);
-        if (rg == (RS == 1 ? 0 : 1)) q8_step_to_f16<true>(src + kQ8StepBytes / 4, dst + 32 * W::ROW, lane);
+        if (rg == 0) q8_step_to_f16<false, D>(src, dst, lane);
+        if (rg == (RS == 1 ? 0 : 1)) q8_step_to_f16<true, D>(src + STEP / 4, dst + 32 * W::ROW, lane);
     };
-    constexpr int LPW = (RS == 1 ? 2 : 1) * (kQ8StepLoads + (GEN ? 1 : 0));
+    constexpr int LPW = (RS == 1 ? 2 : 1) * (Q::LOADS + (GEN ? 1 : 0));
     const int n_plain = min(max((t_full - tb) / TL, 0), (te - tb) / TL);
     {
         // Issue order: steps 0 .. NSQ-2 up front, then step i+NSQ-1 after the barrier of step i
@@ -1730,7 +1744,7 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
         if (n_my > 0) wait_for(0, NSQ - 1);
         __syncthreads();
         if (n_my > 0) convert(0);
-        auto scores = [&](int i, auto masked, WideStep<NTW, 128>& ws) -> bool {
+        auto scores = [&](int i, auto masked, WideStep<NTW, D>& ws) -> bool {
             if (i + 1 < n_my) wait_for(i + 1, i + NSQ - 1);
             __syncthreads();
             if (i + NSQ - 1 < n_my) issue(i + NSQ - 1);
@@ -1739,23 +1753,23 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
                 const int t = t0 + i * TL;
                 const u32x4* kslot = f16buf + (size_t)(i & 1) * (W::SLOT / 16);
                 const uint32_t vlane = lds_addr(kslot) + 32 * W::ROW + vrow;
-                return wide_scores<NTW, MODE, decltype(masked)::value, 128>(
+                return wide_scores<NTW, MODE, decltype(masked)::value, D>(
                     a, acc, ws, kslot, vlane, kofs, qv, t * kWide, ri, mrow,
                     mring_base + (uint32_t)(i % NSQ) * kMaskTile, sd.nc, lane);
             }
             return false;
         };
-        auto finish = [&](int i, auto masked, const WideStep<NTW, 128>& ws) {
+        auto finish = [&](int i, auto masked, const WideStep<NTW, D>& ws) {
             if (!decltype(masked)::value || i < n_my)
-                wide_pv<NTW, MODE, 128>(a, acc, ws, lds_addr(f16buf + (size_t)(i & 1) * (W::SLOT / 16)) + 32 * W::ROW + vrow,
+                wide_pv<NTW, MODE, D>(a, acc, ws, lds_addr(f16buf + (size_t)(i & 1) * (W::SLOT / 16)) + 32 * W::ROW + vrow,
                                         lane);
         };
         int i = 0;
         auto run = [&](int end, auto masked) {
 #pragma unroll 1
             for (; i < end; ++i) {
-                WideStep<NTW, 128> ws;
-                if (scores(i, masked, ws)) wide_rescale<NTW, MODE, 128>(a, acc, ws);
+                WideStep<NTW, D> ws;
+                if (scores(i, masked, ws)) wide_rescale<NTW, MODE, D>(a, acc, ws);
                 finish(i, masked, ws);
             }
         };
@@ -1897,7 +1911,7 @@ decode_d128(FaArgs a, int causal) {
     __shared__ DecodeLds<NTW, KV> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
     __syncthreads();
-    for_each_piece<false>(a, sh.ps, [&](const Piece& pc) { decode_piece<NTW, KV, MODE>(a, sh, causal, pc); });
+    for_each_piece<false>(a, sh.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece<NTW, KV, MODE>(a, sh, causal, pc); });
 }
 
 template <int NTW, int RS, int MODE, int D>
@@ -1906,16 +1920,16 @@ void decode_wide(FaArgs a, int causal) {
     __shared__ WideLds<NTW, RS, D, MODE != MODE_FAST> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
-    for_each_piece<MODE == MODE_FAST && D == 128>(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
+    for_each_piece<MODE == MODE_FAST && D == 128>(a, sh.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
 }
 
-template <int NTW, int RS, int MODE>
-__global__ __launch_bounds__((RS * 2 * 64), (RS * 2 + 3) / 4)
+template <int NTW, int RS, int MODE, int D>
+__global__ __launch_bounds__((RS * Q8Dim<D>::TL * 64), (RS * Q8Dim<D>::TL + 3) / 4)
 void decode_wide_q8(FaArgs a, int causal) {
-    __shared__ WideQ8Lds<NTW, RS, MODE != MODE_FAST> sh;
+    __shared__ WideQ8Lds<NTW, RS, MODE != MODE_FAST, D> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
-    for_each_piece<true>(a, sh.st.ps, [&](const Piece& pc) { decode_piece_wide_q8<NTW, RS, MODE>(a, sh, causal, pc); });
+    for_each_piece<true>(a, sh.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide_q8<NTW, RS, MODE, D>(a, sh, causal, pc); });
 }
 
 // Combines the pieces of every segment that more than one work-group touched, for segments of
@@ -2089,20 +2103,20 @@ hipError_t launch_wide(const FaArgs& a_in, int mode, int causal, hipStream_t str
     return hipGetLastError();
 }
 
-template <int NTW, int RS>
+template <int NTW, int RS, int D = 128>
 hipError_t launch_wide_q8(const FaArgs& a_in, int mode, int causal, hipStream_t stream) {
     const FaArgs a = head_split_args(a_in);
-    if (!slot_fits(a, NTW * RS * 16, 128)) return hipErrorInvalidValue;
-    const dim3 grid(a.P), block(RS * 2 * 64);
+    if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
+    const dim3 grid(a.P), block(RS * Q8Dim<D>::TL * 64);
     if (mode == MODE_GENERIC)
-        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_GENERIC, D>), grid, block, 0, stream, a, causal);
     else if (mode == MODE_MASK)
-        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_MASK>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_MASK, D>), grid, block, 0, stream, a, causal);
     else
-        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_FAST>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_wide_q8<NTW, RS, MODE_FAST, D>), grid, block, 0, stream, a, causal);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_merge<128>(a, NTW * RS * 16, stream);
+    launch_merge<D>(a, NTW * RS * 16, stream);
     return hipGetLastError();
 }
 
@@ -2147,6 +2161,17 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
                                 ? MODE_MASK : MODE_GENERIC)
                          : MODE_FAST;
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
+    if (head_dim == 256 && kv_type == SIXI_TYPE_Q8_0) {
+        // q8_0 at 256-dim heads: the 32-cell q8_0 kernel on one lane, up to two row tiles per
+        // wave (33-48 rows run as 64)
+        switch (row_tiles) {
+            case 1: return launch_wide_q8<1, 1, 256>(a, mode, causal, stream);
+            case 2: return launch_wide_q8<2, 1, 256>(a, mode, causal, stream);
+            case 4: return launch_wide_q8<2, 2, 256>(a, mode, causal, stream);
+            case 6: return launch_wide_q8<2, 3, 256>(a, mode, causal, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
     if (head_dim == 256) {
         // 256-dim heads: every row count runs the 32-cell kernel (one or two row groups)
         if (kv_type != SIXI_TYPE_F16) return hipErrorNotSupported;

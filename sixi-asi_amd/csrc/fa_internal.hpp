@@ -102,7 +102,7 @@ int decode_num_groups(const FaArgs& a, int cu_count, int groups_per_cu);
 // f16 KV under an explicit mask or a softcap (`generic`: the per-cell work needs the 512
 // registers per wave of that kernel), and q8_0 KV with more than 48 rows (128-dim heads).
 inline bool decode_wide_kernel(int kv_type, int row_tiles, int head_dim, bool generic) {
-    if (kv_type == SIXI_TYPE_Q8_0) return head_dim == 128 && (row_tiles > 3 || (generic && row_tiles > 1));
+    if (kv_type == SIXI_TYPE_Q8_0) return head_dim == 256 || (row_tiles > 3 || (generic && row_tiles > 1));
     return kv_type == SIXI_TYPE_F16 && (row_tiles > 3 || head_dim == 256 || generic);
 }
 // Work-groups per CU of the 16-cell kernel: two (256 registers per wave).  One group per CU

@@ -207,12 +207,17 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.D = (int)D;
     const int64_t rows = (int64_t)a.G * n_q;
     pl.splitk = rows <= kSplitMaxRows;
-    // q8_0 KV at 128-dim heads runs the split-K kernels in one launch that reads the KV once:
+    // q8_0 KV runs the split-K kernels in one launch that reads the KV once: at 128-dim heads
     // the 16-cell kernel up to 48 rows (with a mask or softcap: up to 16), the 32-cell q8_0
-    // kernel beyond
+    // kernel beyond; at 256-dim heads (16-byte aligned rows) the 32-cell q8_0 kernel
     pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
-        if (D == 128 && pl.splitk) {
+        // 256-dim q8_0 rows (272 B) are read by 16-byte LDS-DMA loads: every row must start
+        // 16-byte aligned
+        auto rows16 = [](const sixi_view& t) {
+            return aligned(t.data, 16) && t.nb[1] % 16 == 0 && t.nb[2] % 16 == 0 && t.nb[3] % 16 == 0;
+        };
+        if (pl.splitk && (D == 128 || (D == 256 && rows16(k) && rows16(v)))) {
             // one launch of the 32-cell q8_0 kernel
         } else {
             // prefill-sized blocks, more than 48 rows of one head, or 256-dim heads: K, V and Q

@@ -214,6 +214,14 @@ def test_checker_finds_scratch_in_a_step_loop():
     assert scratch_in_step_loops(toy.format(mid="v_mov_b32 v1, v2")) == []
 
 
+def test_decode_kernels_call_no_functions(decode_asm):
+    # every piece function is inlined into its kernel (an out-of-line one gave wrong results);
+    # s_setpc_b64 alone is the compiler's far branch, s_swappc a call
+    assert "s_swappc" not in decode_asm
+    names = re.findall(r"\.type\s+(\S+),@function", decode_asm)
+    assert names and all(re.search(r"sixi.*(decode_|merge)", n) for n in names), names[:5]
+
+
 def test_decode_kernels_touch_no_scratch_in_step_loops(decode_asm):
     bad = scratch_in_step_loops(decode_asm)
     assert not bad, f"{len(bad)} scratch accesses in step loops, first: {bad[:3]}"

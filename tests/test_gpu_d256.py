@@ -1,7 +1,8 @@
 """256-dim heads (the real model's key/value length, configs/qwen3.8-27b-ud-q4-k-xl.sixi) on the
 32-cell split-K kernel, against the oracle through the C ABI: decode, speculative verify (96 rows
 per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q; the
-prefill kernel for 256-dim heads; and q8_0 caches through the f16 staging.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
+prefill kernel for 256-dim heads; q8_0 caches on the 32-cell q8_0 kernel (one lane, up to three
+row groups of two row tiles) and, for prefill-sized blocks, through the f16 staging.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
 import sys
 
 import numpy as np
@@ -91,13 +92,18 @@ def test_d256_prefill_explicit_mask(fa):
     _run_check(fa, w, "prefill explicit mask", explicit=True)
 
 
-@pytest.mark.parametrize("label,kv_len,q_len", [
-    ("q8_0 decode", [3000, 70], [1, 1]),
-    ("q8_0 verify", [1200, 400], [16, 7]),
-    ("q8_0 prefill", [200], [150]),
+@pytest.mark.parametrize("label,kv_len,q_len,explicit", [
+    ("q8_0 decode", [3000, 70], [1, 1], False),                 # 6 rows: one row group of one tile
+    ("q8_0 24 rows", [1800, 640], [4, 3], False),               # one row group of two tiles
+    ("q8_0 48 rows (run as 64)", [2500, 90], [8, 8], False),    # two row groups
+    ("q8_0 verify", [1200, 400], [16, 7], False),               # 96 rows: three row groups
+    ("q8_0 verify, one long stream", [20000], [16], False),     # many pieces
+    ("q8_0 verify, explicit mask", [1500, 333], [16, 5], True),
+    ("q8_0 decode, explicit mask", [4000], [1], True),
+    ("q8_0 prefill (staged)", [200], [150], False),
 ])
-def test_d256_q8_0_staged(fa, label, kv_len, q_len):
-    """q8_0 caches of 256-dim heads run through the f16 staging (the q8_0 split-K kernel holds
-    128-dim rows)."""
+def test_d256_q8_0(fa, label, kv_len, q_len, explicit):
+    """q8_0 caches of 256-dim heads: split-K calls run the 32-cell q8_0 kernel on one lane,
+    prefill-sized blocks the f16 staging."""
     w = wl.Workload("d256 q8", 0x51A7_9700 + sum(q_len), len(kv_len), kv_len, q_len, D=256, kv_type=sa.TYPE_Q8_0)
-    _run_check(fa, w, label)
+    _run_check(fa, w, label, explicit=explicit)

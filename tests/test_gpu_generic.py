@@ -62,6 +62,8 @@ CASES = [
     ("q8_0 72 rows, alibi + softcap", sa.TYPE_Q8_0, 128, [1300, 40], [12, 12], 24, 4, 0.03, 8.0, 20.0, 0),
     ("256-dim 96 rows, alibi", sa.TYPE_F16, 256, [600, 1100], [16, 4], 24, 4, 0.03, 8.0, 0.0, 0),
     ("256-dim 6 rows, softcap", sa.TYPE_F16, 256, [2000], [1], 24, 4, 0.0, 0.0, 30.0, 0),
+    ("q8_0 256-dim 96 rows, alibi + softcap", sa.TYPE_Q8_0, 256, [900, 1300], [16, 11], 24, 4, 0.02, 8.0, 20.0, 0),
+    ("q8_0 256-dim 6 rows, distance mask", sa.TYPE_Q8_0, 256, [2500], [1], 24, 4, 0.03, 0.0, 0.0, 0),
     ("prefill rows, alibi + softcap", sa.TYPE_F16, 128, [200], [150], 24, 4, 0.02, 8.0, 25.0, 0),
     # an explicit mask alone: the prefill kernel's LDS-staged mask mode (dead tiles skipped)
     ("prefill rows, distance mask", sa.TYPE_F16, 128, [200, 700], [150, 260], 24, 4, 0.02, 0.0, 0.0, 0),
