@@ -472,6 +472,16 @@ def batched_verify_q8():
     return dataclasses.replace(wl.config("batched_verify"), name="batched_verify_q8", kv_type=sa.TYPE_Q8_0)
 
 
+def q8_variant(name: str):
+    """A config over a q8_0 cache (same seeds, lengths and heads)."""
+    import dataclasses
+
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    return dataclasses.replace(wl.config(name), name=name + "_q8", kv_type=sa.TYPE_Q8_0)
+
+
 def verify_q8_only(steps: int, warmup: int) -> int:
     import sixi_attn as sa
     from sixi_attn import workloads as wl
@@ -601,9 +611,14 @@ def main() -> int:
     if not args.no_extra:
         extra = {}
         for name in ("decode", "verify", "long_q8_decode", "long_q8_verify", "batched_verify_q8", "decode_d256",
-                     "batched_verify_d256"):
+                     "batched_verify_d256", "decode_d256_q8", "batched_verify_d256_q8"):
             try:
-                we = batched_verify_q8() if name == "batched_verify_q8" else wl.config(name)
+                if name == "batched_verify_q8":
+                    we = batched_verify_q8()
+                elif name.endswith("_q8"):
+                    we = q8_variant(name[:-3])
+                else:
+                    we = wl.config(name)
                 he = wl.make_host(we)
                 de = wl.to_device(he)
                 mse, pere = time_calls(fa, we, de, max(20, args.steps // 2), max(5, args.warmup // 2))
