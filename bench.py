@@ -119,8 +119,8 @@ def time_paged(fa, w, dev, steps: int, warmup: int) -> dict:
 
 
 def ws_bytes(fa, w, dev, mask=None) -> int:
-    """sixi_attn_workspace_bytes of a call of workload w (q8_0 prefill-sized blocks and
-    256-dim q8_0 calls include the f16 staging of the cache)."""
+    """sixi_attn_workspace_bytes of a call of workload w (256-dim q8_0 prefill-sized blocks
+    include the f16 staging of the cache)."""
     import torch
 
     import sixi_attn as sa
@@ -250,7 +250,8 @@ def copy_calibration(steps: int) -> int:
 
 def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None, explicit_mask=False):
     """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks).
-    kv_type q8_0 runs the same chunks over a q8_0 cache (staged as f16 operands per call);
+    kv_type q8_0 runs the same chunks over a q8_0 cache (128-dim heads: tiles converted in LDS;
+    256-dim heads: staged as f16 operands per call);
     explicit_mask hands the causal mask over as a ggml f16 KQ mask (the ggml hook's path)."""
     import dataclasses
 

@@ -255,6 +255,92 @@ __device__ __forceinline__ void dma4x8_to_lds(buf_rsrc rs, const uint32_t (&v)[8
         : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "s"(rs)
         : "memory", "scc");
 }
+// 32 q8_0 rows of 128 dims (34 dwords each) by seventeen 4-byte-per-lane loads.  Loads
+// u = 0..15 move dwords 0..31 of rows 2u and 2u + 1 (lane l: row 2u + l/32, dword l%32, offset
+// v + u * step with v = (l/32) * stride + 4(l%32) and step = 2 * stride) to LDS lds + 264u +
+// 4l; the last moves dwords 32, 33 (lane l: row l/2, dword 32 + l%2, offset vx) to lds + 4224
+// + 4l.  So dword c < 32 of row x sits at byte 264(x/2) + 128(x%2) + 4c, dword 32 + e at
+// 4224 + 8x + 4e.  The offset steps inside the block, so it costs no registers across it.
+__device__ __forceinline__ void dma_q8rows32_to_lds(buf_rsrc rs, uint32_t v, uint32_t vx, uint32_t step,
+                                                    uint32_t lds) {
+    int saved;
+    uint32_t o;
+    asm volatile(
+        "s_nop 4\n\t"
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %6\n\t"
+        "v_mov_b32 %1, %2\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "v_add_u32 %1, %4, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %1, %3, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 264\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dword %5, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved), "=&v"(o)
+        : "v"(v), "s"(rs), "s"(__builtin_amdgcn_readfirstlane(step)), "v"(vx),
+          "s"(__builtin_amdgcn_readfirstlane(lds))
+        : "memory", "scc");
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N <= 63, "vmcnt counts at most 63 loads");

@@ -61,7 +61,7 @@ struct FaArgs {
     int32_t* seg_pieces;   // per segment: logical work-groups of its first and last piece
 };
 
-// q8_0 KV for prefill-sized blocks (fa_q8_stage.hip): K, V and Q staged as dense f16 rows in
+// q8_0 KV at 256-dim heads beyond the q8_0 kernel (fa_q8_stage.hip): K, V and Q staged as dense f16 rows in
 // the workspace, then the f16 kernels.  k16/v16: [S][n_kv][Hkv][D], q16: [S][n_q][H][D].
 struct Q8StageArgs {
     const char* q;

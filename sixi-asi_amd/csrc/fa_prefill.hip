@@ -1,5 +1,5 @@
 // fa_prefill.hip -- chunked causal prefill (and any block of more than 96 rows per GQA group)
-// on gfx950 f16 MFMA (head_dim 128, f16 KV).
+// on gfx950 f16 MFMA (head_dim 128 and 256 over f16 KV; head_dim 128 over q8_0 KV).
 //
 // Work decomposition.  One work-group computes 128 consecutive rows (block rows j) of one
 // q-head of one stream, over every KV cell those rows see.  The grid is ordered heaviest
@@ -34,6 +34,12 @@
 // by LDS-DMA, the next tile's as soon as it has read the current one.  A wave whose 32 rows
 // see none of a tile's cells (a causal mask's upper triangle) skips the tile's MFMAs; a tile
 // whose mask is zero for all of them skips the per-cell work.
+//
+// q8_0 KV (128-dim heads) runs the same tiles: each wave moves 32 q8_0 rows of the next tile
+// (K or V, 4352 bytes) by LDS-DMA into the start of the 8 KB of the f16 buffer that those rows
+// will occupy, and at the end of the tile rewrites them there as f16 (f16(q * d)), so the LDS
+// and the occupancy are the f16 kernel's and the workspace does not grow with the cache.  Q
+// goes through ggml's conversion to the q8_0 dot type first, as in the decode kernels.
 #include <type_traits>
 
 #include "fa_device.hpp"
@@ -66,6 +72,21 @@ struct PrefillLds {
     u32x4 m[MASK ? 4 * kMaskWave / 16 : 1];  // MASK: wave w's rows at kMaskWave * w
 };
 
+// q8_0 KV (128-dim heads): block 2h + M of cell c (f16 scale bits d, 32 int8 quants as eight
+// little-endian dwords) into a tile's f16 layout at dst: K chunk j (dims 8j .. 8j+7) at slot
+// j ^ (c % 16), V's 32-byte chunk j/2 at position (j/2) ^ 2(c % 4).  `key` is the lane's part
+// of those slots, (8h) ^ (c % 16) for K and (4h) ^ 2(c % 4) for V, so that each store address
+// is one XOR with a constant.  The values are f16(q * d), one rounding, as every q8_0 path of
+// this library dequantises.
+template <bool IS_V, int M>
+__device__ __forceinline__ void pf_q8_block_store(char* dst, int c, int key, uint16_t d, const uint32_t (&w)[8]) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int pos = IS_V ? 32 * (key ^ (2 * M + (k >> 1))) + 16 * (k & 1) : 16 * (key ^ (4 * M + k));
+        *reinterpret_cast<u32x4*>(dst + c * 256 + pos) = dequant_q8x8(w[2 * k], w[2 * k + 1], d);
+    }
+}
+
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
@@ -73,9 +94,12 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int MODE, int D>
-__global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs a, int causal, int nrb, int n_cu) {
+template <int MODE, int D, int KV>
+__device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nrb, int n_cu) {
     using P = PfDim<D>;
+    constexpr bool Q8 = KV == SIXI_TYPE_Q8_0;
+    static_assert(!Q8 || D == 128, "q8_0 tiles: 128-dim heads");
+    constexpr int GROUPS = P::GROUPS;
     constexpr int kKBytes = P::TILE, kVBytes = P::TILE;
     __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
     const int tid = threadIdx.x;
@@ -93,7 +117,7 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     const int b = blockIdx.x;
     const int N = gridDim.x;
     int rank = b;
-    if (P::GROUPS == 2 && N > n_cu && N <= 2 * n_cu) {
+    if (GROUPS == 2 && N > n_cu && N <= 2 * n_cu) {
         const int npair = N - n_cu;
         const int alone = n_cu - npair;
         if (b < npair) rank = alone + b;
@@ -122,7 +146,56 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     // ---- Q^T B operands in registers: lane l -> row j, dims 16ks + 8*hl .. +7 ----
     // (every load issued before any is used; rows past the block read its first row)
     f16x8 qop[P::KS];
-    {
+    if constexpr (Q8) {
+        // ggml's conversion of Q to the q8_0 dot type: per 32-dim block (ks = 2bq, 2bq + 1 of
+        // lanes l and l^32) d = amax/127, q = round-half-away(x * 127/amax) clamped to +-127,
+        // and the MFMA takes f16(q * f16(d))
+        const char* src = a.q + (int64_t)(row_ok ? j : j0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3;
+        float xq[P::KS][8];
+        if (a.q_f16) {
+            u32x4 raw[P::KS];
+#pragma unroll
+            for (int ks = 0; ks < P::KS; ++ks) raw[ks] = ld16(src + (16 * ks + 8 * hl) * 2);
+#pragma unroll
+            for (int ks = 0; ks < P::KS; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xq[ks][e] = (float)as_f16x8(raw[ks])[e];
+        } else {
+            f32x4 lo[P::KS], hi[P::KS];
+#pragma unroll
+            for (int ks = 0; ks < P::KS; ++ks) {
+                lo[ks] = *reinterpret_cast<const f32x4*>(src + (16 * ks + 8 * hl) * 4);
+                hi[ks] = *reinterpret_cast<const f32x4*>(src + (16 * ks + 8 * hl) * 4 + 16);
+            }
+#pragma unroll
+            for (int ks = 0; ks < P::KS; ++ks)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xq[ks][e] = lo[ks][e];
+                    xq[ks][4 + e] = hi[ks][e];
+                }
+        }
+#pragma unroll
+        for (int bq = 0; bq < P::KS / 2; ++bq) {
+            float am = 0.0f;
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(xq[2 * bq + k2][e]));
+            am = fmaxf(am, __shfl_xor(am, 32, 64));
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 127.0f / am : 0.0f;
+            const float dh = (float)(_Float16)d;
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                f16x8 hv;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    hv[e] = (_Float16)(fminf(fmaxf(roundf(xq[2 * bq + k2][e] * id), -127.0f), 127.0f) * dh);
+                qop[2 * bq + k2] = row_ok ? hv : f16x8{};
+            }
+        }
+    } else {
         const char* src = a.q + (int64_t)(row_ok ? j : j0) * a.q_nb1 + (int64_t)h * a.q_nb2 + (int64_t)s * a.q_nb3;
         if (a.q_f16) {
             u32x4 raw[P::KS];
@@ -211,6 +284,72 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
         }
     };
 
+    // Q8: wave w moves the q8_0 rows of K cells 32(w % 2) .. +31 (w < 2) or V cells (w >= 2)
+    // of the next tile by 17 dword LDS-DMA loads (two row heads of 128 contiguous bytes per
+    // load, then the rows' last 8 bytes) into the start of its own 8 KB of that tile's f16
+    // buffer -- the rows it later writes as f16 -- and converts them there in place: no other
+    // wave reads or writes that slice before the barrier, so the f16 tiles are all the LDS it
+    // takes.
+    const int wq = __builtin_amdgcn_readfirstlane(w);
+    const uint32_t q8nb = (uint32_t)__builtin_amdgcn_readfirstlane((int)(wq >= 2 ? a.v_nb1 : a.k_nb1));
+    // byte offset of this wave's slice in f16 buffer `buf`
+    auto q8_slice = [&](int buf) { return (wq >= 2 ? kVBase + buf * kVBytes : buf * kKBytes) + (wq & 1) * 32 * P::ROW; };
+    auto issue_q8 = [&](int t, int buf) {
+        if constexpr (Q8) {
+            const int page = t * kBN < sd.nc ? page_id(pages, a, s, (t * kBN) >> 8) : 0;
+            const KvSpan sp = wq >= 2 ? kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, t * kBN, sd.nc, 136, page)
+                                      : kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, t * kBN, sd.nc, 136, page);
+            const buf_rsrc rs = make_rsrc_uniform(sp.p, sp.bytes);
+            // (the lane offsets are recomputed here, not kept in registers across the tile)
+            uint32_t l = (uint32_t)lane;
+            asm volatile("" : "+v"(l));
+            const uint32_t r0 = 32u * (uint32_t)(wq & 1);
+            const uint32_t v = (r0 + (l >> 5)) * q8nb + 4u * (l & 31);
+            const uint32_t vx = (r0 + (l >> 1)) * q8nb + 128u + 4u * (l & 1);
+            dma_q8rows32_to_lds(rs, v, vx, 2u * q8nb, lds0 + (uint32_t)q8_slice(buf));
+        }
+    };
+    // this wave's q8_0 rows in f16 buffer BUF (landed) -> f16 rows of the same slice.  Lane
+    // (x = l % 32, h = l / 32) reads blocks 2h and 2h + 1 of row x, dwords 17h .. 17h + 16 --
+    // dword c < 32 at byte 264(x/2) + 128(x%2) + 4c, dwords 32, 33 at 4224 + 8x, so the 64
+    // lanes of each read hit 64 distinct banks -- every read before any write.
+    auto convert_q8 = [&](auto BUF) {
+        if constexpr (Q8) {
+            constexpr int buf = decltype(BUF)::value;
+            char* sl = lds + q8_slice(buf);
+            // (addresses and store keys are recomputed here, not kept in registers across the tile)
+            int lx = lane;
+            asm volatile("" : "+v"(lx));
+            const int x = lx & 31, hx = lx >> 5;
+            const int bx = 264 * (x >> 1) + 128 * (x & 1);
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(sl + bx + 68 * hx);
+            const uint32_t* src2 = reinterpret_cast<const uint32_t*>(sl + (hx ? 4224 + 8 * x : bx + 60));
+            uint32_t r[17];
+#pragma unroll
+            for (int i = 0; i < 15; ++i) r[i] = src[i];
+            r[15] = src2[0];
+            r[16] = src2[1];
+            asm volatile("" ::: "memory");
+            // block 2h: scale in the low half of dword 0, quants 2 bytes past dwords 0..8;
+            // block 2h + 1: scale in the high half of dword 8, quants dwords 9..16
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                lo[i] = __builtin_amdgcn_alignbyte(r[i + 1], r[i], 2);
+                hi[i] = r[9 + i];
+            }
+            const uint16_t dlo = (uint16_t)(r[0] & 0xffffu), dhi = (uint16_t)(r[8] >> 16);
+            const int key = wq < 2 ? (8 * hx) ^ (x & 15) : (4 * hx) ^ (2 * (x & 3));
+            if (wq < 2) {
+                pf_q8_block_store<false, 0>(sl, x, key, dlo, lo);
+                pf_q8_block_store<false, 1>(sl, x, key, dhi, hi);
+            } else {
+                pf_q8_block_store<true, 0>(sl, x, key, dlo, lo);
+                pf_q8_block_store<true, 1>(sl, x, key, dhi, hi);
+            }
+        }
+    };
+
     f32x16 acc[P::DB];  // O^T blocks: dims 32db + 8(i/4) + 4hl + i%4 of row j
 #pragma unroll
     for (int db = 0; db < P::DB; ++db)
@@ -257,7 +396,10 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
         constexpr int buf = decltype(BUF)::value;
         constexpr bool masked = decltype(MASKED)::value;
         const bool more = t + 1 < t_end;
-        if (more) issue_kv(t + 1, buf ^ 1);
+        if (more) {
+            if constexpr (Q8) issue_q8(t + 1, buf ^ 1);
+            else issue_kv(t + 1, buf ^ 1);
+        }
         const int c0 = t * kBN;
         const char* kt = lds + buf * kKBytes;
 
@@ -425,7 +567,12 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
 
         __builtin_amdgcn_s_setprio(0);
         }  // live
-        if (more) wait_vmcnt<0>();  // this wave's share of tile t+1 (and, masked, its mask rows) is in LDS
+        if (more) {
+            // this wave's share of tile t+1 (and, masked, its mask rows) is in LDS; Q8: it
+            // becomes f16 in place
+            wait_vmcnt<0>();
+            if constexpr (Q8) convert_q8(std::integral_constant<int, buf ^ 1>{});
+        }
         __syncthreads();
     };
     // (256-dim heads run every tail tile masked: two bodies per buffer in one loop would merge
@@ -440,9 +587,11 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
 
     // prologue: the first tile into buffer 0
     if (t_beg < t_end) {
-        issue_kv(t_beg, 0);
+        if constexpr (Q8) issue_q8(t_beg, 0);
+        else issue_kv(t_beg, 0);
         issue_mask(t_beg);
         wait_vmcnt<0>();
+        if constexpr (Q8) convert_q8(std::integral_constant<int, 0>{});
     }
     __syncthreads();
 
@@ -478,31 +627,52 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     }
 }
 
+template <int MODE, int D>
+__global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs a, int causal, int nrb, int n_cu) {
+    prefill_body<MODE, D, SIXI_TYPE_F16>(a, causal, nrb, n_cu);
+}
+
+// q8_0 KV at 128-dim heads: the same tiles, converted from q8_0 rows in place in LDS
+template <int MODE>
+__global__ __launch_bounds__(kThreads, PfDim<128>::GROUPS) void prefill_q8(FaArgs a, int causal, int nrb, int n_cu) {
+    prefill_body<MODE, 128, SIXI_TYPE_Q8_0>(a, causal, nrb, n_cu);
+}
+
+template <int MODE, int D, int KV>
+void launch_prefill_mode(const FaArgs& a, int causal, int nrb, hipStream_t stream) {
+    const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
+    if constexpr (KV == SIXI_TYPE_Q8_0)
+        hipLaunchKernelGGL((prefill_q8<MODE>), grid, block, 0, stream, a, causal, nrb, a.P);
+    else
+        hipLaunchKernelGGL((prefill_f16<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
+}
+
 }  // namespace
 
-template <int D>
+template <int D, int KV>
 hipError_t launch_prefill_d(const FaArgs& a, int mask_mode, hipStream_t stream) {
     const bool generic = mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f;
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
     const int nrb = (a.n_q + kBM - 1) / kBM;
-    const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
     // an explicit mask alone, with 16-byte aligned rows that one 32-bit range covers: LDS-staged
     const bool mask_only = mask_mode == SIXI_MASK_EXPLICIT && a.mask && a.softcap == 0.0f && a.alibi_nlog2 == 0 &&
                            reinterpret_cast<uintptr_t>(a.mask) % 16 == 0 && a.m_nb1 % 16 == 0 &&
                            (a.m_ne3 == 1 || a.m_nb3 % 16 == 0) && (int64_t)a.n_q * a.m_nb1 < (int64_t)UINT32_MAX;
     if (mask_only)
-        hipLaunchKernelGGL((prefill_f16<MODE_MASK, D>), grid, block, 0, stream, a, causal, nrb, a.P);
+        launch_prefill_mode<MODE_MASK, D, KV>(a, causal, nrb, stream);
     else if (generic)
-        hipLaunchKernelGGL((prefill_f16<MODE_GENERIC, D>), grid, block, 0, stream, a, causal, nrb, a.P);
+        launch_prefill_mode<MODE_GENERIC, D, KV>(a, causal, nrb, stream);
     else
-        hipLaunchKernelGGL((prefill_f16<MODE_FAST, D>), grid, block, 0, stream, a, causal, nrb, a.P);
+        launch_prefill_mode<MODE_FAST, D, KV>(a, causal, nrb, stream);
     return hipGetLastError();
 }
 
 hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim, hipStream_t stream) {
+    if (kv_type == SIXI_TYPE_Q8_0)
+        return head_dim == 128 ? launch_prefill_d<128, SIXI_TYPE_Q8_0>(a, mask_mode, stream) : hipErrorNotSupported;
     if (kv_type != SIXI_TYPE_F16) return hipErrorNotSupported;
-    if (head_dim == 128) return launch_prefill_d<128>(a, mask_mode, stream);
-    if (head_dim == 256) return launch_prefill_d<256>(a, mask_mode, stream);
+    if (head_dim == 128) return launch_prefill_d<128, SIXI_TYPE_F16>(a, mask_mode, stream);
+    if (head_dim == 256) return launch_prefill_d<256, SIXI_TYPE_F16>(a, mask_mode, stream);
     return hipErrorNotSupported;
 }
 

@@ -1,6 +1,6 @@
-// fa_q8_stage.hip -- q8_0 KV where the q8_0 split-K kernel does not apply (blocks of more
-// than 48 rows of one head, prefill chunks, 256-dim heads): the operands are staged as f16 in
-// the workspace and the f16 kernels run on them.
+// fa_q8_stage.hip -- q8_0 KV where no q8_0 kernel applies (256-dim heads: prefill chunks, and
+// rows that are not 16-byte aligned): the operands are staged as f16 in the workspace and the
+// f16 kernels run on them.
 //
 // The values are exactly the MFMA operands the q8_0 split-K kernels use (fa_decode.hip), so
 // both paths compute ggml's q8_0 attention the same way:

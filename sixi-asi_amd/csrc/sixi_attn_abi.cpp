@@ -209,7 +209,8 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     pl.splitk = rows <= kSplitMaxRows;
     // q8_0 KV runs the split-K kernels in one launch that reads the KV once: at 128-dim heads
     // the 16-cell kernel up to 48 rows (with a mask or softcap: up to 16), the 32-cell q8_0
-    // kernel beyond; at 256-dim heads (16-byte aligned rows) the 32-cell q8_0 kernel
+    // kernel beyond; at 256-dim heads (16-byte aligned rows) the 32-cell q8_0 kernel.  Prefill
+    // blocks at 128-dim heads read q8_0 tiles directly too; only 256-dim prefill is staged.
     pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
         // 256-dim q8_0 rows (272 B) are read by 16-byte LDS-DMA loads: every row must start
@@ -219,8 +220,10 @@ int resolve(const sixi_attn_params* p, Plan* out) {
         };
         if (pl.splitk && (D == 128 || (D == 256 && rows16(k) && rows16(v)))) {
             // one launch of the 32-cell q8_0 kernel
+        } else if (!pl.splitk && D == 128) {
+            // the prefill kernel converts each tile's q8_0 rows to f16 in LDS
         } else {
-            // prefill-sized blocks, more than 48 rows of one head, or 256-dim heads: K, V and Q
+            // prefill-sized blocks at 256-dim heads (and unaligned 256-dim rows): K, V and Q
             // are staged as f16 operands in the workspace (fa_q8_stage.hip) and the f16 kernels run
             pl.q8_stage = true;
             pl.kv_type = SIXI_TYPE_F16;

@@ -96,6 +96,25 @@ def test_workspace_holds_the_launched_slots(D):
         assert n.value >= need, (G, n_q, D, n.value, need)
 
 
+def test_q8_prefill_workspace_is_independent_of_the_cache_length():
+    """128-dim q8_0 prefill reads the q8_0 tiles itself: the workspace stays a token whatever
+    the cache length (no f16 copy of the cache).  256-dim q8_0 prefill stages K, V and Q as
+    f16, so its workspace grows with the cells."""
+    lib = sa.load_library()
+
+    def ws(**kw):
+        n = ctypes.c_size_t(0)
+        assert lib.sixi_attn_workspace_bytes(ctypes.byref(_params(**kw)), ctypes.byref(n)) == sa.OK
+        return n.value
+
+    sizes = {n_kv: ws(n_q=512, n_kv=n_kv, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 65536, 1 << 20)}
+    assert len(set(sizes.values())) == 1 and sizes[1024] <= 4096, sizes
+    assert ws(n_q=512, n_kv=65536, kv_type=sa.TYPE_Q8_0, mode=sa.MASK_NONE, kv_len=False) == sizes[1024]
+    assert ws(n_q=512, n_kv=1024, kv_type=sa.TYPE_F16) == sizes[1024]
+    d256 = [ws(n_q=512, n_kv=n_kv, D=256, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 65536)]
+    assert d256[1] > d256[0] >= 2 * 2 * 1024 * 4 * 256 * 2
+
+
 @pytest.mark.parametrize("mutate,code", [
     (lambda p: setattr(p, "flags", 1), sa.E_INVALID_ARGUMENT),
     (lambda p: setattr(p.q, "data", None), sa.E_INVALID_ARGUMENT),

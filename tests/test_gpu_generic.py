@@ -3,8 +3,8 @@
 be staged through LDS (rows not 16-byte aligned, more than 32 rows), at every decode shape
 that takes them -- f16 at 6, 24 and 48 rows per GQA group (32-cell kernel, one row group per
 lane), 64 and 96 rows, q8_0 (16-cell kernel up to 48 rows, the 32-cell q8_0 kernel beyond),
-256-dim heads -- and the prefill kernel (its LDS-staged mask mode for a plain explicit mask, the
-generic mode otherwise).
+256-dim heads -- and the prefill kernel over f16 and q8_0 tiles (its LDS-staged mask mode for a
+plain explicit mask, the generic mode otherwise).
 Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output, as for the other parity tests."""
 import sys
 
@@ -70,6 +70,9 @@ CASES = [
     ("prefill rows, causal mask, empty stream", sa.TYPE_F16, 128, [0, 333, 90], [130, 0, 300], 24, 4, 0.0, 0.0, 0.0, 0),
     ("256-dim prefill rows, distance mask", sa.TYPE_F16, 256, [300], [130], 24, 4, 0.01, 0.0, 0.0, 0),
     ("prefill rows, unaligned mask rows", sa.TYPE_F16, 128, [200], [150], 24, 4, 0.02, 0.0, 0.0, 3),
+    ("q8_0 prefill rows, alibi + softcap", sa.TYPE_Q8_0, 128, [200], [150], 24, 4, 0.02, 8.0, 25.0, 0),
+    ("q8_0 prefill rows, distance mask", sa.TYPE_Q8_0, 128, [200, 700], [150, 260], 24, 4, 0.02, 0.0, 0.0, 0),
+    ("q8_0 prefill rows, unaligned mask rows", sa.TYPE_Q8_0, 128, [200], [150], 24, 4, 0.02, 0.0, 0.0, 3),
 ]
 
 

@@ -1,7 +1,8 @@
 """Paged KV caches on the GPU: attention through a page table (include/sixi_attn.h
 page_table) equals the attention over the same cells laid out contiguously, bit for bit, on
 every kernel path (split-K 16- and 32-cell kernels, f16 and q8_0, 128- and 256-dim heads, the
-explicit-mask path, the prefill kernel, the q8_0 staging path); and the page pool's seq_cp
+explicit-mask path, the prefill kernel over f16 and q8_0 tiles, the 256-dim q8_0 staging
+path); and the page pool's seq_cp
 shares pages without moving cells while a write into a shared page copies it first
 (include/sixi_kv.h sixi_kv_pool_*), checked bitwise against the data-copy path (sixi_kv_copy)
 and against the oracle.
@@ -68,6 +69,8 @@ CASES = [
     ("q8_0 96 rows (32-cell q8_0 kernel)", sa.TYPE_Q8_0, 128, [900, 300], [16, 16], 24, 4, False),
     ("q8_0 256-dim (staged)", sa.TYPE_Q8_0, 256, [700, 120], [8, 3], 24, 4, False),
     ("prefill rows", sa.TYPE_F16, 128, [300, 0], [130, 200], 24, 4, False),
+    ("q8_0 prefill rows", sa.TYPE_Q8_0, 128, [300, 0], [130, 200], 24, 4, False),
+    ("q8_0 prefill rows, explicit mask", sa.TYPE_Q8_0, 128, [700, 40], [150, 260], 24, 4, True),
 ]
 
 

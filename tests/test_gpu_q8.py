@@ -121,29 +121,34 @@ def test_q8_more_than_48_rows(fa, kv_len, q_len, H, Hkv):
     _check(w, host, _run(fa, w, dev), list(range(w.S)), "q8 49..96 rows")
 
 
-@pytest.mark.parametrize("name,kv_len,q_len,H,Hkv", [
-    ("q8 64 rows, one stream", [100], [64], 24, 4),              # 384 rows per group: staged prefill
-    ("q8 prefill-sized, ragged", [300, 1000], [200, 130], 24, 4),
-    ("q8 64 rows of one head", [700, 90], [64, 49], 4, 4),       # G = 1: staged split-K
+@pytest.mark.parametrize("name,kv_len,q_len,H,Hkv,q_type", [
+    ("q8 64 rows, one stream", [100], [64], 24, 4, sa.TYPE_F32),          # 384 rows per group: prefill
+    ("q8 prefill-sized, ragged", [300, 1000], [200, 130], 24, 4, sa.TYPE_F32),
+    ("q8 prefill, f16 Q", [300, 1000], [200, 130], 24, 4, sa.TYPE_F16),
+    ("q8 prefill, one-tile and empty streams", [0, 10, 333], [130, 40, 0], 8, 8, sa.TYPE_F32),
+    ("q8 prefill, long stream", [5000], [300], 8, 2, sa.TYPE_F32),          # 83 tiles through the stages
+    ("q8 64 rows of one head", [700, 90], [64, 49], 4, 4, sa.TYPE_F32),     # G = 1: 32-cell q8_0 kernel
 ])
-def test_q8_staged_blocks(fa, name, kv_len, q_len, H, Hkv):
-    """Blocks the q8_0 split-K kernels do not hold: K, V and Q are staged as f16 operands in the
-    workspace and the f16 kernels run on them."""
-    _say(f"{name}: kv_len {kv_len} q_len {q_len} H {H} Hkv {Hkv}")
-    w = wl.Workload("q8_stage", 0x51A7_7100 + sum(q_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv,
-                    kv_type=sa.TYPE_Q8_0)
+def test_q8_prefill_blocks(fa, name, kv_len, q_len, H, Hkv, q_type):
+    """Blocks beyond the q8_0 split-K kernels: the prefill kernel moves each tile's q8_0 rows
+    into LDS and converts them to f16 there (no staging in the workspace)."""
+    _say(f"{name}: kv_len {kv_len} q_len {q_len} H {H} Hkv {Hkv} q_type {q_type}")
+    w = wl.Workload("q8_prefill", 0x51A7_7100 + sum(q_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv,
+                    kv_type=sa.TYPE_Q8_0, q_type=q_type)
     host = wl.make_host(w, poison=True)
     dev = wl.to_device(host)
-    _check(w, host, _run(fa, w, dev), list(range(w.S)), name)
+    streams = [s for s in range(w.S) if q_len[s] > 0]
+    _check(w, host, _run(fa, w, dev), streams, name)
 
 
-def test_q8_staged_prefill_explicit_mask(fa):
-    w = wl.Workload("q8_stage_mask", 0x51A7_7180, 2, [500, 64], [160, 100], kv_type=sa.TYPE_Q8_0)
+def test_q8_prefill_explicit_mask(fa):
+    """A plain explicit mask: the prefill kernel's LDS-staged mask mode over q8_0 tiles."""
+    w = wl.Workload("q8_prefill_mask", 0x51A7_7180, 2, [500, 64], [160, 100], kv_type=sa.TYPE_Q8_0)
     host = wl.make_host(w)
     dev = wl.to_device(host)
     n_kv = dev["k"].shape[1]
     mask = oracle.build_kq_mask(n_kv, w.n_q, host["kv_len"], host["q_len"])
     dmask = torch.from_numpy(mask.view(np.float16)).cuda()
-    _say("q8 staged prefill, explicit mask")
+    _say("q8 prefill, explicit mask")
     got = _run(fa, w, dev, mask_mode=sa.MASK_EXPLICIT, mask=dmask)
-    _check(w, host, got, list(range(w.S)), "q8 staged prefill explicit mask")
+    _check(w, host, got, list(range(w.S)), "q8 prefill explicit mask")
