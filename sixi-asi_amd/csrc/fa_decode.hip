@@ -379,7 +379,11 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT>& acc, const u
 template <int NT>
 __device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT>& acc, int n0, int s, int g,
                                            int R, int lane) {
-    const int r = lane & 15, c = lane >> 4;
+    // (the row addresses are computed here: hoisted out of the piece loop they would be held,
+    // as 64-bit values, across every piece's steps, and spilled)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r = ln & 15, c = ln >> 4;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
         const int row = 16 * (n0 + n) + r;
@@ -402,7 +406,10 @@ __device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT>& acc, 
 template <int NT>
 __device__ __forceinline__ void write_partial(float* slot, int rows_slot, int n0, int R, const Acc<NT>& acc,
                                               int lane) {
-    const int r = lane & 15, c = lane >> 4;
+    // (row offsets computed here, not held across the piece loop; see write_rows)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int r = ln & 15, c = ln >> 4;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
         const int row = 16 * (n0 + n) + r;

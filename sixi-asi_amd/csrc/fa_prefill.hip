@@ -616,13 +616,18 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
         l_sum = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
     if (row_ok) {
+        // (the row and its address are recomputed from the lane here rather than held across
+        // the tile loop)
+        int lx = lane;
+        asm volatile("" : "+v"(lx));
+        const int jw = j0 + 32 * wq + (lx & 31), hw = lx >> 5;
         const float inv = l_sum == 0.0f ? 0.0f : 1.0f / l_sum;
-        char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3;
+        char* dst = a.out + (int64_t)jw * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3;
 #pragma unroll
         for (int db = 0; db < P::DB; ++db)
 #pragma unroll
             for (int bq = 0; bq < 4; ++bq)
-                st16(dst + (32 * db + 8 * bq + 4 * hl) * 4,
+                st16(dst + (32 * db + 8 * bq + 4 * hw) * 4,
                      f32x4{acc[db][4 * bq], acc[db][4 * bq + 1], acc[db][4 * bq + 2], acc[db][4 * bq + 3]} * inv);
     }
 }

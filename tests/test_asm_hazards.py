@@ -227,7 +227,8 @@ def test_decode_kernels_touch_no_scratch_in_step_loops(decode_asm):
     assert not bad, f"{len(bad)} scratch accesses in step loops, first: {bad[:3]}"
 
 
-def test_prefill_kernels_touch_no_scratch_in_tile_loops(tmp_path_factory):
+def _asm_of(src, tmp_path_factory):
+    """gfx950 assembly of one HIP source of the library, built with the library's flags."""
     spec = importlib.util.spec_from_file_location("sixi_build", BUILD)
     build = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(build)
@@ -235,12 +236,57 @@ def test_prefill_kernels_touch_no_scratch_in_tile_loops(tmp_path_factory):
         hipcc = build._hipcc()
     except RuntimeError:
         pytest.skip("hipcc not available")
-    flags = [f for f in build.flags_for("fa_prefill.hip") if f != "-fPIC"]
-    out = tmp_path_factory.mktemp("asm") / "fa_prefill.s"
-    proc = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", str(out), str(build.CSRC / "fa_prefill.hip")],
+    flags = [f for f in build.flags_for(src) if f != "-fPIC"]
+    out = tmp_path_factory.mktemp("asm") / (src + ".s")
+    proc = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", str(out), str(build.CSRC / src)],
                           stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert proc.returncode == 0, proc.stdout[-2000:]
-    asm = out.read_text()
-    assert asm.count("v_mfma") > 0
-    bad = scratch_in_step_loops(asm)
+    return out.read_text()
+
+
+def kernels_with_scratch(asm):
+    """(kernel, bytes) for every kernel whose metadata reserves private (scratch) memory."""
+    meta = asm[asm.index("amdhsa.kernels:"):]
+    found = []
+    for blk in meta.split("\n  - ")[1:]:
+        # kernel-level keys are indented four spaces (argument keys eight)
+        name = re.search(r"^    \.name:\s+(\S+)", blk, re.M)
+        size = re.search(r"^    \.private_segment_fixed_size:\s+(\d+)", blk, re.M)
+        if name and size and int(size.group(1)) > 0:
+            found.append((name.group(1), int(size.group(1))))
+    return found
+
+
+def test_scratch_checker_reads_kernel_metadata():
+    meta = ("amdhsa.kernels:\n  - .agpr_count: 0\n    .args:\n      - .name: a\n        .offset: 0\n"
+            "    .name: k_a\n    .private_segment_fixed_size: 0\n"
+            "  - .agpr_count: 0\n    .name: k_b\n    .private_segment_fixed_size: 36\n")
+    assert kernels_with_scratch(meta) == [("k_b", 36)]
+
+
+@pytest.fixture(scope="module")
+def prefill_asm(tmp_path_factory):
+    return _asm_of("fa_prefill.hip", tmp_path_factory)
+
+
+def test_prefill_kernels_touch_no_scratch_in_tile_loops(prefill_asm):
+    assert prefill_asm.count("v_mfma") > 0
+    bad = scratch_in_step_loops(prefill_asm)
     assert not bad, f"{len(bad)} scratch accesses in tile loops, first: {bad[:3]}"
+
+
+def test_attention_kernels_use_no_scratch(decode_asm, prefill_asm):
+    # every decode, merge and prefill variant the library can launch keeps all its values in
+    # registers and LDS (no spill anywhere, prologue and epilogue included)
+    for asm in (decode_asm, prefill_asm):
+        assert asm.count(".private_segment_fixed_size:") > 5
+        bad = kernels_with_scratch(asm)
+        assert not bad, f"{len(bad)} kernels with scratch: {bad[:4]}"
+
+
+@pytest.mark.parametrize("src", ["fa_q8_stage.hip", "kv_write.hip", "layer_prologue.hip", "gdn_verify.hip"])
+def test_other_kernels_use_no_scratch(src, tmp_path_factory):
+    asm = _asm_of(src, tmp_path_factory)
+    assert asm.count(".private_segment_fixed_size:") > 0
+    bad = kernels_with_scratch(asm)
+    assert not bad, f"{len(bad)} kernels with scratch: {bad[:4]}"
