@@ -1927,7 +1927,7 @@ void decode_wide(FaArgs a, int causal) {
     __shared__ WideLds<NTW, RS, D, MODE != MODE_FAST> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.st.ps, sh.st.dims);
     __syncthreads();
-    for_each_piece<MODE == MODE_FAST && D == 128>(a, sh.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
+    for_each_piece<MODE == MODE_FAST>(a, sh.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide<NTW, RS, MODE, D>(a, sh, causal, pc); });
 }
 
 template <int NTW, int RS, int MODE, int D>
@@ -2024,14 +2024,15 @@ __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    // eight pieces per step (a segment rarely has more): their loads are independent, so
-    // the merge costs one memory latency
-    for (int p0 = p_first; p0 <= p_last; p0 += 8) {
-        f32x4 ov[8];
-        float mv[8], lv[8];
-        u32x2 hv[8];
+    // N pieces per step, their loads independent, so a step costs one memory latency: two or
+    // four for the usual segment (no loads beyond its pieces), eight per step beyond
+    auto merge_step = [&](auto NC, int p0) {
+        constexpr int N = decltype(NC)::value;
+        f32x4 ov[N];
+        float mv[N], lv[N];
+        u32x2 hv[N];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < N; ++u) {
             const int p = p0 + u <= p_last ? p0 + u : p_last;
             const float* sl = base + (int64_t)p * a.piece_stride * a.slot_floats;
             hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * (2 * D) + d0 * 2);
@@ -2039,11 +2040,18 @@ __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot
             lv[u] = sl[(int64_t)rows_slot * (D / 2 + 1) + row];
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < N; ++u) {
             const f16x4 h = __builtin_bit_cast(f16x4, hv[u]);
             ov[u] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]} * lv[u];  // back to O = l * (O/l)
             if (p0 + u <= p_last) merge_row<1>(M, L, &o, mv[u], lv[u], &ov[u]);
         }
+    };
+    if (p_last - p_first < 2) {
+        merge_step(std::integral_constant<int, 2>{}, p_first);
+    } else if (p_last - p_first < 4) {
+        merge_step(std::integral_constant<int, 4>{}, p_first);
+    } else {
+        for (int p0 = p_first; p0 <= p_last; p0 += 8) merge_step(std::integral_constant<int, 8>{}, p0);
     }
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;
     const int j = row / a.Gr;
@@ -2092,8 +2100,8 @@ inline FaArgs head_split_args(const FaArgs& a) {
 // explicit-mask and softcap calls of up to 48 rows as well, whose fast calls run decode_d128).
 template <int NTW, int RS, int D, bool FAST_BUILT = true>
 hipError_t launch_wide(const FaArgs& a_in, int mode, int causal, hipStream_t stream) {
-    // the pipelined fast kernel (128-dim heads) with the head-aligned split
-    const FaArgs a = (D == 128 && mode == MODE_FAST) ? head_split_args(a_in) : a_in;
+    // the fast kernels with the head-aligned split
+    const FaArgs a = (mode == MODE_FAST) ? head_split_args(a_in) : a_in;
     if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(RS * wide_lanes<RS, D>() * 64);
     if (mode == MODE_GENERIC)
