@@ -495,13 +495,13 @@ def verify_q8_only(steps: int, warmup: int) -> int:
     return 0
 
 
-def prefill_only(steps: int, warmup: int) -> int:
+def prefill_only(steps: int, warmup: int, q8: bool = False) -> int:
     import sixi_attn as sa
 
     fa = sa.FlashAttnExt()
-    tf, us, _ = time_prefill(fa, max(1, steps), warmup)
-    print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks", "us_two_chunks": round(us, 2),
-                      "TFLOPs": round(tf, 2)}), flush=True)
+    tf, us, wsb = time_prefill(fa, max(1, steps), warmup, kv_type=sa.TYPE_Q8_0 if q8 else None)
+    print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks" + (" over a q8_0 cache" if q8 else ""),
+                      "us_two_chunks": round(us, 2), "TFLOPs": round(tf, 2), "workspace_bytes": wsb}), flush=True)
     return 0
 
 
@@ -510,7 +510,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "layer", "gdn", "verify_q8"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "layer", "gdn", "verify_q8"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -525,8 +525,8 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.workload == "copy":
         return copy_calibration(max(1, args.steps))
-    if args.workload == "prefill":
-        return prefill_only(args.steps, args.warmup)
+    if args.workload in ("prefill", "prefill_q8"):
+        return prefill_only(args.steps, args.warmup, q8=args.workload == "prefill_q8")
     if args.workload == "layer":
         print(json.dumps(time_layer(max(8, args.steps), args.warmup)), flush=True)
         return 0
