@@ -44,9 +44,10 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None):
+def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None, bounded=False):
     """Per-call GPU times (ms) with events on the stream the library launches on.  With `mask`
-    (a ggml f16 KQ mask) the calls take the explicit-mask path instead of w.mask_mode."""
+    (a ggml f16 KQ mask) the calls take the explicit-mask path instead of w.mask_mode;
+    `bounded` sets FLAG_BOUNDED_WORKSPACE."""
     import torch
 
     import sixi_attn as sa
@@ -59,7 +60,7 @@ def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None):
 
     def call():
         fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
-           mask_mode=mode, mask=mask, stream=stream.cuda_stream)
+           mask_mode=mode, mask=mask, stream=stream.cuda_stream, bounded_workspace=bounded)
 
     for _ in range(warmup):
         call()
@@ -118,16 +119,16 @@ def time_paged(fa, w, dev, steps: int, warmup: int) -> dict:
     return res
 
 
-def ws_bytes(fa, w, dev, mask=None) -> int:
-    """sixi_attn_workspace_bytes of a call of workload w (256-dim q8_0 prefill-sized blocks
-    include the f16 staging of the cache)."""
+def ws_bytes(fa, w, dev, mask=None, bounded=False) -> int:
+    """sixi_attn_workspace_bytes of a call of workload w (only 256-dim q8_0 rows that are not
+    16-byte aligned include an f16 staging of the cache)."""
     import torch
 
     import sixi_attn as sa
 
     out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
     p = fa.params(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
-                  mask_mode=w.mask_mode if mask is None else sa.MASK_EXPLICIT, mask=mask)
+                  mask_mode=w.mask_mode if mask is None else sa.MASK_EXPLICIT, mask=mask, bounded_workspace=bounded)
     return int(fa.workspace_bytes(p))
 
 
@@ -248,11 +249,12 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
-def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None, explicit_mask=False):
+def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None, explicit_mask=False, bounded=False):
     """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks).
     kv_type q8_0 runs the same chunks over a q8_0 cache (128-dim heads: tiles converted in LDS;
     256-dim heads: staged as f16 operands per call);
-    explicit_mask hands the causal mask over as a ggml f16 KQ mask (the ggml hook's path)."""
+    explicit_mask hands the causal mask over as a ggml f16 KQ mask (the ggml hook's path);
+    bounded sets FLAG_BOUNDED_WORKSPACE (a 256-dim q8_0 cache converted in LDS, not staged)."""
     import dataclasses
 
     import torch
@@ -270,8 +272,8 @@ def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None, expli
         mask = None
         if explicit_mask:
             mask = torch.from_numpy(wl.kq_mask(dp["k"].shape[1], wp.n_q, wp.kv_len, wp.q_len)).view(torch.float16).cuda()
-        msp, _ = time_calls(fa, wp, dp, steps, warmup, mask=mask)
-        pre.append((wp, msp, ws_bytes(fa, wp, dp)))
+        msp, _ = time_calls(fa, wp, dp, steps, warmup, mask=mask, bounded=bounded)
+        pre.append((wp, msp, ws_bytes(fa, wp, dp, bounded=bounded)))
         del dp
     flops = sum(wp.flops() for wp, _, _ in pre)
     t = sum(msp for _, msp, _ in pre)
@@ -495,12 +497,13 @@ def verify_q8_only(steps: int, warmup: int) -> int:
     return 0
 
 
-def prefill_only(steps: int, warmup: int, q8: bool = False) -> int:
+def prefill_only(steps: int, warmup: int, q8: bool = False, head_dim=None) -> int:
     import sixi_attn as sa
 
     fa = sa.FlashAttnExt()
-    tf, us, wsb = time_prefill(fa, max(1, steps), warmup, kv_type=sa.TYPE_Q8_0 if q8 else None)
-    print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks" + (" over a q8_0 cache" if q8 else ""),
+    tf, us, wsb = time_prefill(fa, max(1, steps), warmup, kv_type=sa.TYPE_Q8_0 if q8 else None, head_dim=head_dim)
+    print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks" + (" over a q8_0 cache" if q8 else "") +
+                      (f", {head_dim}-dim heads" if head_dim else ""),
                       "us_two_chunks": round(us, 2), "TFLOPs": round(tf, 2), "workspace_bytes": wsb}), flush=True)
     return 0
 
@@ -510,7 +513,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "layer", "gdn", "verify_q8"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_d256_q8", "layer", "gdn",
+                                                               "verify_q8"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -525,8 +529,9 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.workload == "copy":
         return copy_calibration(max(1, args.steps))
-    if args.workload in ("prefill", "prefill_q8"):
-        return prefill_only(args.steps, args.warmup, q8=args.workload == "prefill_q8")
+    if args.workload in ("prefill", "prefill_q8", "prefill_d256_q8"):
+        return prefill_only(args.steps, args.warmup, q8=args.workload != "prefill",
+                            head_dim=256 if args.workload == "prefill_d256_q8" else None)
     if args.workload == "layer":
         print(json.dumps(time_layer(max(8, args.steps), args.warmup)), flush=True)
         return 0
@@ -673,6 +678,16 @@ def main() -> int:
             result["configs"]["prefill_d256"] = {"us_two_chunks": round(ud, 2), "TFLOPs": round(td, 2),
                                                  "workspace_bytes": wsd}
             _log(f"prefill 256-dim heads: {ud:.1f} us for 2 chunks, {td:.1f} TFLOP/s")
+            tdq, udq, wsdq = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0,
+                                          head_dim=256)
+            result["configs"]["prefill_d256_q8_0"] = {"us_two_chunks": round(udq, 2), "TFLOPs": round(tdq, 2),
+                                                      "workspace_bytes": wsdq, "path": "f16 staging"}
+            _log(f"prefill 256-dim heads over q8_0 KV: {udq:.1f} us for 2 chunks, {tdq:.1f} TFLOP/s")
+            tdb, udb, wsdb = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0,
+                                          head_dim=256, bounded=True)
+            result["configs"]["prefill_d256_q8_0_bounded"] = {"us_two_chunks": round(udb, 2), "TFLOPs": round(tdb, 2),
+                                                              "workspace_bytes": wsdb, "path": "q8_0 tiles converted in LDS"}
+            _log(f"the same with a bounded workspace: {udb:.1f} us for 2 chunks, {tdb:.1f} TFLOP/s")
             tm, um, wsm = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), explicit_mask=True)
             result["configs"]["prefill_explicit_mask"] = {"us_two_chunks": round(um, 2), "TFLOPs": round(tm, 2),
                                                           "workspace_bytes": wsm}

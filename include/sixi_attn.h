@@ -71,6 +71,17 @@ enum {
     SIXI_E_UNSUPPORTED = -24        /* ErrorCode::UnsupportedHardware (shape/type not built) */
 };
 
+/* sixi_attn_params.flags.  BOUNDED_WORKSPACE: never stage a q8_0 cache as f16 in the
+ * workspace, so the workspace does not grow with the cache.  Without it, prefill-sized
+ * blocks over a 256-dim q8_0 cache stage K, V and Q as f16 operands while that copy takes at
+ * most SIXI_ATTN_STAGE_CAP_BYTES (a separate pass, then the f16 kernel: faster than
+ * converting every tile in LDS, which repeats the conversion for each row block and q-head),
+ * and convert the q8_0 tiles in LDS beyond it.  256-dim q8_0 rows that are not 16-byte
+ * aligned are always staged (the in-LDS path loads rows by 16-byte DMA).  No counterpart in
+ * the reference (ggml's kernels take no workspace). */
+#define SIXI_ATTN_FLAG_BOUNDED_WORKSPACE 1
+#define SIXI_ATTN_STAGE_CAP_BYTES ((size_t)64 << 20)
+
 /* ggml-compatible strided view.  ne[0] is the innermost extent (elements); nb[] are byte
  * strides; for q8_0, nb[0] = 34 (one 32-element block) and a row of ne[0] elements takes
  * ne[0]/32*34 bytes. */
@@ -94,7 +105,7 @@ typedef struct sixi_attn_params {
     const int32_t* kv_len;  /* device [S]: cells cached before the block, or NULL          */
     const int32_t* q_len;   /* device [S]: rows of stream s (<= n_q), or NULL (= n_q)      */
     int32_t mask_mode;      /* SIXI_MASK_*                                                 */
-    int32_t flags;          /* reserved, must be 0                                         */
+    int32_t flags;          /* SIXI_ATTN_FLAG_* bits; 0 by default                         */
     sixi_view mask;         /* EXPLICIT only: f16 [n_kv, >= n_q, 1, 1 or S]                */
     float scale;            /* 1/sqrt(D) for the engine's models                           */
     float max_bias;         /* ALiBi; 0 = off                                              */
@@ -122,9 +133,10 @@ int sixi_attn_forward(const sixi_attn_params* p);
  * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  The call allocates nothing: its scratch is a fixed
  * SIXI_ATTN_NOALLOC_SCRATCH_BYTES array in the library's device code, one per GPU, held
- * until the process ends; `workspace` and `workspace_bytes` are ignored.  A description
- * whose scratch (split-K partials, q8_0 staging) exceeds that size returns
- * SIXI_E_OUT_OF_BOUNDS before any launch.  The scratch needs no initialisation, but every
+ * until the process ends; `workspace` and `workspace_bytes` are ignored.  q8_0 caches are
+ * staged only while the staging fits the scratch (as with SIXI_ATTN_FLAG_BOUNDED_WORKSPACE
+ * beyond that).  A description whose scratch (split-K partials, a q8_0 staging that cannot
+ * be avoided) exceeds that size returns SIXI_E_OUT_OF_BOUNDS before any launch.  The scratch needs no initialisation, but every
  * call on a GPU shares it: calls that may overlap on one GPU (different streams, or
  * threads without ordering) race; order them on one stream. */
 #define SIXI_ATTN_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)

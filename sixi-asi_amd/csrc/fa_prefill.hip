@@ -98,7 +98,6 @@ template <int MODE, int D, int KV>
 __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nrb, int n_cu) {
     using P = PfDim<D>;
     constexpr bool Q8 = KV == SIXI_TYPE_Q8_0;
-    static_assert(!Q8 || D == 128, "q8_0 tiles: 128-dim heads");
     constexpr int GROUPS = P::GROUPS;
     constexpr int kKBytes = P::TILE, kVBytes = P::TILE;
     __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
@@ -297,16 +296,36 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
     auto issue_q8 = [&](int t, int buf) {
         if constexpr (Q8) {
             const int page = t * kBN < sd.nc ? page_id(pages, a, s, (t * kBN) >> 8) : 0;
-            const KvSpan sp = wq >= 2 ? kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, t * kBN, sd.nc, 136, page)
-                                      : kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, t * kBN, sd.nc, 136, page);
+            constexpr int Q8ROW = D / 32 * 34;
+            const KvSpan sp = wq >= 2 ? kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, t * kBN, sd.nc, Q8ROW, page)
+                                      : kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, t * kBN, sd.nc, Q8ROW, page);
             const buf_rsrc rs = make_rsrc_uniform(sp.p, sp.bytes);
             // (the lane offsets are recomputed here, not kept in registers across the tile)
             uint32_t l = (uint32_t)lane;
             asm volatile("" : "+v"(l));
             const uint32_t r0 = 32u * (uint32_t)(wq & 1);
-            const uint32_t v = (r0 + (l >> 5)) * q8nb + 4u * (l & 31);
-            const uint32_t vx = (r0 + (l >> 1)) * q8nb + 128u + 4u * (l & 1);
-            dma_q8rows32_to_lds(rs, v, vx, 2u * q8nb, lds0 + (uint32_t)q8_slice(buf));
+            if constexpr (D == 128) {
+                const uint32_t v = (r0 + (l >> 5)) * q8nb + 4u * (l & 31);
+                const uint32_t vx = (r0 + (l >> 1)) * q8nb + 128u + 4u * (l & 1);
+                dma_q8rows32_to_lds(rs, v, vx, 2u * q8nb, lds0 + (uint32_t)q8_slice(buf));
+            } else {
+                // 272-byte rows (16-byte aligned): 16-byte piece c = 64u + l of the 32 rows --
+                // row c / 17, piece c % 17 -- lands at 16c, so row x occupies bytes 272x ..
+                // 272x + 271 of the slice (the ninth load's upper half runs past the rows,
+                // inside the slice)
+                uint32_t o[9];
+#pragma unroll
+                for (int u = 0; u < 9; ++u) {
+                    const uint32_t c = 64u * (uint32_t)u + l;
+                    o[u] = (r0 + c / 17u) * q8nb + 16u * (c % 17u);
+                }
+                uint32_t o8[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) o8[u] = o[u];
+                const uint32_t dst = lds0 + (uint32_t)q8_slice(buf);
+                dma16x8_to_lds(rs, o8, dst);
+                dma16x1_to_lds(rs, o[8], dst + 8u * 1024u);
+            }
         }
     };
     // this wave's q8_0 rows in f16 buffer BUF (landed) -> f16 rows of the same slice.  Lane
@@ -314,7 +333,49 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
     // dword c < 32 at byte 264(x/2) + 128(x%2) + 4c, dwords 32, 33 at 4224 + 8x, so the 64
     // lanes of each read hit 64 distinct banks -- every read before any write.
     auto convert_q8 = [&](auto BUF) {
-        if constexpr (Q8) {
+        if constexpr (Q8 && D == 256) {
+            constexpr int buf = decltype(BUF)::value;
+            char* sl = lds + q8_slice(buf);
+            // lane (x = l % 32, h = l / 32) takes blocks 4h .. 4h+3 of row x: the 136 bytes at
+            // 272x + 136h (8-byte aligned), all read before any write
+            int lx = lane;
+            asm volatile("" : "+v"(lx));
+            const int x = lx & 31, hx = lx >> 5;
+            const u32x2* src = reinterpret_cast<const u32x2*>(sl + 272 * x + 136 * hx);
+            uint32_t r[34];
+#pragma unroll
+            for (int i = 0; i < 17; ++i) {
+                const u32x2 v2 = src[i];
+                r[2 * i] = v2[0];
+                r[2 * i + 1] = v2[1];
+            }
+            asm volatile("" ::: "memory");
+            // block m at byte 34m: m even -> scale in the low half of dword 17m/2, quants 2 bytes
+            // past the following dwords; m odd -> scale in the high half, quants dword-aligned
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int d0 = (34 * m) >> 2;
+                uint32_t wq8[8];
+                uint16_t dh;
+                if (m & 1) {
+                    dh = (uint16_t)(r[d0] >> 16);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) wq8[i] = r[d0 + 1 + i];
+                } else {
+                    dh = (uint16_t)(r[d0] & 0xffffu);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) wq8[i] = __builtin_amdgcn_alignbyte(r[d0 + i + 1], r[d0 + i], 2);
+                }
+                const int bk = 4 * hx + m;  // block: dims 32bk .. 32bk+31
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const u32x4 f = dequant_q8x8(wq8[2 * k], wq8[2 * k + 1], dh);
+                    const int j = 4 * bk + k;  // 16-byte chunk: dims 8j .. 8j+7
+                    const int pos = wq >= 2 ? 32 * ((j >> 1) ^ (2 * (x & 3))) + 16 * (j & 1) : 16 * (j ^ (x & 15));
+                    *reinterpret_cast<u32x4*>(sl + x * P::ROW + pos) = f;
+                }
+            }
+        } else if constexpr (Q8) {
             constexpr int buf = decltype(BUF)::value;
             char* sl = lds + q8_slice(buf);
             // (addresses and store keys are recomputed here, not kept in registers across the tile)
@@ -637,17 +698,17 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs
     prefill_body<MODE, D, SIXI_TYPE_F16>(a, causal, nrb, n_cu);
 }
 
-// q8_0 KV at 128-dim heads: the same tiles, converted from q8_0 rows in place in LDS
-template <int MODE>
-__global__ __launch_bounds__(kThreads, PfDim<128>::GROUPS) void prefill_q8(FaArgs a, int causal, int nrb, int n_cu) {
-    prefill_body<MODE, 128, SIXI_TYPE_Q8_0>(a, causal, nrb, n_cu);
+// q8_0 KV: the same tiles, converted from q8_0 rows in place in LDS
+template <int MODE, int D>
+__global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_q8(FaArgs a, int causal, int nrb, int n_cu) {
+    prefill_body<MODE, D, SIXI_TYPE_Q8_0>(a, causal, nrb, n_cu);
 }
 
 template <int MODE, int D, int KV>
 void launch_prefill_mode(const FaArgs& a, int causal, int nrb, hipStream_t stream) {
     const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
     if constexpr (KV == SIXI_TYPE_Q8_0)
-        hipLaunchKernelGGL((prefill_q8<MODE>), grid, block, 0, stream, a, causal, nrb, a.P);
+        hipLaunchKernelGGL((prefill_q8<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
     else
         hipLaunchKernelGGL((prefill_f16<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
 }
@@ -674,7 +735,9 @@ hipError_t launch_prefill_d(const FaArgs& a, int mask_mode, hipStream_t stream) 
 
 hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim, hipStream_t stream) {
     if (kv_type == SIXI_TYPE_Q8_0)
-        return head_dim == 128 ? launch_prefill_d<128, SIXI_TYPE_Q8_0>(a, mask_mode, stream) : hipErrorNotSupported;
+        return head_dim == 128   ? launch_prefill_d<128, SIXI_TYPE_Q8_0>(a, mask_mode, stream)
+               : head_dim == 256 ? launch_prefill_d<256, SIXI_TYPE_Q8_0>(a, mask_mode, stream)
+                                 : hipErrorNotSupported;
     if (kv_type != SIXI_TYPE_F16) return hipErrorNotSupported;
     if (head_dim == 128) return launch_prefill_d<128, SIXI_TYPE_F16>(a, mask_mode, stream);
     if (head_dim == 256) return launch_prefill_d<256, SIXI_TYPE_F16>(a, mask_mode, stream);

@@ -67,10 +67,13 @@ void splitk_layout(Plan& pl, int64_t slots) {
     pl.ws_bytes = pl.stage_bytes + align_up(pl.seg_offset + (size_t)segs * 2 * sizeof(int32_t), kWsAlign);
 }
 
-// Resolves and validates a description.  Touches no device memory.
-int resolve(const sixi_attn_params* p, Plan* out) {
+// Resolves and validates a description.  Touches no device memory.  A q8_0 cache is staged
+// as f16 only where the staging takes at most `stage_cap` bytes (or where it cannot be
+// avoided: 256-dim rows that are not 16-byte aligned).
+int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_STAGE_CAP_BYTES) {
     if (!p || !out) return SIXI_E_INVALID_ARGUMENT;
-    if (p->flags != 0) return SIXI_E_INVALID_ARGUMENT;
+    if ((p->flags & ~SIXI_ATTN_FLAG_BOUNDED_WORKSPACE) != 0) return SIXI_E_INVALID_ARGUMENT;
+    if (p->flags & SIXI_ATTN_FLAG_BOUNDED_WORKSPACE) stage_cap = 0;
     const sixi_view &q = p->q, &k = p->k, &v = p->v, &o = p->out;
     if (!q.data || !k.data || !v.data || !o.data) return SIXI_E_INVALID_ARGUMENT;
 
@@ -210,7 +213,8 @@ int resolve(const sixi_attn_params* p, Plan* out) {
     // q8_0 KV runs the split-K kernels in one launch that reads the KV once: at 128-dim heads
     // the 16-cell kernel up to 48 rows (with a mask or softcap: up to 16), the 32-cell q8_0
     // kernel beyond; at 256-dim heads (16-byte aligned rows) the 32-cell q8_0 kernel.  Prefill
-    // blocks at 128-dim heads read q8_0 tiles directly too; only 256-dim prefill is staged.
+    // blocks at 128-dim heads read q8_0 tiles directly (converted in LDS); at 256-dim heads
+    // they are staged as f16 up to stage_cap bytes, beyond it converted in LDS as well.
     pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
         // 256-dim q8_0 rows (272 B) are read by 16-byte LDS-DMA loads: every row must start
@@ -218,25 +222,32 @@ int resolve(const sixi_attn_params* p, Plan* out) {
         auto rows16 = [](const sixi_view& t) {
             return aligned(t.data, 16) && t.nb[1] % 16 == 0 && t.nb[2] % 16 == 0 && t.nb[3] % 16 == 0;
         };
-        if (pl.splitk && (D == 128 || (D == 256 && rows16(k) && rows16(v)))) {
+        const bool dma16 = D == 128 || (D == 256 && rows16(k) && rows16(v));
+        // the f16 staging of K, V and Q (fa_q8_stage.hip) in the workspace
+        int64_t kv_bytes = 0, q_bytes = 0, cells = 0, span = 0;
+        if (!mul_ok(S * Hkv, n_kv, &cells) || !mul_ok(cells, D * 2, &kv_bytes) ||
+            !mul_ok(S * H, n_q, &q_bytes) || !mul_ok(q_bytes, D * 2, &q_bytes) ||
+            !mul_ok(n_kv + sixi::kDecodeTileWide, Hkv * D * 2, &span))
+            return SIXI_E_INTEGER_OVERFLOW;
+        const size_t stage_v = align_up((size_t)kv_bytes, kWsAlign);
+        const size_t stage_q = stage_v + align_up((size_t)kv_bytes, kWsAlign);
+        const size_t stage_bytes = stage_q + align_up((size_t)q_bytes, kWsAlign);
+        if (pl.splitk && dma16) {
             // one launch of the 32-cell q8_0 kernel
-        } else if (!pl.splitk && D == 128) {
+        } else if (!pl.splitk && dma16 && (D == 128 || stage_bytes > stage_cap)) {
             // the prefill kernel converts each tile's q8_0 rows to f16 in LDS
         } else {
-            // prefill-sized blocks at 256-dim heads (and unaligned 256-dim rows): K, V and Q
-            // are staged as f16 operands in the workspace (fa_q8_stage.hip) and the f16 kernels run
+            // K, V and Q staged as f16 operands in the workspace, then the f16 kernels: a
+            // 256-dim prefill-sized block while the copy is small (one pass over the cache
+            // instead of a conversion per row block and q-head), or rows that are not 16-byte
+            // aligned
+            if (span >= (int64_t)UINT32_MAX) return SIXI_E_UNSUPPORTED;
             pl.q8_stage = true;
             pl.kv_type = SIXI_TYPE_F16;
-            int64_t kv_bytes = 0, q_bytes = 0, cells = 0, span = 0;
-            if (!mul_ok(S * Hkv, n_kv, &cells) || !mul_ok(cells, D * 2, &kv_bytes) ||
-                !mul_ok(S * H, n_q, &q_bytes) || !mul_ok(q_bytes, D * 2, &q_bytes) ||
-                !mul_ok(n_kv + sixi::kDecodeTileWide, Hkv * D * 2, &span))
-                return SIXI_E_INTEGER_OVERFLOW;
-            if (span >= (int64_t)UINT32_MAX) return SIXI_E_UNSUPPORTED;
             pl.stage_k = 0;
-            pl.stage_v = align_up((size_t)kv_bytes, kWsAlign);
-            pl.stage_q = pl.stage_v + align_up((size_t)kv_bytes, kWsAlign);
-            pl.stage_bytes = pl.stage_q + align_up((size_t)q_bytes, kWsAlign);
+            pl.stage_v = stage_v;
+            pl.stage_q = stage_q;
+            pl.stage_bytes = stage_bytes;
         }
     }
     if (pl.splitk) {
@@ -361,7 +372,8 @@ int sixi_attn_forward(const sixi_attn_params* p) {
 
 int sixi_attn_forward_noalloc(const sixi_attn_params* p) {
     Plan pl;
-    int rc = resolve(p, &pl);
+    // stage a q8_0 cache only while the staging leaves room in the scratch for the rest
+    int rc = resolve(p, &pl, kScratchBytes / 2);
     if (rc != SIXI_OK) return rc;
     // exact slots for this launch's work-groups, not the workspace bound of any launch
     if (pl.splitk) splitk_layout(pl, (int64_t)pl.a.S * pl.a.Hkv + launch_groups(pl));

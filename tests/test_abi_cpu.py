@@ -98,25 +98,47 @@ def test_workspace_holds_the_launched_slots(D):
 
 def test_q8_prefill_workspace_is_independent_of_the_cache_length():
     """128-dim q8_0 prefill reads the q8_0 tiles itself: the workspace stays a token whatever
-    the cache length (no f16 copy of the cache).  256-dim q8_0 prefill stages K, V and Q as
-    f16, so its workspace grows with the cells."""
+    the cache length (no f16 copy of the cache).  At 256-dim heads the f16 staging is used
+    while it takes at most STAGE_CAP_BYTES and the q8_0 tiles are read directly beyond that,
+    or always with FLAG_BOUNDED_WORKSPACE.  256-dim rows that are not 16-byte aligned are
+    always staged, so that workspace grows with the cells."""
     lib = sa.load_library()
 
-    def ws(**kw):
+    def ws(flags=0, **kw):
+        p = _params(**kw)
+        p.flags = flags
         n = ctypes.c_size_t(0)
-        assert lib.sixi_attn_workspace_bytes(ctypes.byref(_params(**kw)), ctypes.byref(n)) == sa.OK
+        assert lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n)) == sa.OK
         return n.value
 
     sizes = {n_kv: ws(n_q=512, n_kv=n_kv, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 65536, 1 << 20)}
     assert len(set(sizes.values())) == 1 and sizes[1024] <= 4096, sizes
     assert ws(n_q=512, n_kv=65536, kv_type=sa.TYPE_Q8_0, mode=sa.MASK_NONE, kv_len=False) == sizes[1024]
     assert ws(n_q=512, n_kv=1024, kv_type=sa.TYPE_F16) == sizes[1024]
-    d256 = [ws(n_q=512, n_kv=n_kv, D=256, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 65536)]
-    assert d256[1] > d256[0] >= 2 * 2 * 1024 * 4 * 256 * 2
+    token = sizes[1024]
+    d256 = [ws(n_q=512, n_kv=n_kv, D=256, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 4096, 65536, 1 << 20)]
+    # staged (2 streams x 4 heads x n_kv x 512 B for K and for V, plus Q) up to the cap
+    assert 2 * 2 * 4 * 4096 * 512 <= d256[1] <= sa.STAGE_CAP_BYTES and d256[1] > d256[0] > token, d256
+    assert d256[2:] == [token, token], d256
+    bounded = [ws(sa.FLAG_BOUNDED_WORKSPACE, n_q=512, n_kv=n_kv, D=256, kv_type=sa.TYPE_Q8_0)
+               for n_kv in (1024, 65536, 1 << 20)]
+    assert bounded == [token] * 3, bounded
+
+    def ws_unaligned(n_kv):
+        p = _params(n_q=512, n_kv=n_kv, D=256, kv_type=sa.TYPE_Q8_0)
+        for t in (p.k, p.v):  # 4 spare bytes per cell: no row starts 16-byte aligned
+            t.nb[1] = 4 * 272 + 4
+            t.nb[3] = n_kv * t.nb[1]
+        n = ctypes.c_size_t(0)
+        assert lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n)) == sa.OK
+        return n.value
+
+    staged = [ws_unaligned(n_kv) for n_kv in (1024, 65536)]
+    assert staged[1] > staged[0] >= 2 * 2 * 1024 * 4 * 256 * 2
 
 
 @pytest.mark.parametrize("mutate,code", [
-    (lambda p: setattr(p, "flags", 1), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p, "flags", 2), sa.E_INVALID_ARGUMENT),            # unknown flag bit
     (lambda p: setattr(p.q, "data", None), sa.E_INVALID_ARGUMENT),
     (lambda p: p.q.ne.__setitem__(0, 96), sa.E_INVALID_ARGUMENT),          # q/k head dims differ
     (lambda p: p.q.ne.__setitem__(2, 25), sa.E_INVALID_ARGUMENT),          # H % Hkv != 0
@@ -264,7 +286,7 @@ def _prologue_params(S=2, R=16, H=24, Hkv=4, D=256, n_cells=4096, cache_type=sa.
 
 
 @pytest.mark.parametrize("mutate,code", [
-    (lambda p: setattr(p, "flags", 1), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p, "flags", 2), sa.E_INVALID_ARGUMENT),            # unknown flag bit
     (lambda p: setattr(p, "q_norm", None), sa.E_INVALID_ARGUMENT),
     (lambda p: setattr(p.k_cache, "data", None), sa.E_INVALID_ARGUMENT),
     (lambda p: (p.q_out.ne.__setitem__(0, 64), p.qg.ne.__setitem__(0, 128)), sa.E_UNSUPPORTED),   # head of 64

@@ -2,7 +2,9 @@
 32-cell split-K kernel, against the oracle through the C ABI: decode, speculative verify (96 rows
 per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q; the
 prefill kernel for 256-dim heads; q8_0 caches on the 32-cell q8_0 kernel (one lane, up to three
-row groups of two row tiles) and, for prefill-sized blocks, through the f16 staging.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
+row groups of two row tiles) and, for prefill-sized blocks, on the prefill kernel over q8_0 tiles
+converted in LDS (rows that are not 16-byte aligned: through the f16 staging).  Bar: max-abs <=
+2e-3 and rel-L2 <= 1e-3 on the f32 output."""
 import sys
 
 import numpy as np
@@ -30,9 +32,24 @@ def fa():
     return sa.FlashAttnExt()
 
 
-def _run_check(fa, w, label, mask_mode=sa.MASK_BLOCK_CAUSAL, explicit=False):
+def _unaligned_rows(t):
+    """The same q8_0 cache [S, cells, Hkv, 272] with 4 spare bytes after every cell, so that no
+    cell row starts 16-byte aligned (cell stride Hkv * 272 + 4)."""
+    S, cells, Hkv, row = t.shape
+    buf = torch.zeros((S, cells, Hkv * row + 4), dtype=torch.uint8, device=t.device)
+    buf[:, :, :Hkv * row] = t.reshape(S, cells, Hkv * row)
+    return buf[:, :, :Hkv * row].unflatten(2, (Hkv, row))
+
+
+def _run_check(fa, w, label, mask_mode=sa.MASK_BLOCK_CAUSAL, explicit=False, unaligned=False, both=False):
+    """Against the oracle; ``both``: also with FLAG_BOUNDED_WORKSPACE, whose q8_0 prefill
+    converts the q8_0 tiles in LDS instead of staging them as f16 -- the same operands, so the
+    outputs must agree bitwise."""
     host = wl.make_host(w, poison=not explicit)
     dev = wl.to_device(host)
+    if unaligned:
+        dev["k"], dev["v"] = _unaligned_rows(dev["k"]), _unaligned_rows(dev["v"])
+        assert dev["k"].stride(1) % 16 == 4
     out = torch.full((w.S, w.n_q, w.H, w.D), float("nan"), dtype=torch.float32, device="cuda")
     mask = None
     if explicit:
@@ -43,7 +60,15 @@ def _run_check(fa, w, label, mask_mode=sa.MASK_BLOCK_CAUSAL, explicit=False):
     fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=mask_mode, mask=mask)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
-    want = oracle.attention_for_workload(host, w.kv_type)
+    if both:
+        out2 = torch.full_like(out, float("nan"))
+        fa(dev["q"], dev["k"], dev["v"], out2, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=mask_mode,
+           mask=mask, bounded_workspace=True)
+        torch.cuda.synchronize()
+        got2 = out2.cpu().numpy()
+        for s in range(w.S):
+            assert np.array_equal(got[s, :w.q_len[s]], got2[s, :w.q_len[s]]), f"{label}: stream {s}"
+    want = oracle.attention_for_workload(host, w.kv_type, causal=mask_mode != sa.MASK_NONE)
     ql = host["q_len"]
     g = np.concatenate([got[s, :ql[s]].ravel() for s in range(w.S)])
     r = np.concatenate([want[s, :ql[s]].ravel() for s in range(w.S)])
@@ -100,10 +125,49 @@ def test_d256_prefill_explicit_mask(fa):
     ("q8_0 verify, one long stream", [20000], [16], False),     # many pieces
     ("q8_0 verify, explicit mask", [1500, 333], [16, 5], True),
     ("q8_0 decode, explicit mask", [4000], [1], True),
-    ("q8_0 prefill (staged)", [200], [150], False),
+    ("q8_0 prefill", [200], [150], False),
+    ("q8_0 prefill ragged", [3000, 0, 700], [300, 129, 200], False),
+    ("q8_0 prefill, long stream", [5000], [260], False),    # 83 tiles, 20 pages
+    ("q8_0 prefill, explicit mask", [300, 40], [150, 260], True),
 ])
 def test_d256_q8_0(fa, label, kv_len, q_len, explicit):
-    """q8_0 caches of 256-dim heads: split-K calls run the 32-cell q8_0 kernel on one lane,
-    prefill-sized blocks the f16 staging."""
+    """q8_0 caches of 256-dim heads: split-K calls run the 32-cell q8_0 kernel on one lane;
+    prefill-sized blocks stage K, V and Q as f16 (a small cache) or, with
+    FLAG_BOUNDED_WORKSPACE, run the prefill kernel that converts each tile's q8_0 rows in LDS:
+    both against the oracle, and bitwise against each other."""
     w = wl.Workload("d256 q8", 0x51A7_9700 + sum(q_len), len(kv_len), kv_len, q_len, D=256, kv_type=sa.TYPE_Q8_0)
-    _run_check(fa, w, label, explicit=explicit)
+    _run_check(fa, w, label, explicit=explicit, both=True)
+
+
+def test_d256_q8_0_prefill_f16_q_and_no_mask(fa):
+    w = wl.Workload("d256 q8 f16q", 0x51A7_9750, 2, [900, 64], [200, 150], D=256, kv_type=sa.TYPE_Q8_0,
+                    q_type=sa.TYPE_F16)
+    _run_check(fa, w, "q8_0 prefill, f16 Q", both=True)
+    w = wl.Workload("d256 q8 none", 0x51A7_9760, 2, [900, 64], [200, 150], D=256, kv_type=sa.TYPE_Q8_0)
+    _run_check(fa, w, "q8_0 prefill, no mask", mask_mode=sa.MASK_NONE, both=True)
+
+
+def test_d256_q8_0_prefill_beyond_the_staging_cap(fa):
+    """A cache whose f16 staging would exceed STAGE_CAP_BYTES (4 streams x 9000 cells: 147 MB)
+    runs the in-LDS conversion by default: a token workspace, output against the oracle."""
+    w = wl.Workload("d256 q8 long", 0x51A7_9770, 4, [9000, 8800, 100, 4000], [130, 200, 150, 160], D=256,
+                    kv_type=sa.TYPE_Q8_0)
+    host = wl.make_host(w)
+    dev = wl.to_device(host)
+    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    p = fa.params(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"])
+    assert fa.workspace_bytes(p) <= 4096
+    _run_check(fa, w, "q8_0 prefill beyond the staging cap")
+
+
+@pytest.mark.parametrize("label,kv_len,q_len", [
+    ("q8_0 prefill, rows not 16-byte aligned (staged)", [200, 900], [150, 130]),
+    ("q8_0 verify, rows not 16-byte aligned (staged)", [1200, 400], [16, 7]),
+])
+def test_d256_q8_0_unaligned_rows_are_staged(fa, label, kv_len, q_len):
+    """256-dim q8_0 rows that do not start 16-byte aligned cannot come in by 16-byte LDS-DMA
+    loads: such calls stage K, V and Q as f16 operands in the workspace and run the f16
+    kernels."""
+    w = wl.Workload("d256 q8 unaligned", 0x51A7_9780 + sum(q_len), len(kv_len), kv_len, q_len, D=256,
+                    kv_type=sa.TYPE_Q8_0)
+    _run_check(fa, w, label, unaligned=True)

@@ -67,7 +67,8 @@ CASES = [
     ("256-dim verify", sa.TYPE_F16, 256, [600, 1025], [16, 7], 24, 4, False),
     ("q8_0 decode", sa.TYPE_Q8_0, 128, [1500, 256, 3000], [1, 4, 8], 24, 4, False),
     ("q8_0 96 rows (32-cell q8_0 kernel)", sa.TYPE_Q8_0, 128, [900, 300], [16, 16], 24, 4, False),
-    ("q8_0 256-dim (staged)", sa.TYPE_Q8_0, 256, [700, 120], [8, 3], 24, 4, False),
+    ("q8_0 256-dim", sa.TYPE_Q8_0, 256, [700, 120], [8, 3], 24, 4, False),
+    ("q8_0 256-dim prefill rows", sa.TYPE_Q8_0, 256, [300, 0], [130, 200], 24, 4, False),
     ("prefill rows", sa.TYPE_F16, 128, [300, 0], [130, 200], 24, 4, False),
     ("q8_0 prefill rows", sa.TYPE_Q8_0, 128, [300, 0], [130, 200], 24, 4, False),
     ("q8_0 prefill rows, explicit mask", sa.TYPE_Q8_0, 128, [700, 40], [150, 260], 24, 4, True),

@@ -57,7 +57,8 @@ def _ws_bytes(fa, w, dev):
     ("256-dim heads, 48 rows", [6000, 333], [8, 6], 24, 4, 256, sa.TYPE_F16),
     ("q8_0 split-K", [4000, 64], [8, 3], 24, 4, 128, sa.TYPE_Q8_0),
     ("q8_0 head subsets", [4000, 900], [16, 12], 24, 4, 128, sa.TYPE_Q8_0),
-    ("q8_0 staged prefill", [300, 1000], [200, 130], 24, 4, 128, sa.TYPE_Q8_0),
+    ("q8_0 prefill", [300, 1000], [200, 130], 24, 4, 128, sa.TYPE_Q8_0),
+    ("q8_0 prefill, 256-dim heads", [300, 1000], [200, 130], 24, 4, 256, sa.TYPE_Q8_0),
     ("prefill kernel", [100, 1500], [300, 129], 24, 4, 128, sa.TYPE_F16),
 ])
 def test_nan_filled_workspace_changes_nothing(fa, label, kv_len, q_len, H, Hkv, D, kv_type):

@@ -4,9 +4,9 @@ The launcher runs G * q_len rows per kv-head group as 16-row tiles: 1, 2 or 3 ti
 16-cell kernel (128-dim heads), 4 and 6 tiles (5 runs as 6) on the 32-cell kernel, and at
 256-dim heads 1, 2, 4 (3 runs as 4) and 6 tiles.  Each row count runs twice: as one long
 stream, whose segments split into many pieces (the piece-parallel merge), and as a ragged batch
-of short streams (the row-block merge).  q8_0 caches cover the q8_0 split-K kernel (<= 48
-rows), its launches over head subsets (more rows) and the f16 staging (256-dim heads).  Every
-row of every stream is compared.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output.
+of short streams (the row-block merge).  q8_0 caches cover the 16-cell q8_0 kernel (<= 48 rows)
+and the 32-cell q8_0 kernel (more rows; every row count at 256-dim heads).  Every row of every
+stream is compared.  Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the f32 output.
 """
 import sys
 

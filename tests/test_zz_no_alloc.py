@@ -90,6 +90,22 @@ def test_noalloc_q8_0_head_subsets():
     _against_oracle(w, h, got)
 
 
+def test_noalloc_q8_0_prefill_at_256_dims_converts_in_lds():
+    """A 256-dim q8_0 prefill whose f16 staging (2 streams x 7000 cells: 57 MB) would not fit
+    the fixed scratch: the no-allocation call converts the q8_0 tiles in LDS instead, while
+    sixi_attn_forward stages them (under its cap); the two give the same operands, so the
+    outputs agree bitwise."""
+    fa = sa.FlashAttnExt()
+    w = wl.Workload("noalloc q8 d256 prefill", 0x51A7_C200, 2, [6800, 5000], [200, 130], D=256,
+                    kv_type=sa.TYPE_Q8_0)
+    _say("no-alloc: q8_0 prefill, 256-dim heads, staging beyond the scratch")
+    h = wl.make_host(w, poison=True)
+    ref, got = _both(fa, w, h)
+    for s in range(w.S):
+        assert np.array_equal(ref[s, :w.q_len[s]], got[s, :w.q_len[s]]), s
+    _against_oracle(w, h, got)
+
+
 def test_noalloc_rejects_a_scratch_beyond_the_fixed_size():
     """512 streams of 256-dim heads at 96 rows per group need (2048 + groups) slots of 49920 B,
     more than the fixed scratch: rejected before any launch, output untouched."""
