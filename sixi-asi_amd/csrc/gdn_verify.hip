@@ -9,6 +9,11 @@
 // owns the Hd x K state of one (stream, group) in registers for the whole block, so the state is
 // read once and written once (at the snapshot row), and each token costs 3 Hd K FMAs on chip.
 //
+// Two work-groups share each (stream, group), each owning half of the HD state rows (the rows
+// update independently; q, k, alpha and beta are staged by both): 94 instead of 136 registers at
+// 128 x 128, five waves per SIMD instead of three, so more work-groups' state loads overlap other
+// work-groups' token steps (Qwen verify batch 79 -> 68 us; a four-way split measured slower).
+//
 // Mapping (256 threads): a thread holds R consecutive state rows x C = 16 consecutive columns;
 // the TPR = K/16 lanes that share the rows form a row group (adjacent lanes), whose partial
 // dot products are summed by DPP lane moves (ds_bpermute shuffles measured 94 against 83 us).  The block's tokens are staged through LDS TC at a
@@ -32,12 +37,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kC = 16;   // state columns per thread
 constexpr int kTC = 16;  // tokens staged per pass
 
-template <int K, int HD>
+// SPLIT work-groups share the HD rows of one (stream, group) state: the delta rule updates
+// every row from its own values and the shared k, q, so the rows are independent.
+template <int K, int HD, int SPLIT>
 struct GdnShape {
     static constexpr int TPR = K / kC;         // lanes per row group
     static constexpr int GROUPS = 256 / TPR;   // row groups per block
-    static constexpr int R = HD / GROUPS;      // state rows per thread
-    static_assert(R >= 1 && GROUPS * R == HD, "shape");
+    static constexpr int R = HD / SPLIT / GROUPS;  // state rows per thread
+    static_assert(R >= 1 && GROUPS * R * SPLIT == HD, "shape");
 };
 
 // DPP lane moves (GFX9 encodings): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror (lane i of
@@ -58,18 +65,21 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-template <int K, int HD, bool DECAY_FIRST>
+template <int K, int HD, int SPLIT, bool DECAY_FIRST>
 __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
-    using Sh = GdnShape<K, HD>;
+    using Sh = GdnShape<K, HD, SPLIT>;
     constexpr int R = Sh::R, TPR = Sh::TPR;
+    constexpr int HR = HD / SPLIT;  // state rows of this work-group
     __shared__ f32x4 lq[kTC][K / 4], lk[kTC][K / 4];
-    __shared__ float lv[kTC][HD], la[kTC], lb[kTC];
+    __shared__ float lv[kTC][HR], la[kTC], lb[kTC];
 
-    const int g = (int)(blockIdx.x % (unsigned)a.G);
-    const int s = (int)(blockIdx.x / (unsigned)a.G);
+    const int g = (int)((blockIdx.x / SPLIT) % (unsigned)a.G);
+    const int s = (int)((blockIdx.x / SPLIT) / (unsigned)a.G);
+    const int hr0 = (int)(blockIdx.x % SPLIT) * HR;  // first state row of the work-group
     const int tid = threadIdx.x;
     const int part = tid % TPR;           // column block: columns part*16 .. part*16+15
-    const int row0 = (tid / TPR) * R;     // first state row of the thread
+    const int rw = (tid / TPR) * R;       // first state row of the thread, in the work-group's rows
+    const int row0 = hr0 + rw;            // ... in the state
     int ql = a.q_len ? a.q_len[s] : a.n_rows;
     ql = ql < 0 ? 0 : (ql > a.n_rows ? a.n_rows : ql);
     int snap = a.snap ? a.snap[s] : ql;
@@ -106,10 +116,10 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
             const int64_t offk = (int64_t)g * a.k_nb1 + (int64_t)(t0 + t) * a.k_nb2 + (int64_t)s * a.k_nb3 + 16 * c;
             lk[t][c] = *reinterpret_cast<const f32x4*>(a.k + offk);
         }
-        for (int i = tid; i < nt * (HD / 4); i += 256) {
-            const int t = i / (HD / 4), c = i % (HD / 4);
+        for (int i = tid; i < nt * (HR / 4); i += 256) {
+            const int t = i / (HR / 4), c = i % (HR / 4);
             const f32x4 x = *reinterpret_cast<const f32x4*>(a.v + (int64_t)g * a.v_nb1 + (int64_t)(t0 + t) * a.v_nb2 +
-                                                            (int64_t)s * a.v_nb3 + 16 * c);
+                                                            (int64_t)s * a.v_nb3 + 4 * hr0 + 16 * c);
 #pragma unroll
             for (int e = 0; e < 4; ++e) lv[t][4 * c + e] = x[e];
         }
@@ -140,7 +150,7 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
                 for (int c = 0; c < kC; ++c) sk += st[r][c] * kv[c];
                 sk = group_sum<TPR>(sk);
                 if (DECAY_FIRST) sk *= al;
-                const float delta = be * (lv[t][row0 + r] - sk);
+                const float delta = be * (lv[t][rw + r] - sk);
                 float yv = 0.0f;
 #pragma unroll
                 for (int c = 0; c < kC; ++c) {
@@ -163,14 +173,19 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
     }
 }
 
+template <int K, int HD, int SPLIT>
+hipError_t launch_split(const GdnArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)((int64_t)a.S * a.G * SPLIT)), block(256);
+    if (a.decay_first)
+        hipLaunchKernelGGL((gdn_verify_kernel<K, HD, SPLIT, true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((gdn_verify_kernel<K, HD, SPLIT, false>), grid, block, 0, stream, a);
+    return hipGetLastError();
+}
 template <int K, int HD>
 hipError_t launch_shape(const GdnArgs& a, hipStream_t stream) {
-    const dim3 grid((unsigned)((int64_t)a.S * a.G)), block(256);
-    if (a.decay_first)
-        hipLaunchKernelGGL((gdn_verify_kernel<K, HD, true>), grid, block, 0, stream, a);
-    else
-        hipLaunchKernelGGL((gdn_verify_kernel<K, HD, false>), grid, block, 0, stream, a);
-    return hipGetLastError();
+    if constexpr (HD / (256 / (K / kC)) >= 2) return launch_split<K, HD, 2>(a, stream);
+    else return launch_split<K, HD, 1>(a, stream);
 }
 
 }  // namespace
