@@ -1727,8 +1727,30 @@ __device__ __forceinline__ void decode_piece_wide_q8(const FaArgs& a, WideQ8Lds<
     auto convert = [&](int i) {
         const uint32_t* src = q8ring + (size_t)(i % NSQ) * (SLOTB / 4);
         char* dst = reinterpret_cast<char*>(f16buf + (size_t)(i & 1) * (W::SLOT / 16));
-        if (rg == 0) q8_step_to_f16<false, D>(src, dst, lane);
-        if (rg == (RS == 1 ? 0 : 1)) q8_step_to_f16<true, D>(src + STEP / 4, dst + 32 * W::ROW, lane);
+        if constexpr (RS == 3 && D == 256) {
+            // three row groups: the eight passes (K blocks 4h + m, m < 4, then V's) go round robin
+            // over them (3, 3 and 2 passes) instead of four each to row groups 0 and 1 -- the step
+            // waits for the slowest wave.  Every wave's loads of the step landed before the barrier
+            // that precedes this conversion, so any wave may convert K or V.
+            const int x = lane & 31, h = lane >> 5;
+            const uint32_t* sv = src + STEP / 4;
+            char* dv = dst + 32 * W::ROW;
+            if (rg == 0) {
+                q8_block_to_f16<false, 0, D>(src, dst, x, h);
+                q8_block_to_f16<false, 3, D>(src, dst, x, h);
+                q8_block_to_f16<true, 2, D>(sv, dv, x, h);
+            } else if (rg == 1) {
+                q8_block_to_f16<false, 1, D>(src, dst, x, h);
+                q8_block_to_f16<true, 0, D>(sv, dv, x, h);
+                q8_block_to_f16<true, 3, D>(sv, dv, x, h);
+            } else {
+                q8_block_to_f16<false, 2, D>(src, dst, x, h);
+                q8_block_to_f16<true, 1, D>(sv, dv, x, h);
+            }
+        } else {
+            if (rg == 0) q8_step_to_f16<false, D>(src, dst, lane);
+            if (rg == (RS == 1 ? 0 : 1)) q8_step_to_f16<true, D>(src + STEP / 4, dst + 32 * W::ROW, lane);
+        }
     };
     constexpr int LPW = (RS == 1 ? 2 : 1) * (Q::LOADS + (GEN ? 1 : 0));
     const int n_plain = min(max((t_full - tb) / TL, 0), (te - tb) / TL);
