@@ -18,7 +18,9 @@ same inputs.
 
 `--workload copy` instead times a plain 1 GiB device copy: the calibration run for the HBM
 byte counters (FETCH_SIZE / WRITE_SIZE) used in the traffic figures.  `--workload prefill`
-times only the chunked causal prefill (two 2048-row chunks), for profiling that kernel.
+times only the chunked causal prefill (two 2048-row chunks), for profiling that kernel;
+`prefill_q8` and `prefill_d256_q8` the same over a q8_0 cache (128- and 256-dim heads; f16
+staging), and their `_bounded` forms with FLAG_BOUNDED_WORKSPACE (q8_0 tiles converted in LDS).
 """
 from __future__ import annotations
 
@@ -497,13 +499,14 @@ def verify_q8_only(steps: int, warmup: int) -> int:
     return 0
 
 
-def prefill_only(steps: int, warmup: int, q8: bool = False, head_dim=None) -> int:
+def prefill_only(steps: int, warmup: int, q8: bool = False, head_dim=None, bounded: bool = False) -> int:
     import sixi_attn as sa
 
     fa = sa.FlashAttnExt()
-    tf, us, wsb = time_prefill(fa, max(1, steps), warmup, kv_type=sa.TYPE_Q8_0 if q8 else None, head_dim=head_dim)
+    tf, us, wsb = time_prefill(fa, max(1, steps), warmup, kv_type=sa.TYPE_Q8_0 if q8 else None, head_dim=head_dim,
+                               bounded=bounded)
     print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks" + (" over a q8_0 cache" if q8 else "") +
-                      (f", {head_dim}-dim heads" if head_dim else ""),
+                      (f", {head_dim}-dim heads" if head_dim else "") + (", bounded workspace" if bounded else ""),
                       "us_two_chunks": round(us, 2), "TFLOPs": round(tf, 2), "workspace_bytes": wsb}), flush=True)
     return 0
 
@@ -513,8 +516,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_d256_q8", "layer", "gdn",
-                                                               "verify_q8"])
+    ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_q8_bounded",
+                                                               "prefill_d256_q8", "prefill_d256_q8_bounded", "layer",
+                                                               "gdn", "verify_q8"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -529,9 +533,10 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.workload == "copy":
         return copy_calibration(max(1, args.steps))
-    if args.workload in ("prefill", "prefill_q8", "prefill_d256_q8"):
+    if args.workload.startswith("prefill"):
         return prefill_only(args.steps, args.warmup, q8=args.workload != "prefill",
-                            head_dim=256 if args.workload == "prefill_d256_q8" else None)
+                            head_dim=256 if "d256" in args.workload else None,
+                            bounded=args.workload.endswith("_bounded"))
     if args.workload == "layer":
         print(json.dumps(time_layer(max(8, args.steps), args.warmup)), flush=True)
         return 0
@@ -672,8 +677,13 @@ def main() -> int:
             _log(f"prefill: {us:.1f} us for 2 chunks, {tf:.1f} TFLOP/s")
             tq, uq, wsq = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0)
             result["configs"]["prefill_q8_0"] = {"us_two_chunks": round(uq, 2), "TFLOPs": round(tq, 2),
-                                                 "workspace_bytes": wsq}
+                                                 "workspace_bytes": wsq, "path": "f16 staging"}
             _log(f"prefill q8_0 KV: {uq:.1f} us for 2 chunks, {tq:.1f} TFLOP/s")
+            tqb, uqb, wsqb = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), kv_type=sa.TYPE_Q8_0,
+                                          bounded=True)
+            result["configs"]["prefill_q8_0_bounded"] = {"us_two_chunks": round(uqb, 2), "TFLOPs": round(tqb, 2),
+                                                         "workspace_bytes": wsqb, "path": "q8_0 tiles converted in LDS"}
+            _log(f"the same with a bounded workspace: {uqb:.1f} us for 2 chunks, {tqb:.1f} TFLOP/s")
             td, ud, wsd = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), head_dim=256)
             result["configs"]["prefill_d256"] = {"us_two_chunks": round(ud, 2), "TFLOPs": round(td, 2),
                                                  "workspace_bytes": wsd}

@@ -73,9 +73,9 @@ enum {
 
 /* sixi_attn_params.flags.  BOUNDED_WORKSPACE: never stage a q8_0 cache as f16 in the
  * workspace, so the workspace does not grow with the cache.  Without it, prefill-sized
- * blocks over a 256-dim q8_0 cache stage K, V and Q as f16 operands while that copy takes at
- * most SIXI_ATTN_STAGE_CAP_BYTES (a separate pass, then the f16 kernel: faster than
- * converting every tile in LDS, which repeats the conversion for each row block and q-head),
+ * blocks over a q8_0 cache stage K, V and Q as f16 operands while that copy takes at most
+ * SIXI_ATTN_STAGE_CAP_BYTES (a separate pass, then the f16 kernel: faster than converting
+ * every tile in LDS, which repeats the conversion in every work-group that reads the tile),
  * and convert the q8_0 tiles in LDS beyond it.  256-dim q8_0 rows that are not 16-byte
  * aligned are always staged (the in-LDS path loads rows by 16-byte DMA).  No counterpart in
  * the reference (ggml's kernels take no workspace). */

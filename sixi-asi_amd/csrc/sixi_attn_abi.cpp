@@ -213,8 +213,9 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
     // q8_0 KV runs the split-K kernels in one launch that reads the KV once: at 128-dim heads
     // the 16-cell kernel up to 48 rows (with a mask or softcap: up to 16), the 32-cell q8_0
     // kernel beyond; at 256-dim heads (16-byte aligned rows) the 32-cell q8_0 kernel.  Prefill
-    // blocks at 128-dim heads read q8_0 tiles directly (converted in LDS); at 256-dim heads
-    // they are staged as f16 up to stage_cap bytes, beyond it converted in LDS as well.
+    // blocks are staged as f16 up to stage_cap bytes (one pass over the cache, then the f16
+    // kernel: faster than converting every tile in each work-group that reads it), beyond it the
+    // prefill kernel reads the q8_0 tiles and converts them in LDS.
     pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
         // 256-dim q8_0 rows (272 B) are read by 16-byte LDS-DMA loads: every row must start
@@ -234,12 +235,12 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
         const size_t stage_bytes = stage_q + align_up((size_t)q_bytes, kWsAlign);
         if (pl.splitk && dma16) {
             // one launch of the 32-cell q8_0 kernel
-        } else if (!pl.splitk && dma16 && (D == 128 || stage_bytes > stage_cap)) {
+        } else if (!pl.splitk && dma16 && stage_bytes > stage_cap) {
             // the prefill kernel converts each tile's q8_0 rows to f16 in LDS
         } else {
             // K, V and Q staged as f16 operands in the workspace, then the f16 kernels: a
-            // 256-dim prefill-sized block while the copy is small (one pass over the cache
-            // instead of a conversion per row block and q-head), or rows that are not 16-byte
+            // prefill-sized block while the copy is small (one pass over the cache instead of a
+            // conversion per work-group that reads a tile), or 256-dim rows that are not 16-byte
             // aligned
             if (span >= (int64_t)UINT32_MAX) return SIXI_E_UNSUPPORTED;
             pl.q8_stage = true;

@@ -97,11 +97,10 @@ def test_workspace_holds_the_launched_slots(D):
 
 
 def test_q8_prefill_workspace_is_independent_of_the_cache_length():
-    """128-dim q8_0 prefill reads the q8_0 tiles itself: the workspace stays a token whatever
-    the cache length (no f16 copy of the cache).  At 256-dim heads the f16 staging is used
-    while it takes at most STAGE_CAP_BYTES and the q8_0 tiles are read directly beyond that,
-    or always with FLAG_BOUNDED_WORKSPACE.  256-dim rows that are not 16-byte aligned are
-    always staged, so that workspace grows with the cells."""
+    """q8_0 prefill stages K, V and Q as f16 while that copy takes at most STAGE_CAP_BYTES and
+    reads the q8_0 tiles itself beyond it (a token workspace, whatever the cache length), or
+    always with FLAG_BOUNDED_WORKSPACE.  256-dim rows that are not 16-byte aligned are always
+    staged, so that workspace grows with the cells."""
     lib = sa.load_library()
 
     def ws(flags=0, **kw):
@@ -111,11 +110,15 @@ def test_q8_prefill_workspace_is_independent_of_the_cache_length():
         assert lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n)) == sa.OK
         return n.value
 
-    sizes = {n_kv: ws(n_q=512, n_kv=n_kv, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 65536, 1 << 20)}
-    assert len(set(sizes.values())) == 1 and sizes[1024] <= 4096, sizes
-    assert ws(n_q=512, n_kv=65536, kv_type=sa.TYPE_Q8_0, mode=sa.MASK_NONE, kv_len=False) == sizes[1024]
-    assert ws(n_q=512, n_kv=1024, kv_type=sa.TYPE_F16) == sizes[1024]
-    token = sizes[1024]
+    token = ws(n_q=512, n_kv=1024, kv_type=sa.TYPE_F16)
+    assert token <= 4096
+    d128 = [ws(n_q=512, n_kv=n_kv, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 8192, 65536, 1 << 20)]
+    # staged (2 streams x 4 heads x n_kv x 256 B for K and for V, plus Q) up to the cap
+    assert 2 * 2 * 4 * 8192 * 256 <= d128[1] <= sa.STAGE_CAP_BYTES and d128[1] > d128[0] > token, d128
+    assert d128[2:] == [token, token], d128
+    assert ws(n_q=512, n_kv=65536, kv_type=sa.TYPE_Q8_0, mode=sa.MASK_NONE, kv_len=False) == token
+    assert [ws(sa.FLAG_BOUNDED_WORKSPACE, n_q=512, n_kv=n_kv, kv_type=sa.TYPE_Q8_0)
+            for n_kv in (1024, 65536)] == [token, token]
     d256 = [ws(n_q=512, n_kv=n_kv, D=256, kv_type=sa.TYPE_Q8_0) for n_kv in (1024, 4096, 65536, 1 << 20)]
     # staged (2 streams x 4 heads x n_kv x 512 B for K and for V, plus Q) up to the cap
     assert 2 * 2 * 4 * 4096 * 512 <= d256[1] <= sa.STAGE_CAP_BYTES and d256[1] > d256[0] > token, d256

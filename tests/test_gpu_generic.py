@@ -104,3 +104,14 @@ def test_generic_modes_against_the_oracle(fa, label, kv_type, D, kv_len, q_len, 
     met = oracle.diff_metrics(r, g)
     _say(f"{label}: max_abs={met['max_abs']:.3e} rel_l2={met['rel_l2']:.3e}")
     assert met["max_abs"] <= MAX_ABS and met["rel_l2"] <= REL_L2, met
+    if kv_type == sa.TYPE_Q8_0:
+        # the q8_0 tiles converted in LDS instead of a staged f16 copy (prefill-sized blocks):
+        # the same operands, the same output bit for bit
+        out2 = torch.full_like(out, float("nan"))
+        fa(dev["q"], dev["k"], dev["v"], out2, kv_len=dev["kv_len"], q_len=dev["q_len"],
+           mask_mode=sa.MASK_EXPLICIT, mask=mask_dev, max_bias=max_bias, logit_softcap=softcap,
+           bounded_workspace=True)
+        torch.cuda.synchronize()
+        got2 = out2.cpu().numpy()
+        for s in range(w.S):
+            assert np.array_equal(got[s, :q_len[s]], got2[s, :q_len[s]]), (label, s)

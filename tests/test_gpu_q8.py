@@ -32,10 +32,10 @@ def fa():
     return sa.FlashAttnExt()
 
 
-def _run(fa, w, dev, mask_mode=sa.MASK_BLOCK_CAUSAL, mask=None, k=None, v=None):
+def _run(fa, w, dev, mask_mode=sa.MASK_BLOCK_CAUSAL, mask=None, k=None, v=None, bounded_workspace=False):
     out = torch.full((w.S, w.n_q, w.H, w.D), float("nan"), dtype=torch.float32, device="cuda")
     fa(dev["q"], dev["k"] if k is None else k, dev["v"] if v is None else v, out, kv_len=dev["kv_len"],
-       q_len=dev["q_len"], mask_mode=mask_mode, mask=mask)
+       q_len=dev["q_len"], mask_mode=mask_mode, mask=mask, bounded_workspace=bounded_workspace)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
@@ -130,15 +130,21 @@ def test_q8_more_than_48_rows(fa, kv_len, q_len, H, Hkv):
     ("q8 64 rows of one head", [700, 90], [64, 49], 4, 4, sa.TYPE_F32),     # G = 1: 32-cell q8_0 kernel
 ])
 def test_q8_prefill_blocks(fa, name, kv_len, q_len, H, Hkv, q_type):
-    """Blocks beyond the q8_0 split-K kernels: the prefill kernel moves each tile's q8_0 rows
-    into LDS and converts them to f16 there (no staging in the workspace)."""
+    """Blocks beyond the q8_0 split-K kernels: K, V and Q staged as f16 in the workspace (a
+    small cache), and with FLAG_BOUNDED_WORKSPACE the prefill kernel that moves each tile's
+    q8_0 rows into LDS and converts them to f16 there -- the same operands, so the two agree
+    bitwise."""
     _say(f"{name}: kv_len {kv_len} q_len {q_len} H {H} Hkv {Hkv} q_type {q_type}")
     w = wl.Workload("q8_prefill", 0x51A7_7100 + sum(q_len), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv,
                     kv_type=sa.TYPE_Q8_0, q_type=q_type)
     host = wl.make_host(w, poison=True)
     dev = wl.to_device(host)
     streams = [s for s in range(w.S) if q_len[s] > 0]
-    _check(w, host, _run(fa, w, dev), streams, name)
+    got = _run(fa, w, dev)
+    _check(w, host, got, streams, name)
+    in_lds = _run(fa, w, dev, bounded_workspace=True)
+    for s in streams:
+        assert np.array_equal(got[s, :q_len[s]], in_lds[s, :q_len[s]]), (name, s)
 
 
 def test_q8_prefill_explicit_mask(fa):
@@ -152,3 +158,6 @@ def test_q8_prefill_explicit_mask(fa):
     _say("q8 prefill, explicit mask")
     got = _run(fa, w, dev, mask_mode=sa.MASK_EXPLICIT, mask=dmask)
     _check(w, host, got, list(range(w.S)), "q8 prefill explicit mask")
+    in_lds = _run(fa, w, dev, mask_mode=sa.MASK_EXPLICIT, mask=dmask, bounded_workspace=True)
+    for s in range(w.S):
+        assert np.array_equal(got[s, :w.q_len[s]], in_lds[s, :w.q_len[s]]), s
