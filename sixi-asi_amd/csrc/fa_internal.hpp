@@ -59,6 +59,8 @@ struct FaArgs {
     int32_t seg_cost;      // tiles' worth of work charged to each segment in the split
     int64_t slot_floats;   // floats per partial slot
     int32_t* seg_pieces;   // per segment: logical work-groups of its first and last piece
+    int32_t q_q8;          // prefill over an f16-staged q8_0 cache: convert Q to the q8_0 dot type
+                           // in the kernel (ggml's rule), as the q8_0 kernels do
 };
 
 // q8_0 KV at 256-dim heads beyond the q8_0 kernel (fa_q8_stage.hip): K, V and Q staged as dense f16 rows in
@@ -78,7 +80,7 @@ struct Q8StageArgs {
     const int32_t* q_len;
     int32_t S, H, Hkv, n_q, D;
     int64_t n_kv;
-    char *k16, *v16, *q16;
+    char *k16, *v16, *q16;  // q16 null: Q is not staged (the prefill kernel converts it)
 };
 
 // Host-side launchers (defined in the .hip files).  hipErrorNotSupported = not built.

@@ -94,10 +94,13 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int MODE, int D, int KV>
+// QQ8: Q goes through ggml's conversion to the q8_0 dot type (a q8_0 cache, read as q8_0 tiles or
+// staged as f16 rows).
+template <int MODE, int D, int KV, bool QQ8>
 __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nrb, int n_cu) {
     using P = PfDim<D>;
     constexpr bool Q8 = KV == SIXI_TYPE_Q8_0;
+    static_assert(QQ8 || !Q8, "q8_0 tiles take a q8_0-converted Q");
     constexpr int GROUPS = P::GROUPS;
     constexpr int kKBytes = P::TILE, kVBytes = P::TILE;
     __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
@@ -145,7 +148,7 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
     // ---- Q^T B operands in registers: lane l -> row j, dims 16ks + 8*hl .. +7 ----
     // (every load issued before any is used; rows past the block read its first row)
     f16x8 qop[P::KS];
-    if constexpr (Q8) {
+    if constexpr (QQ8) {
         // ggml's conversion of Q to the q8_0 dot type: per 32-dim block (ks = 2bq, 2bq + 1 of
         // lanes l and l^32) d = amax/127, q = round-half-away(x * 127/amax) clamped to +-127,
         // and the MFMA takes f16(q * f16(d))
@@ -695,13 +698,19 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
 
 template <int MODE, int D>
 __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs a, int causal, int nrb, int n_cu) {
-    prefill_body<MODE, D, SIXI_TYPE_F16>(a, causal, nrb, n_cu);
+    prefill_body<MODE, D, SIXI_TYPE_F16, false>(a, causal, nrb, n_cu);
+}
+
+// f16 rows staged from a q8_0 cache: Q converted to the q8_0 dot type in the kernel
+template <int MODE, int D>
+__global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16_qq8(FaArgs a, int causal, int nrb, int n_cu) {
+    prefill_body<MODE, D, SIXI_TYPE_F16, true>(a, causal, nrb, n_cu);
 }
 
 // q8_0 KV: the same tiles, converted from q8_0 rows in place in LDS
 template <int MODE, int D>
 __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_q8(FaArgs a, int causal, int nrb, int n_cu) {
-    prefill_body<MODE, D, SIXI_TYPE_Q8_0>(a, causal, nrb, n_cu);
+    prefill_body<MODE, D, SIXI_TYPE_Q8_0, true>(a, causal, nrb, n_cu);
 }
 
 template <int MODE, int D, int KV>
@@ -709,6 +718,8 @@ void launch_prefill_mode(const FaArgs& a, int causal, int nrb, hipStream_t strea
     const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
     if constexpr (KV == SIXI_TYPE_Q8_0)
         hipLaunchKernelGGL((prefill_q8<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
+    else if (a.q_q8)
+        hipLaunchKernelGGL((prefill_f16_qq8<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
     else
         hipLaunchKernelGGL((prefill_f16<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
 }

@@ -27,13 +27,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-__global__ __launch_bounds__(256) void q8_kv_to_f16(Q8StageArgs a, int which) {
+// K (blocks 0 .. g-1) and V (blocks g .. 2g-1) in one launch
+__global__ __launch_bounds__(256) void q8_kv_to_f16(Q8StageArgs a, unsigned g) {
+    const int which = blockIdx.x >= g ? 1 : 0;
     const char* src = which ? a.v : a.k;
     const int64_t nb1 = which ? a.v_nb1 : a.k_nb1, nb2 = which ? a.v_nb2 : a.k_nb2, nb3 = which ? a.v_nb3 : a.k_nb3;
     char* dst = which ? a.v16 : a.k16;
     const int nb = a.D / 32;  // q8_0 blocks per head row
     const int64_t n = (int64_t)a.S * a.n_kv * a.Hkv * nb;
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i = (int64_t)(blockIdx.x - (which ? g : 0u)) * blockDim.x + threadIdx.x;
     if (i >= n) return;
     const int b = (int)(i % nb);
     int64_t r = i / nb;
@@ -128,10 +130,9 @@ hipError_t launch_q8_stage(const Q8StageArgs& a, hipStream_t stream) {
     const int64_t nq = (int64_t)a.S * a.n_q * a.H * (a.D / 32);
     if (nkv > 0) {
         const unsigned g = (unsigned)((nkv + 255) / 256);
-        hipLaunchKernelGGL(q8_kv_to_f16, dim3(g), dim3(256), 0, stream, a, 0);
-        hipLaunchKernelGGL(q8_kv_to_f16, dim3(g), dim3(256), 0, stream, a, 1);
+        hipLaunchKernelGGL(q8_kv_to_f16, dim3(2 * g), dim3(256), 0, stream, a, g);
     }
-    if (nq > 0) hipLaunchKernelGGL(q8_q_to_f16, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, stream, a);
+    if (nq > 0 && a.q16) hipLaunchKernelGGL(q8_q_to_f16, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -230,9 +230,10 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
             !mul_ok(S * H, n_q, &q_bytes) || !mul_ok(q_bytes, D * 2, &q_bytes) ||
             !mul_ok(n_kv + sixi::kDecodeTileWide, Hkv * D * 2, &span))
             return SIXI_E_INTEGER_OVERFLOW;
+        // (prefill converts Q in the kernel: only split-K calls stage it)
         const size_t stage_v = align_up((size_t)kv_bytes, kWsAlign);
         const size_t stage_q = stage_v + align_up((size_t)kv_bytes, kWsAlign);
-        const size_t stage_bytes = stage_q + align_up((size_t)q_bytes, kWsAlign);
+        const size_t stage_bytes = stage_q + (pl.splitk ? align_up((size_t)q_bytes, kWsAlign) : 0);
         if (pl.splitk && dma16) {
             // one launch of the 32-cell q8_0 kernel
         } else if (!pl.splitk && dma16 && stage_bytes > stage_cap) {
@@ -311,12 +312,16 @@ int run(Plan& pl, char* ws, hipStream_t stream) {
         st.pt = a.pt; st.pt_stride = a.pt_stride; st.n_pages = a.n_pages;
         st.kv_len = a.kv_len; st.q_len = a.q_len;
         st.S = a.S; st.H = a.H; st.Hkv = a.Hkv; st.n_q = a.n_q; st.n_kv = a.n_kv; st.D = pl.D;
-        st.k16 = ws + pl.stage_k; st.v16 = ws + pl.stage_v; st.q16 = ws + pl.stage_q;
+        st.k16 = ws + pl.stage_k; st.v16 = ws + pl.stage_v; st.q16 = pl.splitk ? ws + pl.stage_q : nullptr;
         e = sixi::launch_q8_stage(st, stream);
         if (e != hipSuccess) return SIXI_E_BACKEND;
         const int64_t row = (int64_t)pl.D * 2;
-        a.q = st.q16; a.q_nb2 = row; a.q_nb1 = (int64_t)a.H * row; a.q_nb3 = (int64_t)a.n_q * a.H * row;
-        a.q_es = 2; a.q_f16 = 1;
+        if (pl.splitk) {
+            a.q = st.q16; a.q_nb2 = row; a.q_nb1 = (int64_t)a.H * row; a.q_nb3 = (int64_t)a.n_q * a.H * row;
+            a.q_es = 2; a.q_f16 = 1;
+        } else {
+            a.q_q8 = 1;  // the prefill kernel converts Q to the q8_0 dot type itself
+        }
         a.k = st.k16; a.k_nb2 = row; a.k_nb1 = (int64_t)a.Hkv * row; a.k_nb3 = (int64_t)a.n_kv * a.Hkv * row;
         a.v = st.v16; a.v_nb2 = row; a.v_nb1 = a.k_nb1; a.v_nb3 = a.k_nb3;
         a.pt = nullptr;  // the staged rows are one range per stream
