@@ -224,13 +224,13 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
             return aligned(t.data, 16) && t.nb[1] % 16 == 0 && t.nb[2] % 16 == 0 && t.nb[3] % 16 == 0;
         };
         const bool dma16 = D == 128 || (D == 256 && rows16(k) && rows16(v));
-        // the f16 staging of K, V and Q (fa_q8_stage.hip) in the workspace
+        // the f16 staging (fa_q8_stage.hip) in the workspace: K and V, and for a split-K call Q
+        // (the prefill kernel converts Q itself)
         int64_t kv_bytes = 0, q_bytes = 0, cells = 0, span = 0;
         if (!mul_ok(S * Hkv, n_kv, &cells) || !mul_ok(cells, D * 2, &kv_bytes) ||
             !mul_ok(S * H, n_q, &q_bytes) || !mul_ok(q_bytes, D * 2, &q_bytes) ||
             !mul_ok(n_kv + sixi::kDecodeTileWide, Hkv * D * 2, &span))
             return SIXI_E_INTEGER_OVERFLOW;
-        // (prefill converts Q in the kernel: only split-K calls stage it)
         const size_t stage_v = align_up((size_t)kv_bytes, kWsAlign);
         const size_t stage_q = stage_v + align_up((size_t)kv_bytes, kWsAlign);
         const size_t stage_bytes = stage_q + (pl.splitk ? align_up((size_t)q_bytes, kWsAlign) : 0);
@@ -239,10 +239,9 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
         } else if (!pl.splitk && dma16 && stage_bytes > stage_cap) {
             // the prefill kernel converts each tile's q8_0 rows to f16 in LDS
         } else {
-            // K, V and Q staged as f16 operands in the workspace, then the f16 kernels: a
-            // prefill-sized block while the copy is small (one pass over the cache instead of a
-            // conversion per work-group that reads a tile), or 256-dim rows that are not 16-byte
-            // aligned
+            // staged as f16 operands in the workspace, then the f16 kernels: a prefill-sized
+            // block while the copy is small (one pass over the cache instead of a conversion per
+            // work-group that reads a tile), or 256-dim rows that are not 16-byte aligned
             if (span >= (int64_t)UINT32_MAX) return SIXI_E_UNSUPPORTED;
             pl.q8_stage = true;
             pl.kv_type = SIXI_TYPE_F16;
