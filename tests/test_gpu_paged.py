@@ -1,8 +1,8 @@
 """Paged KV caches on the GPU: attention through a page table (include/sixi_attn.h
 page_table) equals the attention over the same cells laid out contiguously, bit for bit, on
 every kernel path (split-K 16- and 32-cell kernels, f16 and q8_0, 128- and 256-dim heads, the
-explicit-mask path, the prefill kernel over f16 and q8_0 tiles, the 256-dim q8_0 staging
-path); and the page pool's seq_cp
+explicit-mask path, the prefill kernel over f16 tiles, over q8_0 caches staged as f16 and,
+with FLAG_BOUNDED_WORKSPACE, over q8_0 tiles converted in LDS); and the page pool's seq_cp
 shares pages without moving cells while a write into a shared page copies it first
 (include/sixi_kv.h sixi_kv_pool_*), checked bitwise against the data-copy path (sixi_kv_copy)
 and against the oracle.
@@ -102,6 +102,15 @@ def test_paged_equals_contiguous(fa, label, kv_type, D, kv_len, q_len, H, Hkv, e
         a, b = out_c[s, :q_len[s]], out_p[s, :q_len[s]]
         assert torch.isfinite(b).all(), (label, s)
         assert torch.equal(a, b), (label, s, (a - b).abs().max().item())
+    if kv_type == sa.TYPE_Q8_0:
+        # with FLAG_BOUNDED_WORKSPACE prefill-sized blocks read the q8_0 pages themselves
+        # (converted in LDS) instead of a staged f16 copy: the same output
+        out_b = torch.full_like(out_c, float("nan"))
+        fa(dev["q"], kpool, vpool, out_b, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=mode, mask=mask,
+           page_table=table, bounded_workspace=True)
+        torch.cuda.synchronize()
+        for s in range(S):
+            assert torch.equal(out_c[s, :q_len[s]], out_b[s, :q_len[s]]), (label, "bounded", s)
 
 
 def test_paged_matches_the_oracle_on_shared_pages(fa):
