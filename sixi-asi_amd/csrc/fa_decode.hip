@@ -2027,12 +2027,14 @@ __global__ __launch_bounds__(256) void decode_merge_pieces(FaArgs a, int rows_sl
 }
 
 // Combines the pieces of every segment that more than one work-group touched, for segments of
-// few pieces (at most eight on average), in the order of the work-groups.  grid = (S*Hkv segments, row blocks of 8); 256 threads = 8 rows x 32
-// four-dim chunks, so every (row, chunk) is one thread.  The split kernel recorded the
+// few pieces (at most eight on average), in the order of the work-groups.  grid = (S*Hkv
+// segments, row blocks of 256 / (D/8) rows); 256 threads = rows x eight-dim chunks, so every
+// (row, chunk) is one thread.  The split kernel recorded the
 // segment's first and last piece; the stream extents come in the same round trip.
 template <int D>
 __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot) {
-    constexpr int TPR = D / 4;  // threads per row (4 dims each)
+    constexpr int DPT = 8;        // dims per thread: one 16-byte partial load, two 16-byte stores
+    constexpr int TPR = D / DPT;  // threads per row
     const int64_t k = blockIdx.x;
     const int s = (int)(k / a.Hkv);
     const int g = (int)(k % a.Hkv);
@@ -2042,30 +2044,32 @@ __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot
     if (row >= a.Gr * sd.ql) return;  // (a segment without rows has stale entries)
     if (p_first == p_last) return;    // written whole by its only work-group
 
-    const int d0 = (int)(threadIdx.x % TPR) * 4;
+    const int d0 = (int)(threadIdx.x % TPR) * DPT;
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    f32x4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     // N pieces per step, their loads independent, so a step costs one memory latency: two or
     // four for the usual segment (no loads beyond its pieces), eight per step beyond
     auto merge_step = [&](auto NC, int p0) {
         constexpr int N = decltype(NC)::value;
-        f32x4 ov[N];
+        f32x4 ov[N][2];
         float mv[N], lv[N];
-        u32x2 hv[N];
+        u32x4 hv[N];
 #pragma unroll
         for (int u = 0; u < N; ++u) {
             const int p = p0 + u <= p_last ? p0 + u : p_last;
             const float* sl = base + (int64_t)p * a.piece_stride * a.slot_floats;
-            hv[u] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(sl) + (int64_t)row * (2 * D) + d0 * 2);
+            hv[u] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(sl) + (int64_t)row * (2 * D) + d0 * 2);
             mv[u] = sl[(int64_t)rows_slot * (D / 2) + row];
             lv[u] = sl[(int64_t)rows_slot * (D / 2 + 1) + row];
         }
 #pragma unroll
         for (int u = 0; u < N; ++u) {
-            const f16x4 h = __builtin_bit_cast(f16x4, hv[u]);
-            ov[u] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]} * lv[u];  // back to O = l * (O/l)
-            if (p0 + u <= p_last) merge_row<1>(M, L, &o, mv[u], lv[u], &ov[u]);
+            const f16x8 h = as_f16x8(hv[u]);
+            // back to O = l * (O/l)
+            ov[u][0] = f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]} * lv[u];
+            ov[u][1] = f32x4{(float)h[4], (float)h[5], (float)h[6], (float)h[7]} * lv[u];
+            if (p0 + u <= p_last) merge_row<2>(M, L, o, mv[u], lv[u], ov[u]);
         }
     };
     if (p_last - p_first < 2) {
@@ -2078,7 +2082,9 @@ __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;
     const int j = row / a.Gr;
     const int h = g * a.G + a.hoff + row % a.Gr;
-    st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
+    char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4;
+    st16(dst, o[0] * inv);
+    st16(dst + 16, o[1] * inv);
 }
 
 // The merge form for a split launch: the piece-parallel one once segments average more than
@@ -2089,7 +2095,7 @@ void launch_merge(const FaArgs& a, int rows_slot, hipStream_t stream) {
         hipLaunchKernelGGL(decode_merge_pieces<D>, dim3((unsigned)(a.S * a.Hkv), (unsigned)rows_slot), dim3(256), 0,
                            stream, a, rows_slot);
     } else {
-        const int rows_wg = 256 / (D / 4);
+        const int rows_wg = 256 / (D / 8);
         hipLaunchKernelGGL(decode_merge_rows<D>,
                            dim3((unsigned)(a.S * a.Hkv), (unsigned)((rows_slot + rows_wg - 1) / rows_wg)), dim3(256), 0,
                            stream, a, rows_slot);
