@@ -122,9 +122,14 @@ inline int decode_tile_cells(int kv_type, int row_tiles, int head_dim, bool gene
 // Fixed cost of starting a piece (loading Q, filling the ring, merging and writing the
 // rows), in tiles of the split: each segment weighs tiles + seg_cost, so a work-group whose
 // range enters a segment gets that many tiles less.
+// (f16 at 128-dim heads, the pipelined kernel: 16; interleaved sweep on the 32 x 16 verify, 8 / 12
+// / 16 / 24 / 32 tiles: 149.2 / 145.4 / 144.0 / 145.2 / 147.4 us.  256-dim heads: 276.1 us at 12,
+// 277.9 at 16.)
 constexpr int kWideSegCost = 12;
+constexpr int kWideSegCostF16D128 = 16;
 inline int decode_seg_cost(int kv_type, int row_tiles, int head_dim, bool generic) {
-    return decode_wide_kernel(kv_type, row_tiles, head_dim, generic) ? kWideSegCost : 0;
+    if (!decode_wide_kernel(kv_type, row_tiles, head_dim, generic)) return 0;
+    return kv_type == SIXI_TYPE_F16 && head_dim == 128 ? kWideSegCostF16D128 : kWideSegCost;
 }
 // Row tiles the decode kernel runs for `rows` = G * n_q rows, i.e. exactly the rows of the
 // launched kernel's partial slots (16 per tile): 128-dim heads run up to 3 per wave, beyond
