@@ -127,8 +127,9 @@ def test_q8_prefill_workspace_is_independent_of_the_cache_length():
                for n_kv in (1024, 65536, 1 << 20)]
     assert bounded == [token] * 3, bounded
 
-    def ws_unaligned(n_kv):
+    def ws_unaligned(n_kv, flags=0):
         p = _params(n_q=512, n_kv=n_kv, D=256, kv_type=sa.TYPE_Q8_0)
+        p.flags = flags
         for t in (p.k, p.v):  # 4 spare bytes per cell: no row starts 16-byte aligned
             t.nb[1] = 4 * 272 + 4
             t.nb[3] = n_kv * t.nb[1]
@@ -138,6 +139,8 @@ def test_q8_prefill_workspace_is_independent_of_the_cache_length():
 
     staged = [ws_unaligned(n_kv) for n_kv in (1024, 65536)]
     assert staged[1] > staged[0] >= 2 * 2 * 1024 * 4 * 256 * 2
+    # only the staging can read such rows: the flag does not change it
+    assert [ws_unaligned(n_kv, sa.FLAG_BOUNDED_WORKSPACE) for n_kv in (1024, 65536)] == staged
 
 
 @pytest.mark.parametrize("mutate,code", [
