@@ -123,13 +123,17 @@ inline int decode_tile_cells(int kv_type, int row_tiles, int head_dim, bool gene
 // rows), in tiles of the split: each segment weighs tiles + seg_cost, so a work-group whose
 // range enters a segment gets that many tiles less.
 // (f16 at 128-dim heads, the pipelined kernel: 16; interleaved sweep on the 32 x 16 verify, 8 / 12
-// / 16 / 24 / 32 tiles: 149.2 / 145.4 / 144.0 / 145.2 / 147.4 us.  256-dim heads: 276.1 us at 12,
-// 277.9 at 16.)
+// / 16 / 24 / 32 tiles: 149.2 / 145.4 / 144.0 / 145.2 / 147.4 us.  q8_0 at 128-dim heads, 32 x 16
+// verify, 8 / 12 / 16 / 20: 167.0 / 163.4 / 163.0 / 164.6 us.  256-dim heads, whose tiles are twice
+// the bytes, 32 x 16 verify at 2 / 4 / 6 / 8 / 12 tiles: f16 278.7 / 274.7 / 272.1 / 271.5 / 274.0 us,
+// q8_0 387.6 / 383.3 / 382.4 / 384.6 / 389.0 us.)
 constexpr int kWideSegCost = 12;
 constexpr int kWideSegCostF16D128 = 16;
+constexpr int kWideSegCostD256 = 6;
 inline int decode_seg_cost(int kv_type, int row_tiles, int head_dim, bool generic) {
     if (!decode_wide_kernel(kv_type, row_tiles, head_dim, generic)) return 0;
-    return kv_type == SIXI_TYPE_F16 && head_dim == 128 ? kWideSegCostF16D128 : kWideSegCost;
+    if (head_dim == 256) return kWideSegCostD256;
+    return kv_type == SIXI_TYPE_F16 ? kWideSegCostF16D128 : kWideSegCost;
 }
 // Row tiles the decode kernel runs for `rows` = G * n_q rows, i.e. exactly the rows of the
 // launched kernel's partial slots (16 per tile): 128-dim heads run up to 3 per wave, beyond
