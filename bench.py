@@ -21,6 +21,8 @@ byte counters (FETCH_SIZE / WRITE_SIZE) used in the traffic figures.  `--workloa
 times only the chunked causal prefill (two 2048-row chunks), for profiling that kernel;
 `prefill_q8` and `prefill_d256_q8` the same over a q8_0 cache (128- and 256-dim heads; f16
 staging), and their `_bounded` forms with FLAG_BOUNDED_WORKSPACE (q8_0 tiles converted in LDS).
+`verify_q8`, `verify_d256` and `verify_d256_q8` time the batched verify alone over a q8_0 cache
+(128-dim heads) and at 256-dim heads over an f16 or q8_0 cache.
 """
 from __future__ import annotations
 
@@ -487,15 +489,22 @@ def q8_variant(name: str):
     return dataclasses.replace(wl.config(name), name=name + "_q8", kv_type=sa.TYPE_Q8_0)
 
 
-def verify_q8_only(steps: int, warmup: int) -> int:
+def verify_q8_only(steps: int, warmup: int, head_dim: int = 128, q8: bool = True) -> int:
+    """The 32 x 16 batched verify alone: a q8_0 cache at 128-dim heads, or 256-dim heads over
+    an f16 or q8_0 cache."""
+    import dataclasses
+
     import sixi_attn as sa
     from sixi_attn import workloads as wl
 
     fa = sa.FlashAttnExt()
-    w = batched_verify_q8()
+    w = batched_verify_q8() if head_dim == 128 else wl.config("batched_verify_d256")
+    if q8:
+        w = dataclasses.replace(w, kv_type=sa.TYPE_Q8_0)
     dev = wl.to_device(wl.make_host(w))
     ms, per = time_calls(fa, w, dev, max(1, steps), warmup)
-    print(json.dumps({"workload": "batched verify over a q8_0 cache", **summarize(w, ms, per)}), flush=True)
+    print(json.dumps({"workload": f"batched verify, {w.D}-dim heads, {'q8_0' if q8 else 'f16'} cache",
+                      **summarize(w, ms, per)}), flush=True)
     return 0
 
 
@@ -518,7 +527,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_q8_bounded",
                                                                "prefill_d256_q8", "prefill_d256_q8_bounded", "layer",
-                                                               "gdn", "verify_q8"])
+                                                               "gdn", "verify_q8", "verify_d256", "verify_d256_q8"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -545,6 +554,8 @@ def main() -> int:
         return 0
     if args.workload == "verify_q8":
         return verify_q8_only(args.steps, args.warmup)
+    if args.workload.startswith("verify_d256"):
+        return verify_q8_only(args.steps, args.warmup, head_dim=256, q8=args.workload.endswith("_q8"))
 
     import sixi_attn as sa
     from sixi_attn import workloads as wl
