@@ -73,7 +73,9 @@ enum {
 
 /* sixi_attn_params.flags.  BOUNDED_WORKSPACE: never stage a q8_0 cache as f16 in the
  * workspace, so the workspace does not grow with the cache.  Without it, prefill-sized
- * blocks over a q8_0 cache stage K, V and Q as f16 operands while that copy takes at most
+ * blocks over a q8_0 cache stage K and V as f16 operands (the prefill kernel converts Q to
+ * the q8_0 dot type itself; split-K calls of unaligned 256-dim rows also stage Q) while that
+ * copy takes at most
  * SIXI_ATTN_STAGE_CAP_BYTES (a separate pass, then the f16 kernel: faster than converting
  * every tile in LDS, which repeats the conversion in every work-group that reads the tile),
  * and convert the q8_0 tiles in LDS beyond it.  256-dim q8_0 rows that are not 16-byte

@@ -117,8 +117,12 @@ int sixi_kv_pool_seq_cp(sixi_kv_pool* pool, int32_t src, int32_t dst, int64_t n)
 
 /* The page table, n_streams rows of max_pages int32 entries (-1: no page), into host memory. */
 int sixi_kv_pool_page_table(const sixi_kv_pool* pool, int32_t* host_dst);
-/* The same into device memory (n_streams * max_pages int32), copied on `stream`; returns once
- * the table has been read from the pool (later pool changes do not reach this copy). */
+/* The same into device memory (n_streams * max_pages int32), copied on `stream` and ordered
+ * with the caller's work there; later pool changes do not reach this copy.  The call does
+ * not wait for the stream: it copies from one of two pinned snapshots of the pool (waiting
+ * only, if at all, for the copy two uploads earlier that read the same snapshot).  Under
+ * HIP graph capture it records kernel launches that carry the table in their arguments, so
+ * every replay stores the table as it was at capture. */
 int sixi_kv_pool_upload(const sixi_kv_pool* pool, int32_t* dev_dst, void* stream);
 
 int32_t sixi_kv_pool_free_pages(const sixi_kv_pool* pool);             /* < 0: error */

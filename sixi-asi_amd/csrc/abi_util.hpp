@@ -59,4 +59,17 @@ inline bool rows_disjoint(const sixi_view& v, int64_t row_bytes) {
 
 inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)a) == 0; }
 
+// Whether the byte ranges [a, a + a_bytes) and [b, b + b_bytes) intersect (empty ranges never do).
+inline bool ranges_overlap(const void* a, int64_t a_bytes, const void* b, int64_t b_bytes) {
+    if (a_bytes <= 0 || b_bytes <= 0) return false;
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + (uintptr_t)b_bytes && b0 < a0 + (uintptr_t)a_bytes;
+}
+
+// Whether two views' byte ranges intersect; each view's span (view_span with its row bytes)
+// must have been checked for overflow.
+inline bool views_overlap(const sixi_view& a, int64_t a_row, const sixi_view& b, int64_t b_row) {
+    return ranges_overlap(a.data, view_span(a, a_row), b.data, view_span(b, b_row));
+}
+
 }  // namespace sixi_abi

@@ -37,6 +37,7 @@ struct FaArgs {
     int32_t mask_stage;    // EXPLICIT, rows j < 32 of a step staged through LDS (16-byte aligned
                            // rows); 0: read per cell from global memory
     uint32_t m_bytes;      // staged: bytes of a stream's mask rows the kernel may read
+    int64_t m_span;        // EXPLICIT: bytes of a stream's n_q mask rows, (n_q-1)*nb1 + 2*ne[0]
 
     int32_t S, H, Hkv, G;  // streams, q heads, kv heads, H / Hkv
     int32_t Gr, hoff;      // heads of each GQA group this launch covers: hoff .. hoff+Gr-1

@@ -429,7 +429,7 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
         mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3 + (int64_t)min(j, j_last) * a.m_nb1;
     const f32x16 zero16 = {};
 
-    // MODE_MASK: the stream's mask rows through a range-checked resource (rows up to n_q);
+    // MODE_MASK: the stream's mask rows through a range-checked resource (exactly its n_q rows);
     // wave w's load u stages its rows 8u + l/8, the 16-byte piece at slot l%8 of a row
     // holding cells 8((l%8) ^ ((row >> 1) & 7)) .. +7 of the tile, so that the 32 lanes of a
     // read (one row each, same piece) spread over the banks
@@ -438,7 +438,7 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
     const uint32_t m_lds = lds0 + 4 * kKBytes + (uint32_t)w * kMaskWave;
     const float inv_scale = 1.0f / a.scale;
     if constexpr (MODE == MODE_MASK) {
-        mrs = make_rsrc_uniform(a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3, (uint32_t)((int64_t)a.n_q * a.m_nb1));
+        mrs = make_rsrc_uniform(a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3, (uint32_t)a.m_span);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int r = 8 * u + lane / 8;
@@ -734,7 +734,7 @@ hipError_t launch_prefill_d(const FaArgs& a, int mask_mode, hipStream_t stream) 
     // an explicit mask alone, with 16-byte aligned rows that one 32-bit range covers: LDS-staged
     const bool mask_only = mask_mode == SIXI_MASK_EXPLICIT && a.mask && a.softcap == 0.0f && a.alibi_nlog2 == 0 &&
                            reinterpret_cast<uintptr_t>(a.mask) % 16 == 0 && a.m_nb1 % 16 == 0 &&
-                           (a.m_ne3 == 1 || a.m_nb3 % 16 == 0) && (int64_t)a.n_q * a.m_nb1 < (int64_t)UINT32_MAX;
+                           (a.m_ne3 == 1 || a.m_nb3 % 16 == 0) && a.m_span < (int64_t)UINT32_MAX;
     if (mask_only)
         launch_prefill_mode<MODE_MASK, D, KV>(a, causal, nrb, stream);
     else if (generic)

@@ -43,4 +43,10 @@ struct KvCopyArgs {
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t stream);
 hipError_t launch_kv_copy(const KvCopyArgs& a, hipStream_t stream);
 
+// dst[0, n) = src[0, n) by kernel launches that carry the values as by-value arguments
+// (kTableChunk entries per launch): a captured graph keeps the values of the call, and the
+// host memory may change as soon as the call returns.
+constexpr int kTableChunk = 960;
+hipError_t launch_table_store(int32_t* dst, const int32_t* src, int64_t n, hipStream_t stream);
+
 }  // namespace sixi

@@ -123,7 +123,32 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(KvCopyArgs a) {
     dst[w] = src[w];
 }
 
+// One chunk of a table store: the values travel in the kernel's arguments.
+struct TableChunk {
+    int32_t* dst;
+    int32_t n;
+    int32_t v[kTableChunk];
+};
+static_assert(sizeof(TableChunk) <= 4000, "kernel arguments stay below 4 KB");
+
+__global__ __launch_bounds__(256) void table_store_kernel(TableChunk c) {
+    for (int i = threadIdx.x; i < c.n; i += blockDim.x) c.dst[i] = c.v[i];
+}
+
 }  // namespace
+
+hipError_t launch_table_store(int32_t* dst, const int32_t* src, int64_t n, hipStream_t stream) {
+    for (int64_t i = 0; i < n; i += kTableChunk) {
+        TableChunk c;
+        c.dst = dst + i;
+        c.n = (int32_t)(n - i < kTableChunk ? n - i : kTableChunk);
+        for (int k = 0; k < c.n; ++k) c.v[k] = src[i + k];
+        hipLaunchKernelGGL(table_store_kernel, dim3(1), dim3(256), 0, stream, c);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
 
 hipError_t launch_kv_write(const KvWriteArgs& a, hipStream_t stream) {
     const int64_t n = (int64_t)a.S * a.n_rows * a.Hkv * (a.D / 32);

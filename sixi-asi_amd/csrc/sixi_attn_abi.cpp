@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -30,6 +31,35 @@ constexpr int64_t kQ8MaxRows = 48;  // rows per kv-head group of one q8_0 split-
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// The small device arrays a call reads besides its views: the lengths and the page table.
+struct DevRange {
+    const void* p;
+    int64_t bytes;
+};
+std::array<DevRange, 3> device_arrays(const sixi_attn_params* p, int64_t S) {
+    const int64_t pt = p->page_table ? S * p->page_table_stride * 4 : 0;
+    return {DevRange{p->kv_len, p->kv_len ? S * 4 : 0}, DevRange{p->q_len, p->q_len ? S * 4 : 0},
+            DevRange{p->page_table, pt}};
+}
+
+// Whether [ws, ws + bytes) meets anything the call reads or writes.  The views' spans were
+// checked for overflow by resolve().
+bool workspace_overlaps(const sixi_attn_params* p, const void* ws, size_t bytes) {
+    const int64_t D = p->q.ne[0];
+    const int64_t n = (int64_t)bytes;
+    const int64_t kvrow = row_bytes(p->k.type, D);
+    if (ranges_overlap(ws, n, p->q.data, view_span(p->q, D * elem_bytes(p->q.type))) ||
+        ranges_overlap(ws, n, p->k.data, view_span(p->k, kvrow)) ||
+        ranges_overlap(ws, n, p->v.data, view_span(p->v, kvrow)) ||
+        ranges_overlap(ws, n, p->out.data, view_span(p->out, D * 4)))
+        return true;
+    if (p->mask_mode == SIXI_MASK_EXPLICIT && ranges_overlap(ws, n, p->mask.data, view_span(p->mask, p->mask.ne[0] * 2)))
+        return true;
+    for (const DevRange& x : device_arrays(p, p->q.ne[3]))
+        if (ranges_overlap(ws, n, x.p, x.bytes)) return true;
+    return false;
+}
+
 struct Plan {
     FaArgs a{};
     int kv_type = 0;
@@ -39,7 +69,6 @@ struct Plan {
     bool generic = false;      // explicit mask or softcap: the decode kernels' per-cell mode
     size_t seg_offset = 0;  // split-K: byte offset of the per-segment piece table
     int row_tiles = 0;
-    int heads_per_launch = 0;  // split-K: heads of each GQA group per launch (the group in parts)
     bool q8_stage = false;     // q8_0 KV staged as f16 rows in the workspace, then the f16 kernels
     size_t stage_k = 0, stage_v = 0, stage_q = 0;  // byte offsets of the staged K, V and Q
     size_t stage_bytes = 0;    // the split-K workspace follows the staging area
@@ -134,6 +163,13 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
     if (view_span(q, D * qes) < 0 || view_span(k, kvrow) < 0 || view_span(v, kvrow) < 0 ||
         view_span(o, D * 4) < 0)
         return SIXI_E_INTEGER_OVERFLOW;
+    // Work-groups write output rows in no fixed order: every row must be its own, and no
+    // written byte may be one that a work-group reads (Q, K, V; the mask below).
+    if (!rows_disjoint(o, D * 4)) return SIXI_E_INVALID_ARGUMENT;
+    if (views_overlap(o, D * 4, q, D * qes) || views_overlap(o, D * 4, k, kvrow) || views_overlap(o, D * 4, v, kvrow))
+        return SIXI_E_INVALID_ARGUMENT;
+    for (const DevRange& x : device_arrays(p, S))
+        if (ranges_overlap(o.data, view_span(o, D * 4), x.p, x.bytes)) return SIXI_E_INVALID_ARGUMENT;
 
     // mask
     const int mode = p->mask_mode;
@@ -147,6 +183,7 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
             return SIXI_E_INVALID_ARGUMENT;
         if (m.nb[1] % 2 || m.nb[3] % 2 || !aligned(m.data, 2)) return SIXI_E_ALIGNMENT;
         if (view_span(m, m.ne[0] * 2) < 0) return SIXI_E_INTEGER_OVERFLOW;
+        if (views_overlap(o, D * 4, m, m.ne[0] * 2)) return SIXI_E_INVALID_ARGUMENT;
     }
 
     // scalars (ggml: ALiBi slopes multiply the mask, so they need one)
@@ -186,6 +223,10 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
                         aligned(m.data, 16) && span < (int64_t)UINT32_MAX)
                            ? 1 : 0;
         a.m_bytes = a.mask_stage ? (uint32_t)span : 0u;
+        // the prefill kernel stages every row j < n_q: the exact bytes of one stream's rows
+        // (its tail tile reads cells past ne[0], which this bound turns into zeros on the last
+        // row; the other rows read into their successor and mask those cells by length)
+        a.m_span = (n_q - 1) * m.nb[1] + m.ne[0] * 2;
     } else {
         a.m_ne3 = 1;
     }
@@ -216,7 +257,6 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
     // blocks are staged as f16 up to stage_cap bytes (one pass over the cache, then the f16
     // kernel: faster than converting every tile in each work-group that reads it), beyond it the
     // prefill kernel reads the q8_0 tiles and converts them in LDS.
-    pl.heads_per_launch = a.G;
     if (k.type == SIXI_TYPE_Q8_0 && (rows > kQ8MaxRows || D != 128)) {
         // 256-dim q8_0 rows (272 B) are read by 16-byte LDS-DMA loads: every row must start
         // 16-byte aligned
@@ -252,10 +292,14 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
         }
     }
     if (pl.splitk) {
-        pl.row_tiles = sixi::decode_row_tiles((int64_t)pl.heads_per_launch * n_q, pl.D);
+        pl.row_tiles = sixi::decode_row_tiles(rows, pl.D);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles, pl.D);
         a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles, pl.D, pl.generic);
         a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles, pl.D, pl.generic);
+        // the kernels sum the streams' costs (tiles + seg_cost each) in 32-bit integers: a paged
+        // call may describe up to 2^26 cells per stream, which 512 full streams would overflow
+        const int64_t stream_cost = (n_kv + a.tile_cells - 1) / a.tile_cells + a.seg_cost;
+        if (stream_cost * S > (int64_t)INT32_MAX) return SIXI_E_UNSUPPORTED;
         // slot indices run up to S*Hkv + P - 2 for a launch of P <= kMaxSplitGroups work-groups
         splitk_layout(pl, S * Hkv + sixi::kMaxSplitGroups);
     } else {
@@ -333,14 +377,9 @@ int run(Plan& pl, char* ws, hipStream_t stream) {
         a.xcd_remap = 0;
         a.head_split = 0;
         a.piece_stride = 1;
-        e = hipSuccess;
-        // one launch pair per head subset, ordered on the stream (they share the workspace)
-        for (int h0 = 0; h0 < a.G && e == hipSuccess; h0 += pl.heads_per_launch) {
-            a.hoff = h0;
-            a.Gr = std::min(pl.heads_per_launch, a.G - h0);
-            e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D,
-                                    sixi::decode_row_tiles((int64_t)a.Gr * a.n_q, pl.D), stream);
-        }
+        // every head of a GQA group in one launch (the split kernel and its merge), so each
+        // K/V byte is read once for all of the group's rows
+        e = sixi::launch_decode(a, pl.kv_type, pl.mask_mode, pl.D, pl.row_tiles, stream);
     } else {
         e = sixi::launch_prefill(a, pl.kv_type, pl.mask_mode, pl.D, stream);
     }
@@ -372,6 +411,8 @@ int sixi_attn_forward(const sixi_attn_params* p) {
     if (rc != SIXI_OK) return rc;
     if (!p->workspace || p->workspace_bytes < pl.ws_bytes) return SIXI_E_OUT_OF_BOUNDS;
     if (!aligned(p->workspace, kWsAlign)) return SIXI_E_ALIGNMENT;
+    // the kernels write the workspace while they read the views
+    if (workspace_overlaps(p, p->workspace, pl.ws_bytes)) return SIXI_E_INVALID_ARGUMENT;
     return run(pl, static_cast<char*>(p->workspace), static_cast<hipStream_t>(p->stream));
 }
 

@@ -33,6 +33,22 @@ struct sixi_kv_pool {
     std::vector<sixi_view> views;
     mutable std::mutex mu;
 
+    // Upload staging: pinned host copies of the table that alternate between uploads, each
+    // with the event recorded after its copy, waited on only before that copy is refilled.
+    static constexpr int kStages = 2;
+    mutable int32_t* stage[kStages] = {};
+    mutable hipEvent_t stage_ev[kStages] = {};
+    mutable bool stage_busy[kStages] = {};
+    mutable int next_stage = 0;
+
+    ~sixi_kv_pool() {
+        for (int i = 0; i < kStages; ++i) {
+            if (stage_busy[i]) (void)hipEventSynchronize(stage_ev[i]);
+            if (stage_ev[i]) (void)hipEventDestroy(stage_ev[i]);
+            if (stage[i]) (void)hipHostFree(stage[i]);
+        }
+    }
+
     int32_t* row(int32_t s) { return table.data() + (size_t)s * max_pages; }
 
     void release(int32_t page) {
@@ -203,16 +219,39 @@ int sixi_kv_pool_page_table(const sixi_kv_pool* pool, int32_t* host_dst) {
 
 int sixi_kv_pool_upload(const sixi_kv_pool* pool, int32_t* dev_dst, void* stream) {
     if (!pool || !dev_dst) return SIXI_E_INVALID_ARGUMENT;
-    std::vector<int32_t> snap;
-    {
-        std::lock_guard<std::mutex> lock(pool->mu);
-        snap = pool->table;
-    }
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    // the snapshot dies with this call: wait until the copy has read it
-    if (hipMemcpyAsync(dev_dst, snap.data(), snap.size() * sizeof(int32_t), hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return SIXI_E_BACKEND;
+    std::lock_guard<std::mutex> lock(pool->mu);
+    const size_t n = pool->table.size();
+    if (cs != hipStreamCaptureStatusNone) {
+        // under capture: the table travels in kernel arguments, so every replay stores this
+        // call's table, and no host buffer has to outlive the call
+        return sixi::launch_table_store(dev_dst, pool->table.data(), (int64_t)n, st) == hipSuccess ? SIXI_OK
+                                                                                                  : SIXI_E_BACKEND;
+    }
+    // eager: an asynchronous copy from a pinned snapshot; the only wait is for the copy that
+    // last read the same snapshot buffer (two uploads ago), never for the stream's other work
+    const int i = pool->next_stage;
+    if (!pool->stage[i]) {
+        void* h = nullptr;
+        if (hipHostMalloc(&h, n * sizeof(int32_t), hipHostMallocDefault) != hipSuccess) return SIXI_E_BACKEND;
+        if (hipEventCreateWithFlags(&pool->stage_ev[i], hipEventDisableTiming) != hipSuccess) {
+            (void)hipHostFree(h);
+            pool->stage_ev[i] = nullptr;
+            return SIXI_E_BACKEND;
+        }
+        pool->stage[i] = static_cast<int32_t*>(h);
+    } else if (pool->stage_busy[i]) {
+        if (hipEventSynchronize(pool->stage_ev[i]) != hipSuccess) return SIXI_E_BACKEND;
+        pool->stage_busy[i] = false;
+    }
+    std::copy(pool->table.begin(), pool->table.end(), pool->stage[i]);
+    if (hipMemcpyAsync(dev_dst, pool->stage[i], n * sizeof(int32_t), hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipEventRecord(pool->stage_ev[i], st) != hipSuccess)
         return SIXI_E_BACKEND;
+    pool->stage_busy[i] = true;
+    pool->next_stage = (i + 1) % sixi_kv_pool::kStages;
     return SIXI_OK;
 }
 

@@ -40,6 +40,7 @@ hipError_t launch_prefill(const FaArgs&, int, int, int, hipStream_t) { no_launch
 int decode_num_groups(const FaArgs&, int cu_count, int per_cu) { return cu_count * per_cu; }
 hipError_t launch_kv_write(const KvWriteArgs&, hipStream_t) { no_launch("kv write"); }
 hipError_t launch_kv_copy(const KvCopyArgs&, hipStream_t) { no_launch("kv copy"); }
+hipError_t launch_table_store(int32_t*, const int32_t*, int64_t, hipStream_t) { no_launch("table store"); }
 hipError_t launch_qk_prologue(const QkPrologueArgs&, hipStream_t) { no_launch("prologue"); }
 hipError_t launch_attn_gate(const AttnGateArgs&, hipStream_t) { no_launch("gate"); }
 hipError_t launch_gdn_verify(const GdnArgs&, hipStream_t) { no_launch("gdn"); }

@@ -36,6 +36,9 @@ def test_status_strings():
 
 
 FAKE = 0x7F0000000000  # aligned host address; validation never dereferences it
+# each view of an attention description in an address range of its own (the ABI rejects a
+# written view that overlaps anything the call reads)
+ADDR = {name: FAKE + (i << 36) for i, name in enumerate(("q", "k", "v", "out", "kv_len", "mask", "ws", "pt"))}
 
 
 def _params(S=2, n_q=16, H=24, Hkv=4, D=128, n_kv=4096, q_type=sa.TYPE_F32, kv_type=sa.TYPE_F16,
@@ -43,14 +46,14 @@ def _params(S=2, n_q=16, H=24, Hkv=4, D=128, n_kv=4096, q_type=sa.TYPE_F32, kv_t
     p = sa.SixiAttnParams()
     qes = 4 if q_type == sa.TYPE_F32 else 2
     kves = 2
-    p.q = sa.make_view(FAKE, q_type, [D, n_q, H, S], [qes, H * D * qes, D * qes, n_q * H * D * qes])
+    p.q = sa.make_view(ADDR["q"], q_type, [D, n_q, H, S], [qes, H * D * qes, D * qes, n_q * H * D * qes])
     row = D * kves if kv_type == sa.TYPE_F16 else D // 32 * 34
     nb0 = kves if kv_type == sa.TYPE_F16 else 34
     kv_nb = [nb0, Hkv * row, row, n_kv * Hkv * row]
-    p.k = sa.make_view(FAKE, kv_type, [D, n_kv, Hkv, S], kv_nb)
-    p.v = sa.make_view(FAKE, kv_type, [D, n_kv, Hkv, S], kv_nb)
-    p.out = sa.make_view(FAKE, sa.TYPE_F32, [D, H, n_q, S], [4, D * 4, H * D * 4, n_q * H * D * 4])
-    p.kv_len = FAKE if kv_len else None
+    p.k = sa.make_view(ADDR["k"], kv_type, [D, n_kv, Hkv, S], kv_nb)
+    p.v = sa.make_view(ADDR["v"], kv_type, [D, n_kv, Hkv, S], kv_nb)
+    p.out = sa.make_view(ADDR["out"], sa.TYPE_F32, [D, H, n_q, S], [4, D * 4, H * D * 4, n_q * H * D * 4])
+    p.kv_len = ADDR["kv_len"] if kv_len else None
     p.q_len = None
     p.mask_mode = mode
     p.scale = 1.0 / D ** 0.5
@@ -150,7 +153,7 @@ def test_q8_prefill_workspace_is_independent_of_the_cache_length():
     (lambda p: p.q.ne.__setitem__(2, 25), sa.E_INVALID_ARGUMENT),          # H % Hkv != 0
     (lambda p: p.out.ne.__setitem__(2, 15), sa.E_INVALID_ARGUMENT),        # out rows != n_q
     (lambda p: p.k.nb.__setitem__(1, 1032), sa.E_ALIGNMENT),              # cell stride not 16-B
-    (lambda p: setattr(p.k, "data", FAKE + 8), sa.E_ALIGNMENT),
+    (lambda p: setattr(p.k, "data", ADDR["k"] + 8), sa.E_ALIGNMENT),
     (lambda p: p.k.nb.__setitem__(1, 128), sa.E_INVALID_ARGUMENT),         # rows would overlap
     (lambda p: setattr(p, "mask_mode", 7), sa.E_INVALID_ARGUMENT),
     (lambda p: setattr(p, "kv_len", None), sa.E_INVALID_ARGUMENT),         # block-causal needs lengths
@@ -173,10 +176,64 @@ def test_stream_count_and_head_dim_limits():
 def test_explicit_mask_view_is_checked():
     p = _params(mode=sa.MASK_EXPLICIT)
     assert _validate(p) == sa.E_INVALID_ARGUMENT  # no mask view given
-    p.mask = sa.make_view(FAKE, sa.TYPE_F16, [4096, 16, 1, 2], [2, 8192, 8192 * 16, 8192 * 16])
+    p.mask = sa.make_view(ADDR["mask"], sa.TYPE_F16, [4096, 16, 1, 2], [2, 8192, 8192 * 16, 8192 * 16])
     assert _validate(p) == sa.OK
     p.mask.ne[1] = 8
     assert _validate(p) == sa.E_INVALID_ARGUMENT  # fewer mask rows than n_q
+    p.mask.ne[1] = 16
+    p.mask.data = ADDR["out"] + 4096  # the output would overwrite the mask it reads
+    assert _validate(p) == sa.E_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("mutate", [
+    lambda p: p.out.nb.__setitem__(2, p.out.nb[1]),          # rows j and head h+1 of row j-1 alias
+    lambda p: p.out.nb.__setitem__(3, 4096),                 # streams inside one another's rows
+    lambda p: setattr(p.out, "data", ADDR["q"]),             # output over Q
+    lambda p: setattr(p.out, "data", ADDR["k"] + (1 << 20)),  # output inside the K cache
+    lambda p: setattr(p.out, "data", ADDR["v"]),
+    lambda p: setattr(p, "kv_len", ADDR["out"] + 256),       # the lengths under the output
+])
+def test_output_must_not_alias_itself_or_what_the_call_reads(mutate):
+    """Work-groups write output rows in no fixed order, while others still read Q, K, V, the
+    mask and the lengths: every output row must be its own and touch nothing that is read."""
+    p = _params()
+    assert _validate(p) == sa.OK
+    mutate(p)
+    assert _validate(p) == sa.E_INVALID_ARGUMENT
+
+
+def test_workspace_must_not_overlap_the_views():
+    """The split kernel writes its partials into the workspace while it reads the views; an
+    overlapping workspace is rejected before any launch (so this runs without a GPU)."""
+    lib = sa.load_library()
+    p = _params()
+    n = ctypes.c_size_t(0)
+    assert lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n)) == sa.OK
+    for where in ("q", "k", "v", "out", "kv_len"):
+        p.workspace = ADDR[where] - 256 if where != "q" else ADDR["q"]
+        p.workspace_bytes = n.value + 512
+        assert lib.sixi_attn_forward(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT, where
+
+
+def _paged_params(S, stride, n_q=1, n_pages=1024):
+    """A paged call: K and V pools of 256-cell pages, a page table of `stride` pages per stream."""
+    p = _params(S=S, n_q=n_q)
+    D, Hkv, row = 128, 4, 256
+    nb = [2, Hkv * row, row, 256 * Hkv * row]
+    p.k = sa.make_view(ADDR["k"], sa.TYPE_F16, [D, 256, Hkv, n_pages], nb)
+    p.v = sa.make_view(ADDR["v"], sa.TYPE_F16, [D, 256, Hkv, n_pages], nb)
+    p.page_table = ADDR["pt"]
+    p.page_table_stride = stride
+    return p
+
+
+def test_paged_cost_line_stays_within_32_bits():
+    """The split kernels sum the streams' tile counts in 32-bit integers.  A paged description
+    may give every stream 2^26 cells; 512 such streams on the 16-cell kernel (2^22 tiles each)
+    would overflow the sum, so the call is refused; half the cells per stream fit."""
+    assert _validate(_paged_params(S=512, stride=1 << 18)) == sa.E_UNSUPPORTED
+    assert _validate(_paged_params(S=512, stride=1 << 17)) == sa.OK
+    assert _validate(_paged_params(S=2, stride=1 << 18)) == sa.OK
 
 
 def test_forward_without_workspace_fails_before_any_launch():

@@ -121,3 +121,76 @@ def test_gdn_graph():
 
     _replays(run, [st_out, y])
     assert torch.all(torch.isfinite(y[0])) and torch.all(y[4] == 0)   # stream 4 has no rows
+
+
+def _noalloc_call(fa, dev, out, w, stream):
+    import ctypes
+
+    p = fa.params(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
+                  mask_mode=w.mask_mode)
+    p.stream = stream
+    rc = fa.lib.sixi_attn_forward_noalloc(ctypes.byref(p))
+    assert rc == sa.OK, sa.strerror(rc)
+
+
+def test_noalloc_graph():
+    """The no-allocation entry point captured and replayed: every replay bitwise equal to the
+    eager sixi_attn_forward call (the scratch's device address is looked up once per device,
+    outside any stream work, and the kernels take it as an argument)."""
+    w = wl.Workload("graph noalloc", 0x51A7_C300, 5, [3000, 17, 900, 6000, 255], [16, 3, 16, 9, 1])
+    _say(f"graph: no-allocation verify S={w.S}")
+    dev = wl.to_device(wl.make_host(w))
+    fa = sa.FlashAttnExt()
+    out = torch.empty((w.S, w.n_q, w.H, w.D), device="cuda")
+    ref = torch.empty_like(out)
+    ref.zero_()
+    fa(dev["q"], dev["k"], dev["v"], ref, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=w.mask_mode)
+    torch.cuda.synchronize()
+    _replays(lambda: _noalloc_call(fa, dev, out, w, torch.cuda.current_stream().cuda_stream), [out])
+    out.zero_()
+    _noalloc_call(fa, dev, out, w, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+_FIRST_CALL_CHILD = r'''
+import ctypes, sys
+sys.path[:0] = [sys.argv[1]]
+import torch
+import sixi_attn as sa
+from sixi_attn import workloads as wl
+w = wl.Workload("graph noalloc first", 0x51A7_C301, 3, [2500, 40, 700], [16, 5, 12])
+dev = wl.to_device(wl.make_host(w))
+fa = sa.FlashAttnExt()
+out = torch.zeros((w.S, w.n_q, w.H, w.D), device="cuda")
+ref = torch.zeros_like(out)
+side = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=side):   # the process's first no-allocation call
+    p = fa.params(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=w.mask_mode)
+    p.stream = side.cuda_stream
+    rc = fa.lib.sixi_attn_forward_noalloc(ctypes.byref(p))
+assert rc == sa.OK, sa.strerror(rc)
+fa(dev["q"], dev["k"], dev["v"], ref, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=w.mask_mode)
+torch.cuda.synchronize()
+for r in range(3):
+    out.zero_()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), f"replay {r}"
+    _ = torch.ones(1024, device="cuda").sum().item()
+print("first-call capture ok", flush=True)
+'''
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process():
+    """In a fresh process, the first no-allocation call (which looks up the scratch's device
+    address) is made under graph capture; its replays equal the eager call bitwise."""
+    import pathlib
+    import subprocess
+
+    _say("graph: first no-allocation call captured, child process")
+    pkg = str(pathlib.Path(sa.__file__).resolve().parent.parent)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CHILD, pkg], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "first-call capture ok" in r.stdout, (r.returncode, r.stdout[-2000:], r.stderr[-4000:])

@@ -264,3 +264,57 @@ def test_prologue_store_through_the_page_table(q8):
         unused = torch.ones(n_pages, dtype=torch.bool, device="cuda")
         unused[idx] = False
         assert torch.equal(pool[unused].view(torch.uint8), before[unused].view(torch.uint8)), name
+
+
+def test_pool_upload_snapshots_without_waiting():
+    """sixi_kv_pool_upload copies from pinned snapshots that alternate between calls, with no
+    stream synchronisation: several uploads queued behind busy work each land the table as it
+    was at their call, including the third, which reuses the first snapshot buffer."""
+    _say("pool upload: queued snapshots")
+    pool = sa.KvPool(n_pages=64, n_streams=3, max_pages=8)
+    busy = torch.randn(4096, 4096, device="cuda")
+    want, dsts = [], []
+    for step in range(5):
+        pool.prepare_write(step % 3, 256 * step, 256)   # the table changes between uploads
+        if step % 2:
+            pool.seq_cp(step % 3, (step + 1) % 3)
+        for _ in range(3):
+            busy = busy @ busy.T * 1e-3                     # keep the stream busy meanwhile
+        dsts.append(pool.upload())
+        want.append(pool.page_table())
+    torch.cuda.synchronize()
+    for step, (d, w) in enumerate(zip(dsts, want)):
+        assert np.array_equal(d.cpu().numpy(), w), step
+    pool.close()
+
+
+def test_pool_upload_under_graph_capture_keeps_the_captured_table():
+    """Captured into a HIP graph, the upload stores the table as it was at capture on every
+    replay (the values travel in kernel arguments), whatever the pool holds by then; eager
+    uploads between the replays still see the current table."""
+    _say("pool upload: graph capture")
+    pool = sa.KvPool(n_pages=64, n_streams=4, max_pages=300)  # 1200 entries: two launches
+    for s in range(4):
+        pool.prepare_write(s, 0, 256 * (s + 1))
+    captured = pool.page_table()
+    dst = torch.full((4, 300), 7, dtype=torch.int32, device="cuda")
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        pool.upload(dst)  # warm the eager path on this stream before capturing
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        pool.upload(dst, stream=side.cuda_stream)
+    pool.seq_rm(0, 0)
+    pool.seq_cp(3, 1)
+    now = pool.page_table()
+    assert not np.array_equal(now, captured)
+    for rep in range(3):
+        dst.fill_(-5)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dst.cpu().numpy(), captured), rep
+        eager = pool.upload()
+        torch.cuda.synchronize()
+        assert np.array_equal(eager.cpu().numpy(), now), rep
+    pool.close()

@@ -2,8 +2,9 @@
 
 * The workspace needs no initialisation (include/sixi_attn.h): a call whose workspace is
   filled with NaN bit patterns gives bitwise the output of a call with a zeroed one, on every
-  kernel path (16-cell and 32-cell split-K with either merge, 256-dim heads, q8_0 split-K and
-  head-subset launches, the q8_0 staging, the prefill kernel), and two calls in a row agree.
+  kernel path (16-cell and 32-cell split-K with either merge, 256-dim heads, the 16-cell and
+  32-cell q8_0 split-K kernels, the q8_0 staging, the prefill kernel), and two calls in a row
+  agree.
 * Non-finite inputs give the oracle's result.  ggml's CPU kernel propagates a NaN score or V
   value through its online softmax: a row whose Q holds NaN or Inf is NaN in every dim; NaN in
   the K of a cell a row sees makes that row NaN; NaN in dim d of the V of a cell a row sees
@@ -56,7 +57,7 @@ def _ws_bytes(fa, w, dev):
     ("32-cell split-K, piece merge", [40000], [16], 24, 4, 128, sa.TYPE_F16),
     ("256-dim heads, 48 rows", [6000, 333], [8, 6], 24, 4, 256, sa.TYPE_F16),
     ("q8_0 split-K", [4000, 64], [8, 3], 24, 4, 128, sa.TYPE_Q8_0),
-    ("q8_0 head subsets", [4000, 900], [16, 12], 24, 4, 128, sa.TYPE_Q8_0),
+    ("q8_0 96 rows, 32-cell kernel", [4000, 900], [16, 12], 24, 4, 128, sa.TYPE_Q8_0),
     ("q8_0 prefill", [300, 1000], [200, 130], 24, 4, 128, sa.TYPE_Q8_0),
     ("q8_0 prefill, 256-dim heads", [300, 1000], [200, 130], 24, 4, 256, sa.TYPE_Q8_0),
     ("prefill kernel", [100, 1500], [300, 129], 24, 4, 128, sa.TYPE_F16),

@@ -79,8 +79,9 @@ def test_noalloc_matches_forward_on_two_calls():
     _against_oracle(w2, h2, got2)
 
 
-def test_noalloc_q8_0_head_subsets():
-    """q8_0 at 96 rows per group: launches over head subsets that share the scratch."""
+def test_noalloc_q8_0_96_rows():
+    """q8_0 at 96 rows per group: one launch of the 32-cell q8_0 kernel and its merge on the
+    scratch (every head of a group rides along with each tile)."""
     fa = sa.FlashAttnExt()
     w = wl.Workload("noalloc q8", 0x51A7_C100, 4, [5000, 12, 800, 2000], [16, 16, 5, 9], kv_type=sa.TYPE_Q8_0)
     _say("no-alloc: q8_0, 96 rows per group")
