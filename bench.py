@@ -22,7 +22,8 @@ times only the chunked causal prefill (two 2048-row chunks), for profiling that 
 `prefill_q8` and `prefill_d256_q8` the same over a q8_0 cache (128- and 256-dim heads; f16
 staging), and their `_bounded` forms with FLAG_BOUNDED_WORKSPACE (q8_0 tiles converted in LDS).
 `verify_q8`, `verify_d256` and `verify_d256_q8` time the batched verify alone over a q8_0 cache
-(128-dim heads) and at 256-dim heads over an f16 or q8_0 cache.
+(128-dim heads) and at 256-dim heads over an f16 or q8_0 cache; `verify_op` the engine's own
+operating point (32 streams x q_len 4 and 6, 256-dim heads, f16 and q8_0 caches).
 """
 from __future__ import annotations
 
@@ -518,6 +519,33 @@ def operating_point(q_len: int, q8: bool):
 OPERATING_POINTS = tuple((ql, q8) for q8 in (False, True) for ql in (4, 6))
 
 
+def verify_op_only(steps: int, warmup: int) -> int:
+    """The four operating-point verify calls alone (32 streams, q_len 4 and 6, 256-dim heads,
+    f16 and q8_0 caches): eager median and graph-replay time per call, GB/s of each."""
+    import torch
+
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    fa = sa.FlashAttnExt()
+    res = {}
+    for ql, q8 in OPERATING_POINTS:
+        w = operating_point(ql, q8)
+        dev = wl.to_device(wl.make_host(w))
+        ms, per = time_calls(fa, w, dev, max(1, steps), warmup)
+        r = summarize(w, ms, per)
+        out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+        usg = _graph_us(lambda: fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
+                                   mask_mode=w.mask_mode), max(40, steps), 3)
+        r["us_graph"] = round(usg, 2)
+        r["GBps_graph"] = round(w.bytes() / (usg * 1e-6) / 1e9, 1)
+        res[w.name] = r
+        _log(f"{w.name}: {r}")
+        del dev
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def q8_variant(name: str):
     """A config over a q8_0 cache (same seeds, lengths and heads)."""
     import dataclasses
@@ -566,7 +594,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_q8_bounded",
                                                                "prefill_d256_q8", "prefill_d256_q8_bounded", "layer",
-                                                               "gdn", "verify_q8", "verify_d256", "verify_d256_q8"])
+                                                               "gdn", "verify_q8", "verify_d256", "verify_d256_q8", "verify_op"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -593,6 +621,8 @@ def main() -> int:
         return 0
     if args.workload == "verify_q8":
         return verify_q8_only(args.steps, args.warmup)
+    if args.workload == "verify_op":
+        return verify_op_only(args.steps, args.warmup)
     if args.workload.startswith("verify_d256"):
         return verify_q8_only(args.steps, args.warmup, head_dim=256, q8=args.workload.endswith("_q8"))
 

@@ -77,13 +77,24 @@ __device__ __forceinline__ StreamDims table_dims(const StreamTable& t, int s) {
     return d;
 }
 
-// Per KV type: bytes of one ring slot (one 16-cell tile of K and V) and LDS-DMA loads
-// a tile takes (per wave when one wave stages it all).
-template <int KV> struct KvTile;
-template <> struct KvTile<SIXI_TYPE_F16> { static constexpr int slot_bytes = 8192, dma = 8; };
-template <> struct KvTile<SIXI_TYPE_Q8_0> { static constexpr int slot_bytes = 2 * kQ8Dma * 256, dma = 2 * kQ8Dma; };
+// Per head dim of the 16-cell kernel: k-steps of 32 dims (KS), output tiles of 16 dims (DT),
+// dims of a V row that one lane stages (VD), bytes of a q8_0 head row (Q8ROW).
+template <int D> struct T16Dim;
+template <> struct T16Dim<128> { static constexpr int KS = 4, DT = 8, VD = 8, Q8ROW = kQ8Row; };
+template <> struct T16Dim<256> { static constexpr int KS = 8, DT = 16, VD = 16, Q8ROW = 2 * kQ8Row; };
 
-// Four independent tile lanes (one wave each) per work-group, two work-groups per CU.
+// Per KV type and head dim: bytes of one ring slot (one 16-cell tile of K and V), LDS-DMA loads
+// a tile takes per wave, and the byte offset of V in the slot.  256-dim q8_0 rows (272 B,
+// 16-byte aligned) come in as five 1 KB loads each for K and V (4352 B of rows, then spare).
+template <int KV, int D> struct KvTile;
+template <> struct KvTile<SIXI_TYPE_F16, 128> { static constexpr int slot_bytes = 8192, dma = 8, v_off = 4096; };
+template <> struct KvTile<SIXI_TYPE_Q8_0, 128> {
+    static constexpr int slot_bytes = 2 * kQ8Dma * 256, dma = 2 * kQ8Dma, v_off = kQ8Dma * 256;
+};
+template <> struct KvTile<SIXI_TYPE_Q8_0, 256> { static constexpr int slot_bytes = 2 * 5 * 1024, dma = 10, v_off = 5 * 1024; };
+
+// Four independent tile lanes (one wave each) per work-group: two work-groups per CU at
+// 128-dim heads, one at 256 (t16_groups_per_cu).
 template <int KV> struct Shape;
 template <> struct Shape<SIXI_TYPE_F16> { static constexpr int waves = 4, lanes = 4, slots = 2; };
 template <> struct Shape<SIXI_TYPE_Q8_0> { static constexpr int waves = 4, lanes = 4, slots = 3; };
@@ -96,15 +107,15 @@ struct MergeBuf {
 };
 
 // NTW = row tiles per wave.
-template <int NTW, int KV>
+template <int NTW, int KV, int D = 128>
 struct DecodeLds {
     using Sh = Shape<KV>;
     union {
         struct {
-            u32x4 ring[Sh::lanes * Sh::slots * KvTile<KV>::slot_bytes / 16];
-            u32x4 q[NTW * 4 * 64];  // Q^T B operands: [row tile][ks][lane], 8 f16 each
+            u32x4 ring[Sh::lanes * Sh::slots * KvTile<KV, D>::slot_bytes / 16];
+            u32x4 q[NTW * T16Dim<D>::KS * 64];  // Q^T B operands: [row tile][ks][lane], 8 f16 each
         } t;
-        MergeBuf<NTW, Sh::lanes / 2> mg;  // reused after the tile loop
+        MergeBuf<NTW, Sh::lanes / 2, T16Dim<D>::DT> mg;  // reused after the tile loop
     };
     int ps[kMaxStreams + 1];  // (no extents table: it would not leave room for two groups per CU)
 };
@@ -224,39 +235,54 @@ struct RowInfo {
 // `after_reads` runs once the slot's LDS reads are consumed.  The phases run over all row
 // tiles at once (every QK^T, then every row max, one rare rescale branch, then every
 // exponential and PV), so each phase offers the scheduler NT independent chains.
-template <int NT, int KV, int MODE, bool MASKED, typename F>
-__device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT>& acc, const u32x4* slot,
+template <int NT, int KV, int MODE, bool MASKED, int D, typename F>
+__device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT, T16Dim<D>::DT>& acc, const u32x4* slot,
                                           const u32x4* qs, int c0, const RowInfo<NT>& ri,
                                           const char* mrow, int nc, int lane, F&& after_reads) {
+    using TD = T16Dim<D>;
+    constexpr int KS = TD::KS, DT = TD::DT, VH = TD::VD / 8;
+    static_assert(D == 128 || KV == SIXI_TYPE_Q8_0, "256-dim heads: q8_0 only");
     const int c = lane >> 4;
     const int r = lane & 15;
 
-    // K operands (cell r, dims 32ks + 8c .. +7) and V rows (cells 4c + e, dims 8r .. 8r+7)
-    f16x8 kop[4];
-    u32x4 vr[4];
+    // K operands (cell r, dims 32ks + 8c .. +7) and V rows (cells 4c + e, dims VD*r .. +VD-1,
+    // as VH groups of eight f16)
+    f16x8 kop[KS];
+    u32x4 vr[4][VH];
     if constexpr (KV == SIXI_TYPE_F16) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kop[ks] = as_f16x8(slot[ks * 64 + lane]);
+        for (int ks = 0; ks < KS; ++ks) kop[ks] = as_f16x8(slot[ks * 64 + lane]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) vr[e] = slot[(4 + e) * 64 + lane];
+        for (int e = 0; e < 4; ++e) vr[e][0] = slot[(4 + e) * 64 + lane];
     } else {
-        // raw q8_0 rows packed at 136 B: block b of row x holds d at x*136 + 34b and the
-        // int8 values at x*136 + 34b + 2 (2 bytes past a dword boundary for even b)
+        // raw q8_0 rows packed at Q8ROW bytes: block b of row x holds d at x*Q8ROW + 34b and the
+        // int8 values at x*Q8ROW + 34b + 2 (2 bytes past a dword boundary for even b)
+        constexpr int RB = TD::Q8ROW;
         const uint32_t* kraw = reinterpret_cast<const uint32_t*>(slot);
-        const uint32_t* vraw = kraw + kQ8Dma * 64;
+        const uint32_t* vraw = kraw + KvTile<KV, D>::v_off / 4;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int ks = 0; ks < KS; ++ks) {
             uint32_t w0, w1;
-            ld8_at(kraw, r * kQ8Row + 34 * ks + 2 + 8 * c, (ks & 1) == 0, w0, w1);
-            kop[ks] = as_f16x8(dequant_q8x8(w0, w1, ld_half_at(kraw, r * kQ8Row + 34 * ks)));
+            ld8_at(kraw, r * RB + 34 * ks + 2 + 8 * c, (ks & 1) == 0, w0, w1);
+            kop[ks] = as_f16x8(dequant_q8x8(w0, w1, ld_half_at(kraw, r * RB + 34 * ks)));
         }
-        const int b = r >> 2;
+        // the lane's VD dims lie in block b at byte VD * (r % (32 / VD)) of its quants
+        const int b = (TD::VD * r) >> 5;
+        const int qo = 2 + TD::VD * (r & (32 / TD::VD - 1));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int x = 4 * c + e;
-            uint32_t w0, w1;
-            ld8_at(vraw, x * kQ8Row + 34 * b + 2 + 8 * (r & 3), (b & 1) == 0, w0, w1);
-            vr[e] = dequant_q8x8(w0, w1, ld_half_at(vraw, x * kQ8Row + 34 * b));
+            const uint16_t dv = ld_half_at(vraw, x * RB + 34 * b);
+            if constexpr (VH == 1) {
+                uint32_t w0, w1;
+                ld8_at(vraw, x * RB + 34 * b + qo, (b & 1) == 0, w0, w1);
+                vr[e][0] = dequant_q8x8(w0, w1, dv);
+            } else {
+                uint32_t w[4];
+                ld16_at_any(vraw, x * RB + 34 * b + qo, w);
+                vr[e][0] = dequant_q8x8(w[0], w[1], dv);
+                vr[e][1] = dequant_q8x8(w[2], w[3], dv);
+            }
         }
     }
 
@@ -266,18 +292,18 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT>& acc, const u
     for (int n = 0; n < NT; ++n) {
         st[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) st[n] = mfma16x16x32(kop[ks], as_f16x8(qs[(n * 4 + ks) * 64 + lane]), st[n]);
+        for (int ks = 0; ks < KS; ++ks) st[n] = mfma16x16x32(kop[ks], as_f16x8(qs[(n * KS + ks) * 64 + lane]), st[n]);
     }
     after_reads();
 
-    // V^T operands: tile tt holds dim 8r + tt of cells 4c..4c+3
-    u32x2 vt[8];
+    // V^T operands: tile tt holds dim VD*r + tt of cells 4c..4c+3
+    u32x2 vt[DT];
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-        const int d2 = tt >> 1;
+    for (int tt = 0; tt < DT; ++tt) {
+        const int h = tt >> 3, d2 = (tt & 7) >> 1;
         const uint32_t sel = (tt & 1) ? 0x07060302u : 0x05040100u;
-        vt[tt][0] = __builtin_amdgcn_perm(vr[1][d2], vr[0][d2], sel);
-        vt[tt][1] = __builtin_amdgcn_perm(vr[3][d2], vr[2][d2], sel);
+        vt[tt][0] = __builtin_amdgcn_perm(vr[1][h][d2], vr[0][h][d2], sel);
+        vt[tt][1] = __builtin_amdgcn_perm(vr[3][h][d2], vr[2][h][d2], sel);
     }
 
     // ---- scores (FAST: raw dot products; GENERIC: log2-domain logits) and row maxima ----
@@ -333,7 +359,7 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT>& acc, const u
             }
             acc.l[n] *= alpha;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) acc.o[t][n] *= alpha;
+            for (int t = 0; t < DT; ++t) acc.o[t][n] *= alpha;
         }
     }
 
@@ -363,21 +389,22 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT>& acc, const u
                           ((((b1 >> (16 * c)) & 0xffffull) != 0) ? 0xffff0000u : 0u);
             }
 #pragma unroll
-            for (int tt = 0; tt < 8; ++tt) {
+            for (int tt = 0; tt < DT; ++tt) {
                 const u32x2 vm = {vt[tt][0] & keep[0], vt[tt][1] & keep[1]};
                 acc.o[tt][n] = mfma16x16x16(__builtin_bit_cast(f16x4, vm), pf, acc.o[tt][n]);
             }
         } else {
 #pragma unroll
-            for (int tt = 0; tt < 8; ++tt)
+            for (int tt = 0; tt < DT; ++tt)
                 acc.o[tt][n] = mfma16x16x16(__builtin_bit_cast(f16x4, vt[tt]), pf, acc.o[tt][n]);
         }
     }
 }
 
-// Writes the normalised rows of row tiles n0 .. n0+NT-1 held by this lane.
-template <int NT>
-__device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT>& acc, int n0, int s, int g,
+// Writes the normalised rows of row tiles n0 .. n0+NT-1 held by this lane: dims
+// (D/4)c + DT*i + tt of row 16n + r at o[tt][n][i].
+template <int NT, int DT>
+__device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT, DT>& acc, int n0, int s, int g,
                                            int R, int lane) {
     // (the row addresses are computed here: hoisted out of the piece loop they would be held,
     // as 64-bit values, across every piece's steps, and spilled)
@@ -391,21 +418,23 @@ __device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT>& acc, 
         const int j = row / a.Gr;
         const int h = g * a.G + a.hoff + row % a.Gr;
         const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
-        char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + c * 32 * 4;
+        char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + c * 4 * DT * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            st16(dst + i * 32, f32x4{acc.o[0][n][i], acc.o[1][n][i], acc.o[2][n][i], acc.o[3][n][i]} * inv);
-            st16(dst + i * 32 + 16, f32x4{acc.o[4][n][i], acc.o[5][n][i], acc.o[6][n][i], acc.o[7][n][i]} * inv);
-        }
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int t = 0; t < DT; t += 4)
+                st16(dst + (i * DT + t) * 4,
+                     f32x4{acc.o[t][n][i], acc.o[t + 1][n][i], acc.o[t + 2][n][i], acc.o[t + 3][n][i]} * inv);
     }
 }
 
 // Partial slot of `rows_slot` rows: normalised O rows [row][128] f16 (O/l, a convex
 // combination of f16 V rows, so it fits f16 and rounds by at most 2^-11 relative), then
 // m[row] and l[row] in f32 (log2-domain references).
-template <int NT>
-__device__ __forceinline__ void write_partial(float* slot, int rows_slot, int n0, int R, const Acc<NT>& acc,
+template <int NT, int DT>
+__device__ __forceinline__ void write_partial(float* slot, int rows_slot, int n0, int R, const Acc<NT, DT>& acc,
                                               int lane) {
+    constexpr int D = 16 * DT;
     // (row offsets computed here, not held across the piece loop; see write_rows)
     int ln = lane;
     asm volatile("" : "+v"(ln));
@@ -415,17 +444,19 @@ __device__ __forceinline__ void write_partial(float* slot, int rows_slot, int n0
         const int row = 16 * (n0 + n) + r;
         if (row >= R) continue;
         const float inv = acc.l[n] == 0.0f ? 0.0f : 1.0f / acc.l[n];
-        char* dst = reinterpret_cast<char*>(slot) + (int64_t)row * 256 + c * 64;  // dims 32c .. 32c+31
+        char* dst = reinterpret_cast<char*>(slot) + (int64_t)row * (2 * D) + c * (D / 2);  // dims (D/4)c ..
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f16x8 h;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int t = 0; t < 8; ++t) h[t] = (_Float16)(acc.o[t][n][i] * inv);
-            *reinterpret_cast<u32x4*>(dst + i * 16) = as_u32x4(h);
-        }
+            for (int t0 = 0; t0 < DT; t0 += 8) {
+                f16x8 h;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) h[t] = (_Float16)(acc.o[t0 + t][n][i] * inv);
+                *reinterpret_cast<u32x4*>(dst + (i * DT + t0) * 2) = as_u32x4(h);
+            }
         if (c == 0) {
-            slot[(int64_t)rows_slot * 64 + row] = acc.m[n];
-            slot[(int64_t)rows_slot * 65 + row] = acc.l[n];
+            slot[(int64_t)rows_slot * (D / 2) + row] = acc.m[n];
+            slot[(int64_t)rows_slot * (D / 2 + 1) + row] = acc.l[n];
         }
     }
 }
@@ -437,14 +468,16 @@ struct Piece {
 };
 
 // One piece: tiles [tb, te) of segment (s, g).
-template <int NTW, int KV, int MODE>
-__device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>& sh, int causal, const Piece& pc) {
+template <int NTW, int KV, int MODE, int D>
+__device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV, D>& sh, int causal, const Piece& pc) {
+    using TD = T16Dim<D>;
+    constexpr int KS = TD::KS, DCH = D / 8;  // k-steps; 8-dim chunks of a Q row
     constexpr int NTOT = NTW;
     constexpr int TL = Shape<KV>::lanes;   // tile lanes (one wave each)
     constexpr int NSLOT = Shape<KV>::slots;
     constexpr int NTHREADS = Shape<KV>::waves * 64;
-    constexpr int SLOT16 = KvTile<KV>::slot_bytes / 16;
-    constexpr int DMA = KvTile<KV>::dma;  // LDS-DMA loads per tile per wave
+    constexpr int SLOT16 = KvTile<KV, D>::slot_bytes / 16;
+    constexpr int DMA = KvTile<KV, D>::dma;  // LDS-DMA loads per tile per wave
     static_assert(Shape<KV>::waves == TL, "one row group");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -461,21 +494,21 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
     const int n0 = rg * NTW;  // first row tile of this wave
 
     // ---- Q rows of the group -> f16 B operands in LDS (row 16n+r, dims 32ks+8c..+7) ----
-    // Item idx = tid + k*NTHREADS is row idx/16, 8-dim chunk idx%16.  Every load is issued
+    // Item idx = tid + k*NTHREADS is row idx/DCH, 8-dim chunk idx%DCH.  Every load is issued
     // before any is used (padding rows read row 0, which every piece has), so the staging
     // costs one memory latency.
-    constexpr int QIT = NTOT * 16 * 16 / NTHREADS;
-    static_assert(QIT * NTHREADS == NTOT * 16 * 16, "Q items per thread");
+    constexpr int QIT = NTOT * 16 * DCH / NTHREADS;
+    static_assert(QIT * NTHREADS == NTOT * 16 * DCH, "Q items per thread");
     const char* qsrc[QIT];
     bool qok[QIT];
 #pragma unroll
     for (int k = 0; k < QIT; ++k) {
         const int idx = tid + k * NTHREADS;
-        const int row = idx >> 4;
+        const int row = idx / DCH;
         qok[k] = row < R;
         const int rr = qok[k] ? row : 0;
         qsrc[k] = a.q + (int64_t)(rr / G) * a.q_nb1 + (int64_t)(hb + rr % G) * a.q_nb2 + (int64_t)s * a.q_nb3 +
-                  (int64_t)(idx & 15) * 8 * a.q_es;
+                  (int64_t)(idx % DCH) * 8 * a.q_es;
     }
     float xv[QIT][8];
     if (a.q_f16) {
@@ -525,10 +558,10 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
             for (int e = 0; e < 8; ++e) hv[e] = (_Float16)xv[k][e];
         }
         const int idx = tid + k * NTHREADS;
-        const int row = idx >> 4;
-        const int chunk = idx & 15;  // ks = chunk/4, c = chunk%4
+        const int row = idx / DCH;
+        const int chunk = idx % DCH;  // ks = chunk/4, c = chunk%4
         const int n = row >> 4, rr = row & 15, ks = chunk >> 2, cc = chunk & 3;
-        sh.t.q[(n * 4 + ks) * 64 + cc * 16 + rr] = qok[k] ? as_u32x4(hv) : u32x4{0u, 0u, 0u, 0u};
+        sh.t.q[(n * KS + ks) * 64 + cc * 16 + rr] = qok[k] ? as_u32x4(hv) : u32x4{0u, 0u, 0u, 0u};
     }
     __syncthreads();
 
@@ -546,15 +579,15 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
     const int t_full = (MODE == MODE_GENERIC) ? 0 : (causal ? (sd.kl + 1) / kTile : sd.nc / kTile);
     const char* mrow = nullptr;
     if (MODE == MODE_GENERIC && a.mask) mrow = a.mask + (int64_t)(s % a.m_ne3) * a.m_nb3;
-    const u32x4* qs = sh.t.q + n0 * 4 * 64;
+    const u32x4* qs = sh.t.q + n0 * KS * 64;
 
-    Acc<NTW> acc;
+    Acc<NTW, TD::DT> acc;
     acc_clear(acc);
 
     // K/V of this (stream, kv-head), per tile through range-checked buffer resources based at
     // the tile's first cell (in its page, for paged caches): cells >= nc read as zeros (and are
     // masked), so the tail tile needs no clamping and cannot fault.
-    const int64_t rowb = (KV == SIXI_TYPE_F16) ? 128 * 2 : kQ8Row;
+    const int64_t rowb = (KV == SIXI_TYPE_F16) ? D * 2 : TD::Q8ROW;
     const uint32_t knb = (uint32_t)a.k_nb1, vnb = (uint32_t)a.v_nb1;
 
     // tiles of this lane: tb + tl + TL*i, i < n_my
@@ -563,16 +596,20 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
     u32x4* ring = sh.t.ring + (size_t)tl * NSLOT * SLOT16;
     const uint32_t ring_base = lds_addr(ring);
 
-    // q8_0: dword t = 64u + lane of the packed 16-row tile is dword t % 34 of row t / 34
-    // (lanes past the 16 rows repeat the last dword into the slot's spare tail)
-    uint32_t q8_cell[kQ8Dma], q8_dw[kQ8Dma];
+    // q8_0: unit t = 64u + lane of the packed 16-row tile (a dword at 128-dim heads, 16 bytes
+    // at 256) is unit t % UPR of row t / UPR; lanes past the 16 rows repeat the last unit into
+    // the slot's spare tail
+    constexpr int Q8U = (D == 128) ? 4 : 16;          // bytes per lane and load
+    constexpr int UPR = TD::Q8ROW / Q8U;              // units per row: 34 dwords or 17 x 16 B
+    constexpr int Q8L = (D == 128) ? kQ8Dma : 5;      // loads per K (or V) of a tile
+    uint32_t q8_cell[Q8L], q8_dw[Q8L];
     if constexpr (KV == SIXI_TYPE_Q8_0) {
 #pragma unroll
-        for (int u = 0; u < kQ8Dma; ++u) {
+        for (int u = 0; u < Q8L; ++u) {
             const int t = 64 * u + lane;
-            const bool in = t < 16 * (kQ8Row / 4);
-            q8_cell[u] = in ? t / (kQ8Row / 4) : 15;
-            q8_dw[u] = in ? t % (kQ8Row / 4) : kQ8Row / 4 - 1;
+            const bool in = t < 16 * UPR;
+            q8_cell[u] = in ? t / UPR : 15;
+            q8_dw[u] = in ? t % UPR : UPR - 1;
         }
     }
 
@@ -581,7 +618,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
     auto issue = [&](int i) {
         // uniform over the wave (the compiler cannot tell): scalar page and span arithmetic
         const int c0 = __builtin_amdgcn_readfirstlane((t0 + i * TL) * kTile);
-        const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * KvTile<KV>::slot_bytes;
+        const uint32_t base = ring_base + (uint32_t)(i % NSLOT) * KvTile<KV, D>::slot_bytes;
         const int page = c0 < sd.nc ? page_id(pages, a, s, c0 >> 8) : 0;
         const KvSpan ksp = kv_span(a, a.k, a.k_nb1, a.k_nb2, a.k_nb3, s, g, c0, sd.nc, rowb, page);
         const KvSpan vsp = kv_span(a, a.v, a.v_nb1, a.v_nb2, a.v_nb3, s, g, c0, sd.nc, rowb, page);
@@ -600,23 +637,28 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV>
             dma16x4_to_lds(vrs, vo4, base + 4 * 1024);
         } else {
             static_assert(kQ8Dma == 9, "dword LDS-DMA batch of nine loads");
-            uint32_t ko[kQ8Dma], vo[kQ8Dma];
+            uint32_t ko[Q8L], vo[Q8L];
 #pragma unroll
-            for (int u = 0; u < kQ8Dma; ++u) {
-                ko[u] = q8_cell[u] * knb + q8_dw[u] * 4;
-                vo[u] = q8_cell[u] * vnb + q8_dw[u] * 4;
+            for (int u = 0; u < Q8L; ++u) {
+                ko[u] = q8_cell[u] * knb + q8_dw[u] * Q8U;
+                vo[u] = q8_cell[u] * vnb + q8_dw[u] * Q8U;
             }
-            dma4x9_to_lds(krs, ko, base);
-            dma4x9_to_lds(vrs, vo, base + kQ8Dma * 256);
+            if constexpr (D == 128) {
+                dma4x9_to_lds(krs, ko, base);
+                dma4x9_to_lds(vrs, vo, base + KvTile<KV, D>::v_off);
+            } else {
+                dma16x5_to_lds(krs, ko, base);
+                dma16x5_to_lds(vrs, vo, base + KvTile<KV, D>::v_off);
+            }
         }
     };
     auto step = [&](int i, auto&& after_reads) {
         const u32x4* slot = ring + (i % NSLOT) * SLOT16;
         const int t = t0 + i * TL;
         if (t < t_full)
-            tile_step<NTW, KV, MODE, false>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
+            tile_step<NTW, KV, MODE, false, D>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
         else
-            tile_step<NTW, KV, MODE, true>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
+            tile_step<NTW, KV, MODE, true, D>(a, acc, slot, qs, t * kTile, ri, mrow, sd.nc, lane, after_reads);
     };
 
     // private ring: the slot just read is refilled with tile i+NSLOT
@@ -1934,13 +1976,15 @@ __device__ __forceinline__ void for_each_piece(const FaArgs& a, const int* ps, F
     }
 }
 
-template <int NTW, int KV, int MODE>
-__global__ __launch_bounds__((Shape<KV>::waves * 64), (Shape<KV>::waves * d128_groups_per_cu(KV, NTW, MODE != MODE_FAST) / 4)) void
-decode_d128(FaArgs a, int causal) {
-    __shared__ DecodeLds<NTW, KV> sh;
+// The 16-cell kernel.  At 256-dim heads (q8_0) it runs the head-aligned split of the 32-cell
+// q8_0 kernel: neighbouring heads' 272-byte rows share cache lines.
+template <int NTW, int KV, int MODE, int D>
+__global__ __launch_bounds__((Shape<KV>::waves * 64), (Shape<KV>::waves * t16_groups_per_cu(D) / 4)) void
+decode_t16(FaArgs a, int causal) {
+    __shared__ DecodeLds<NTW, KV, D> sh;
     if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
     __syncthreads();
-    for_each_piece<false>(a, sh.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece<NTW, KV, MODE>(a, sh, causal, pc); });
+    for_each_piece<D == 256>(a, sh.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece<NTW, KV, MODE, D>(a, sh, causal, pc); });
 }
 
 template <int NTW, int RS, int MODE, int D>
@@ -2125,7 +2169,7 @@ inline FaArgs head_split_args(const FaArgs& a) {
 }
 
 // FAST_BUILT: whether the launch shape has a fast-mode kernel (the 32-cell kernel takes f16
-// explicit-mask and softcap calls of up to 48 rows as well, whose fast calls run decode_d128).
+// explicit-mask and softcap calls of up to 48 rows as well, whose fast calls run decode_t16).
 template <int NTW, int RS, int D, bool FAST_BUILT = true>
 hipError_t launch_wide(const FaArgs& a_in, int mode, int causal, hipStream_t stream) {
     // the fast kernels with the head-aligned split
@@ -2163,22 +2207,23 @@ hipError_t launch_wide_q8(const FaArgs& a_in, int mode, int causal, hipStream_t 
     return hipGetLastError();
 }
 
-template <int NTW, int KV>
-hipError_t launch_nt(const FaArgs& a, int mode, int causal, hipStream_t stream) {
-    if (!slot_fits(a, NTW * 16, 128)) return hipErrorInvalidValue;
+template <int NTW, int KV, int D = 128>
+hipError_t launch_nt(const FaArgs& a_in, int mode, int causal, hipStream_t stream) {
+    const FaArgs a = (D == 256) ? head_split_args(a_in) : a_in;
+    if (!slot_fits(a, NTW * 16, D)) return hipErrorInvalidValue;
     const dim3 grid(a.P), block(Shape<KV>::waves * 64);
     if (mode == MODE_FAST) {
-        hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_FAST>), grid, block, 0, stream, a, causal);
-    } else if constexpr (KV == SIXI_TYPE_Q8_0 && NTW == 1) {
-        // (f16 explicit-mask and softcap calls, and q8_0 ones of more than 16 rows, run the
-        // 32-cell kernels)
-        hipLaunchKernelGGL((decode_d128<NTW, KV, MODE_GENERIC>), grid, block, 0, stream, a, causal);
+        hipLaunchKernelGGL((decode_t16<NTW, KV, MODE_FAST, D>), grid, block, 0, stream, a, causal);
+    } else if constexpr (KV == SIXI_TYPE_Q8_0 && NTW == 1 && D == 128) {
+        // (f16 explicit-mask and softcap calls, and q8_0 ones of more than 16 rows or of 256-dim
+        // heads, run the 32-cell kernels)
+        hipLaunchKernelGGL((decode_t16<NTW, KV, MODE_GENERIC, D>), grid, block, 0, stream, a, causal);
     } else {
         return hipErrorNotSupported;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_merge<128>(a, NTW * 16, stream);
+    launch_merge<D>(a, NTW * 16, stream);
     return hipGetLastError();
 }
 
@@ -2205,8 +2250,18 @@ hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_d
                          : MODE_FAST;
     const int causal = mask_mode == SIXI_MASK_BLOCK_CAUSAL;
     if (head_dim == 256 && kv_type == SIXI_TYPE_Q8_0) {
-        // q8_0 at 256-dim heads: the 32-cell q8_0 kernel on one lane, up to two row tiles per
-        // wave (33-48 rows run as 64)
+        // q8_0 at 256-dim heads, up to 48 rows and lengths only: the 16-cell kernel (four
+        // waves per CU, each dequantising its tiles in registers)
+        if (mode == MODE_FAST && row_tiles <= 3) {
+            switch (row_tiles) {
+                case 1: return launch_nt<1, SIXI_TYPE_Q8_0, 256>(a, mode, causal, stream);
+                case 2: return launch_nt<2, SIXI_TYPE_Q8_0, 256>(a, mode, causal, stream);
+                case 3: return launch_nt<3, SIXI_TYPE_Q8_0, 256>(a, mode, causal, stream);
+                default: return hipErrorNotSupported;
+            }
+        }
+        // the rest: the 32-cell q8_0 kernel on one lane, up to two row tiles per wave (33-48
+        // rows run as 64)
         switch (row_tiles) {
             case 1: return launch_wide_q8<1, 1, 256>(a, mode, causal, stream);
             case 2: return launch_wide_q8<2, 1, 256>(a, mode, causal, stream);

@@ -168,6 +168,32 @@ __device__ __forceinline__ void dma16x8_to_lds(buf_rsrc rs, const uint32_t (&v)[
         : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "s"(rs)
         : "memory", "scc");
 }
+// Five 16-byte-per-lane loads (5 KB): 16 q8_0 rows of 256 dims (17 x 256 B) and a spare tail.
+__device__ __forceinline__ void dma16x5_to_lds(buf_rsrc rs, const uint32_t (&v)[5], uint32_t lds) {
+    int saved;
+    asm volatile(
+        "s_nop 4\n\t"
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %7, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %3, %7, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %4, %7, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %5, %7, 0 offen lds\n\t"
+        "s_add_u32 m0, m0, 1024\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %6, %7, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "s"(rs)
+        : "memory", "scc");
+}
 // One 16-byte-per-lane load (1 KB).
 __device__ __forceinline__ void dma16x1_to_lds(buf_rsrc rs, uint32_t v, uint32_t lds) {
     int saved;
@@ -551,6 +577,19 @@ __device__ __forceinline__ void ld8_at(const uint32_t* base, int a, bool odd2, u
         w0 = base[a >> 2];
         w1 = base[(a >> 2) + 1];
     }
+}
+
+// The 16 bytes at byte offset `a` (even; its parity over dwords may differ between lanes) of
+// a dword array: five dword reads from the dword holding `a`, realigned by a & 3.  Reads up to
+// 4 bytes past the 16 when `a` is dword-aligned.
+__device__ __forceinline__ void ld16_at_any(const uint32_t* base, int a, uint32_t (&w)[4]) {
+    const int d0 = a >> 2;
+    const uint32_t sh = (uint32_t)(a & 3);
+    uint32_t x[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) x[i] = base[d0 + i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = __builtin_amdgcn_alignbyte(x[i + 1], x[i], sh);
 }
 
 // The f16 bits at an even byte offset `a` of a dword array.

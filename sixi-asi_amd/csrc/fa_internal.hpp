@@ -92,7 +92,7 @@ hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_
                           hipStream_t stream);
 
 // Sizing rules shared by the dispatcher and the launchers.
-constexpr int kDecodeTile = 16;        // KV cells per wave step of the decode kernel (<= 48 rows, q8_0)
+constexpr int kDecodeTile = 16;        // KV cells per wave step of the 16-cell kernel (<= 48 rows)
 constexpr int kDecodeTileWide = 32;    // KV cells per step of the f16 kernel for 49..96 rows
 constexpr int kDecodeMaxRowTiles = 6;  // 16-row MFMA tiles per (stream, kv-head): G*q_len <= 96
 constexpr int kMaxStreams = 512;       // LDS prefix table bound
@@ -103,18 +103,24 @@ constexpr int kXcds = 8;               // MI355X: work-groups are dealt round-ro
 int decode_num_groups(const FaArgs& a, int cu_count, int groups_per_cu);
 // Whether the 32-cell kernel runs this launch: f16 KV with more than 48 rows or 256-dim heads,
 // f16 KV under an explicit mask or a softcap (`generic`: the per-cell work needs the 512
-// registers per wave of that kernel), and q8_0 KV with more than 48 rows (128-dim heads).
+// registers per wave of that kernel), and q8_0 KV with more than 48 rows, or under a mask or
+// softcap with more than 16 (128-dim heads) or any rows (256-dim heads).  Everything else --
+// f16 and q8_0 up to 48 rows at 128-dim heads, q8_0 up to 48 rows at 256-dim heads -- runs the
+// 16-cell kernel, which dequantises q8_0 in registers.
 inline bool decode_wide_kernel(int kv_type, int row_tiles, int head_dim, bool generic) {
-    if (kv_type == SIXI_TYPE_Q8_0) return head_dim == 256 || (row_tiles > 3 || (generic && row_tiles > 1));
+    if (kv_type == SIXI_TYPE_Q8_0)
+        return row_tiles > 3 || (generic && (head_dim == 256 || row_tiles > 1));
     return kv_type == SIXI_TYPE_F16 && (row_tiles > 3 || head_dim == 256 || generic);
 }
-// Work-groups per CU of the 16-cell kernel: two (256 registers per wave).  One group per CU
-// removes the few spills of q8_0 at 48 rows and of q8_0 under a mask, but halves the waves that
-// hide the loads: the 8 x 64k q8_0 verify took 286 against 171 us.
-constexpr int d128_groups_per_cu(int /*kv_type*/, int /*row_tiles*/, bool /*generic*/) { return 2; }
+// Work-groups per CU of the 16-cell kernel: two at 128-dim heads (256 registers per wave; one
+// group per CU removes the few spills of q8_0 at 48 rows and of q8_0 under a mask, but halves
+// the waves that hide the loads: the 8 x 64k q8_0 verify took 286 against 171 us), one at
+// 256-dim heads (its rings and Q operands fill the LDS, and 48 rows of 256-dim accumulators
+// need the 512 registers of one wave per SIMD).
+constexpr int t16_groups_per_cu(int head_dim) { return head_dim == 256 ? 1 : 2; }
 // Work-groups per CU of a decode launch (the 32-cell kernel runs one).
 inline int decode_groups_per_cu(int kv_type, int row_tiles, int head_dim, bool generic) {
-    return decode_wide_kernel(kv_type, row_tiles, head_dim, generic) ? 1 : d128_groups_per_cu(kv_type, row_tiles, generic);
+    return decode_wide_kernel(kv_type, row_tiles, head_dim, generic) ? 1 : t16_groups_per_cu(head_dim);
 }
 // Cells per split tile of the decode launch.
 inline int decode_tile_cells(int kv_type, int row_tiles, int head_dim, bool generic) {
@@ -137,12 +143,13 @@ inline int decode_seg_cost(int kv_type, int row_tiles, int head_dim, bool generi
     return kv_type == SIXI_TYPE_F16 ? kWideSegCostF16D128 : kWideSegCost;
 }
 // Row tiles the decode kernel runs for `rows` = G * n_q rows, i.e. exactly the rows of the
-// launched kernel's partial slots (16 per tile): 128-dim heads run up to 3 per wave, beyond
-// that two row groups of equal size (so 5 tiles run as 6); 256-dim heads hold at most two
-// per wave, so 3 tiles run as two row groups of two.
-inline int decode_row_tiles(int64_t rows, int head_dim) {
+// launched kernel's partial slots (16 per tile): up to 3 per wave on the 16-cell kernel, beyond
+// that two row groups of equal size (so 5 tiles run as 6); the 32-cell kernel holds at most
+// two per wave at 256-dim heads, so there 3 tiles run as two row groups of two.
+inline int decode_row_tiles(int64_t rows, int head_dim, int kv_type, bool generic) {
     const int rt = (int)((rows + 15) / 16);
-    if (rt <= 2 || (rt == 3 && head_dim != 256)) return rt;
+    if (rt <= 2 || (rt == 3 && !decode_wide_kernel(kv_type, rt, head_dim, generic))) return rt;
+    if (rt == 3 && head_dim != 256) return rt;
     return 2 * ((rt + 1) / 2);
 }
 inline int64_t decode_slot_floats(int row_tiles, int head_dim) {

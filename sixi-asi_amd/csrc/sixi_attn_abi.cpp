@@ -292,7 +292,7 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
         }
     }
     if (pl.splitk) {
-        pl.row_tiles = sixi::decode_row_tiles(rows, pl.D);
+        pl.row_tiles = sixi::decode_row_tiles(rows, pl.D, pl.kv_type, pl.generic);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles, pl.D);
         a.tile_cells = sixi::decode_tile_cells(pl.kv_type, pl.row_tiles, pl.D, pl.generic);
         a.seg_cost = sixi::decode_seg_cost(pl.kv_type, pl.row_tiles, pl.D, pl.generic);

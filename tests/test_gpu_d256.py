@@ -1,8 +1,10 @@
 """256-dim heads (the real model's key/value length, configs/qwen3.8-27b-ud-q4-k-xl.sixi) on the
 32-cell split-K kernel, against the oracle through the C ABI: decode, speculative verify (96 rows
 per group as one lane of three row groups), ragged streams, an explicit mask and f16 Q; the
-prefill kernel for 256-dim heads; q8_0 caches on the 32-cell q8_0 kernel (one lane, up to three
-row groups of two row tiles) and, for prefill-sized blocks, on the prefill kernel over q8_0 tiles
+prefill kernel for 256-dim heads; q8_0 caches on the 16-cell kernel (up to 48 rows, lengths
+only: q8_0 dequantised in registers), on the 32-cell q8_0 kernel (explicit masks, more rows: one
+lane, up to three row groups of two row tiles) and, for prefill-sized blocks, on the prefill
+kernel over q8_0 tiles
 converted in LDS (rows that are not 16-byte aligned: through the f16 staging).  Bar: max-abs <=
 2e-3 and rel-L2 <= 1e-3 on the f32 output."""
 import sys
@@ -118,9 +120,13 @@ def test_d256_prefill_explicit_mask(fa):
 
 
 @pytest.mark.parametrize("label,kv_len,q_len,explicit", [
-    ("q8_0 decode", [3000, 70], [1, 1], False),                 # 6 rows: one row group of one tile
-    ("q8_0 24 rows", [1800, 640], [4, 3], False),               # one row group of two tiles
-    ("q8_0 48 rows (run as 64)", [2500, 90], [8, 8], False),    # two row groups
+    ("q8_0 decode", [3000, 70], [1, 1], False),                 # 6 rows: the 16-cell kernel, one tile
+    ("q8_0 24 rows", [1800, 640], [4, 3], False),               # 16-cell kernel, two row tiles
+    ("q8_0 36 rows", [2300, 17, 5000], [6, 6, 2], False),       # 16-cell kernel, three row tiles
+    ("q8_0 48 rows", [2500, 90], [8, 8], False),                # 16-cell kernel, three row tiles
+    ("q8_0 24 rows, one long stream", [30000], [4], False),     # 16-cell kernel, many pieces
+    ("q8_0 ragged batch", [700, 12000, 3, 255, 4096, 1, 9000, 513], [4, 6, 6, 1, 5, 6, 3, 4], False),
+    ("q8_0 24 rows, explicit mask", [1800, 640], [4, 3], True),  # the 32-cell q8_0 kernel
     ("q8_0 verify", [1200, 400], [16, 7], False),               # 96 rows: three row groups
     ("q8_0 verify, one long stream", [20000], [16], False),     # many pieces
     ("q8_0 verify, explicit mask", [1500, 333], [16, 5], True),
@@ -131,7 +137,8 @@ def test_d256_prefill_explicit_mask(fa):
     ("q8_0 prefill, explicit mask", [300, 40], [150, 260], True),
 ])
 def test_d256_q8_0(fa, label, kv_len, q_len, explicit):
-    """q8_0 caches of 256-dim heads: split-K calls run the 32-cell q8_0 kernel on one lane;
+    """q8_0 caches of 256-dim heads: split-K calls of up to 48 rows with lengths only run the
+    16-cell kernel (q8_0 dequantised in registers), the others the 32-cell q8_0 kernel on one lane;
     prefill-sized blocks stage K, V and Q as f16 (a small cache) or, with
     FLAG_BOUNDED_WORKSPACE, run the prefill kernel that converts each tile's q8_0 rows in LDS:
     both against the oracle, and bitwise against each other."""
