@@ -1,11 +1,13 @@
 """Benchmark of the MI355X attention hot path (one GPU).
 
 Headline workload: batched speculative verify -- 32 streams x 16 drafted rows, block-causal,
-per-stream cached lengths drawn from [512, 16384], 24 q-heads / 4 kv-heads x 128, f16 KV in
-per-stream 256-cell pages, f32 Q -- one attention layer per step.  A step is one call of
-the C ABI (sixi_attn_forward), i.e. the split-K kernel (decode_wide, 32-cell steps)
-plus its merge kernel, timed with HIP events on the stream the library launches on, inputs
-resident in HBM.
+per-stream cached lengths drawn from [512, 16384], 24 q-heads / 4 kv-heads x 128, f32 Q, f16
+KV in the page pool (every stream's 256-cell pages at shuffled pool positions, read through
+the page table; each page head-major, [kv-head][256 cells][D]) -- one attention layer per
+step.  The same call over llama.cpp's token-major cell rows (in pages, and as one contiguous
+cache per stream) is reported beside it.  A step is one call of the C ABI
+(sixi_attn_forward), i.e. the split-K kernel (decode_wide, 32-cell steps) plus its merge
+kernel, timed with HIP events on the stream the library launches on, inputs resident in HBM.
 
 Prints one JSON line: value = algorithmic HBM GB/s of the verify call (K/V of every attended
 cell + Q + O, counted once) at the median per-call time (p10/p90 beside it); roofline = that
@@ -103,9 +105,12 @@ def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None, bounded
     return total / steps, per
 
 
-def time_paged(fa, w, dev, steps: int, warmup: int) -> dict:
+def time_paged(fa, w, dev, steps: int, warmup: int, head_major: bool = False, out=None):
     """The workload's call with K and V in a page pool (include/sixi_attn.h page_table): each
-    stream's 256-cell pages placed at shuffled pool pages (seeded), read through the table."""
+    stream's 256-cell pages placed at shuffled pool pages (seeded), read through the table.
+    head_major: each page holds its kv-heads one after the other ([Hkv][256 cells][D], the
+    page pool's layout: a kv-head's cells of a page are one contiguous 64 KB run); otherwise
+    token-major ([256 cells][Hkv][D], llama.cpp's cell rows).  Returns (ms, per-call ms, pages)."""
     import numpy as np
     import torch
 
@@ -120,10 +125,15 @@ def time_paged(fa, w, dev, steps: int, warmup: int) -> dict:
     pools = []
     for name in ("k", "v"):
         c = dev[name]
-        pool = torch.empty((n_pages, sa.PAGE_CELLS) + tuple(c.shape[2:]), dtype=c.dtype, device="cuda")
-        pool[idx] = c.reshape(n_pages, sa.PAGE_CELLS, *c.shape[2:])
+        Hkv, X = c.shape[2], c.shape[3]
+        if head_major:
+            pool = torch.empty((n_pages, Hkv, sa.PAGE_CELLS, X), dtype=c.dtype, device="cuda").permute(0, 2, 1, 3)
+        else:
+            pool = torch.empty((n_pages, sa.PAGE_CELLS, Hkv, X), dtype=c.dtype, device="cuda")
+        pool[idx] = c.reshape(n_pages, sa.PAGE_CELLS, Hkv, X)
         pools.append(pool)
-    out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
+    if out is None:
+        out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
 
     def call():
@@ -141,10 +151,8 @@ def time_paged(fa, w, dev, steps: int, warmup: int) -> dict:
         ev[i + 1].record(stream)
     torch.cuda.synchronize()
     per_call = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    res = summarize(w, ev[0].elapsed_time(ev[steps]) / steps, per_call)
-    res["pages"] = n_pages
     del pools
-    return res
+    return ev[0].elapsed_time(ev[steps]) / steps, per_call, n_pages
 
 
 def ws_bytes(fa, w, dev, mask=None, bounded=False) -> int:
@@ -639,7 +647,9 @@ def main() -> int:
     dev = wl.to_device(host)
     _log(f"timing {args.steps} steps after {args.warmup} warm-up")
     out = torch.empty((w.S, w.n_q, w.H, w.D), dtype=torch.float32, device="cuda")
-    ms, per = time_calls(fa, w, dev, args.steps, args.warmup, out=out)
+    # the headline: the cache in the page pool's own layout (shuffled 256-cell pages, each page
+    # head-major), read through the page table
+    ms, per, n_pages = time_paged(fa, w, dev, args.steps, args.warmup, head_major=True, out=out)
     head = summarize(w, ms, per)
     gbs = head["GBps"]
     _log(f"verify: median {head['us_median']} us/call (mean {head['us']}), {gbs} GB/s, {head['TFLOPs']} TFLOP/s")
@@ -661,9 +671,13 @@ def main() -> int:
         "data": "synthetic (PCG32 seed 0x51A70003, N(0,1))",
         "config": {
             "workload": "batched speculative verify: 32 streams x 16 rows, block-causal, cached lengths "
-                        "U[512,16384] (seeded), 24 q-heads / 4 kv-heads x 128, f16 KV in 256-cell pages, f32 Q",
+                        "U[512,16384] (seeded), 24 q-heads / 4 kv-heads x 128, f32 Q, f16 KV in the page pool: "
+                        "256-cell pages at shuffled pool positions, read through the page table, each page "
+                        "head-major ([kv-head][256 cells][128]); llama.cpp's token-major cells beside it "
+                        "(verify_token_major_pages, verify_contiguous)",
             "streams": w.S, "rows_per_stream": 16, "mean_cached_len": round(sum(w.kv_len) / w.S, 1),
-            "bytes_per_call": w.bytes(), "flops_per_call": w.flops(),
+            "bytes_per_call": w.bytes(), "flops_per_call": w.flops(), "pool_pages": n_pages,
+            "page_layout": "head-major",
         },
         "value_stat": "median of the per-call times (HIP events between consecutive calls); "
                       "ms_per_step is the mean over the bracketed steps; before the warm-up steps the call "
@@ -688,9 +702,14 @@ def main() -> int:
         },
     }
 
-    # the same verify over a paged cache: every stream's 256-cell pages shuffled over one pool
-    result["verify_paged"] = time_paged(fa, w, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
-    _log(f"verify, paged KV: {result['verify_paged']}")
+    # the same verify with llama.cpp's token-major cell rows: in the page pool, and as one
+    # contiguous cache per stream (the ggml hook's layout)
+    msp, perp, _ = time_paged(fa, w, dev, max(20, args.steps // 2), max(5, args.warmup // 2), head_major=False)
+    result["verify_token_major_pages"] = summarize(w, msp, perp)
+    _log(f"verify, token-major pages: {result['verify_token_major_pages']}")
+    msc, perc = time_calls(fa, w, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
+    result["verify_contiguous"] = summarize(w, msc, perc)
+    _log(f"verify, contiguous token-major cache: {result['verify_contiguous']}")
 
     # the same verify with the block-causal mask handed over as an explicit ggml KQ mask (the
     # ggml FLASH_ATTN_EXT drop-in path)

@@ -44,14 +44,17 @@ def _nan_fill(t):
         t.fill_(float("nan"))
 
 
-def _paginate(cache, perm, n_pages):
+def _paginate(cache, perm, n_pages, head_major=False):
     """cache [S, cap, Hkv, X] -> (pool [n_pages, P, Hkv, X], page table [S, cap/P] int32) with
-    stream s's page i at pool page perm[s * cap/P + i]."""
+    stream s's page i at pool page perm[s * cap/P + i].  head_major: each page stores its kv-heads
+    one after the other ([n_pages, Hkv, P, X] in memory, viewed as [n_pages, P, Hkv, X])."""
     S, cap = cache.shape[0], cache.shape[1]
     per = cap // P
-    pool = torch.empty((n_pages,) + tuple(cache.shape[2:]), dtype=cache.dtype, device=cache.device)
-    pool = pool.unsqueeze(1).expand(n_pages, P, *cache.shape[2:]).contiguous()
-    _nan_fill(pool)
+    Hkv, X = cache.shape[2], cache.shape[3]
+    base = torch.empty((n_pages, Hkv, P, X) if head_major else (n_pages, P, Hkv, X), dtype=cache.dtype,
+                       device=cache.device)
+    _nan_fill(base)
+    pool = base.permute(0, 2, 1, 3) if head_major else base
     table = torch.tensor(np.asarray(perm[:S * per], dtype=np.int32).reshape(S, per), device=cache.device)
     idx = table.reshape(-1).long()
     pool[idx] = cache.reshape(S * per, P, *cache.shape[2:])
@@ -75,8 +78,12 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("head_major", [False, True], ids=["token-major pages", "head-major pages"])
 @pytest.mark.parametrize("label,kv_type,D,kv_len,q_len,H,Hkv,explicit", CASES, ids=[c[0] for c in CASES])
-def test_paged_equals_contiguous(fa, label, kv_type, D, kv_len, q_len, H, Hkv, explicit):
+def test_paged_equals_contiguous(fa, label, kv_type, D, kv_len, q_len, H, Hkv, explicit, head_major):
+    """The pool's pages may hold a page token-major (cell rows of all kv-heads together, as
+    llama.cpp's cache) or head-major (each kv-head's 256 cells together): the kernels take the
+    strides as they are, so both give the contiguous cache's output bit for bit."""
     w = wl.Workload(label, 0x51A7_9300 + len(label), len(kv_len), kv_len, q_len, H=H, Hkv=Hkv, D=D, kv_type=kv_type)
     host = wl.make_host(w, poison=not explicit)
     dev = wl.to_device(host)
@@ -85,13 +92,13 @@ def test_paged_equals_contiguous(fa, label, kv_type, D, kv_len, q_len, H, Hkv, e
     n_pages = S * per + 5
     rng = np.random.default_rng(len(label))
     perm = rng.permutation(n_pages)
-    kpool, table = _paginate(dev["k"], perm, n_pages)
-    vpool, _ = _paginate(dev["v"], perm, n_pages)
+    kpool, table = _paginate(dev["k"], perm, n_pages, head_major)
+    vpool, _ = _paginate(dev["v"], perm, n_pages, head_major)
     mask = None
     if explicit:
         mask = torch.from_numpy(wl.kq_mask(cap, w.n_q, w.kv_len, w.q_len)).view(torch.float16).cuda()
     mode = sa.MASK_EXPLICIT if explicit else sa.MASK_BLOCK_CAUSAL
-    _say(f"{label}: S={S} kv_len={kv_len} q_len={q_len} D={D} type={kv_type} pages={n_pages}")
+    _say(f"{label}: S={S} kv_len={kv_len} q_len={q_len} D={D} type={kv_type} pages={n_pages} head_major={head_major}")
     out_c = torch.full((S, w.n_q, H, D), float("nan"), device="cuda")
     out_p = torch.full_like(out_c, float("nan"))
     fa(dev["q"], dev["k"], dev["v"], out_c, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=mode, mask=mask)
@@ -140,8 +147,9 @@ def test_paged_matches_the_oracle_on_shared_pages(fa):
     assert m["max_abs"] <= MAX_ABS and m["rel_l2"] <= REL_L2, m
 
 
+@pytest.mark.parametrize("head_major", [False, True], ids=["token-major pages", "head-major pages"])
 @pytest.mark.parametrize("kv_type", [sa.TYPE_F16, sa.TYPE_Q8_0])
-def test_pool_seq_cp_shares_and_writes_copy_on_write(fa, kv_type):
+def test_pool_seq_cp_shares_and_writes_copy_on_write(fa, kv_type, head_major):
     """Through the page pool: stream 0 is written (kv_write through the page table), copied to
     stream 1 with seq_cp (no cell moves: stream 1's row of the page table is stream 0's),
     then both append 16 different rows -- the shared last page is copied for the first
@@ -153,10 +161,12 @@ def test_pool_seq_cp_shares_and_writes_copy_on_write(fa, kv_type):
     dt = torch.uint8 if kv_type == sa.TYPE_Q8_0 else torch.float16
     max_pages, n_pages = 4, 9
     pool = sa.KvPool(n_pages, 2, max_pages)
-    kp = torch.zeros((n_pages, P, Hkv, row), dtype=dt, device="cuda")
-    vp = torch.zeros_like(kp)
-    _nan_fill(kp)
-    _nan_fill(vp)
+    shape = (n_pages, Hkv, P, row) if head_major else (n_pages, P, Hkv, row)
+    kb, vb = torch.zeros(shape, dtype=dt, device="cuda"), torch.zeros(shape, dtype=dt, device="cuda")
+    _nan_fill(kb)
+    _nan_fill(vb)
+    kp = kb.permute(0, 2, 1, 3) if head_major else kb  # [n_pages, P, Hkv, row] either way
+    vp = vb.permute(0, 2, 1, 3) if head_major else vb
     pool.attach(kp, D)
     pool.attach(vp, D)
     cap = max_pages * P
@@ -223,8 +233,9 @@ def test_pool_seq_cp_shares_and_writes_copy_on_write(fa, kv_type):
     pool.close()
 
 
+@pytest.mark.parametrize("head_major", [False, True], ids=["token-major pages", "head-major pages"])
 @pytest.mark.parametrize("q8", [False, True])
-def test_prologue_store_through_the_page_table(q8):
+def test_prologue_store_through_the_page_table(q8, head_major):
     """The layer prologue's fused KV store (include/sixi_layer.h) into a paged cache writes the
     same bytes, cell for cell, as into the contiguous cache; the pages the block does not touch
     (and the cells of touched pages outside the block) keep their bytes."""
@@ -246,8 +257,8 @@ def test_prologue_store_through_the_page_table(q8):
         kc = (kc.to(torch.float16) - 127.0) / 64.0
     vc = kc.clone()
     perm = np.random.default_rng(3).permutation(n_pages)
-    kp, table = _paginate(kc, perm, n_pages)
-    vp, _ = _paginate(vc, perm, n_pages)
+    kp, table = _paginate(kc, perm, n_pages, head_major)
+    vp, _ = _paginate(vc, perm, n_pages, head_major)
     kp0, vp0 = kp.clone(), vp.clone()
     kl = torch.tensor(kv_len, dtype=torch.int32, device="cuda")
     ql = torch.tensor(q_len, dtype=torch.int32, device="cuda")
