@@ -25,7 +25,8 @@ times only the chunked causal prefill (two 2048-row chunks), for profiling that 
 staging), and their `_bounded` forms with FLAG_BOUNDED_WORKSPACE (q8_0 tiles converted in LDS).
 `verify_q8`, `verify_d256` and `verify_d256_q8` time the batched verify alone over a q8_0 cache
 (128-dim heads) and at 256-dim heads over an f16 or q8_0 cache; `verify_op` the engine's own
-operating point (32 streams x q_len 4 and 6, 256-dim heads, f16 and q8_0 caches).
+operating point (32 streams x q_len 4 and 6, 256-dim heads, f16 and q8_0 caches); `headline`
+the headline call alone (for the profiler).
 """
 from __future__ import annotations
 
@@ -44,7 +45,7 @@ METRIC = "verify-attn µs/layer & HBM GB/s (32 streams×16 tok, 8k ctx); prefill
 HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3  # published dense FP32 (vector) peak
-TRAFFIC_PROFILE = ROOT / "profiles" / "decode_verify_b32_counters.txt"
+TRAFFIC_PROFILE = ROOT / "profiles" / "verify_b32_headmajor_pages.txt"
 
 
 def _log(msg: str) -> None:
@@ -72,6 +73,35 @@ def _precondition(fn, seconds: float = PRECONDITION_S) -> None:
         torch.cuda.synchronize()
 
 
+def _timed(call, steps: int, warmup: int):
+    """(ms per call, per-call ms list): after the preconditioning and `warmup` untimed calls,
+    `steps` calls bracketed by synchronisation and one event pair -- the timed region, whose
+    mean is the rate reported -- then the same number of calls again with an event after each,
+    for the distribution (those events cost about 2 us per call on MI355X, so the per-call
+    figures sit slightly above the bracketed mean)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    _precondition(call)
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        call()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return ms, [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+
+
 def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None, bounded=False):
     """Per-call GPU times (ms) with events on the stream the library launches on.  With `mask`
     (a ggml f16 KQ mask) the calls take the explicit-mask path instead of w.mask_mode;
@@ -90,19 +120,7 @@ def time_calls(fa, w, dev, steps: int, warmup: int, out=None, mask=None, bounded
         fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
            mask_mode=mode, mask=mask, stream=stream.cuda_stream, bounded_workspace=bounded)
 
-    _precondition(call)
-    for _ in range(warmup):
-        call()
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    ev[0].record(stream)
-    for i in range(steps):
-        call()
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    total = ev[0].elapsed_time(ev[steps])
-    return total / steps, per
+    return _timed(call, steps, warmup)
 
 
 def time_paged(fa, w, dev, steps: int, warmup: int, head_major: bool = False, out=None):
@@ -140,19 +158,9 @@ def time_paged(fa, w, dev, steps: int, warmup: int, head_major: bool = False, ou
         fa(dev["q"], pools[0], pools[1], out, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=w.mask_mode,
            stream=stream.cuda_stream, page_table=table)
 
-    _precondition(call)
-    for _ in range(warmup):
-        call()
-    torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    ev[0].record(stream)
-    for i in range(steps):
-        call()
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    per_call = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    ms, per_call = _timed(call, steps, warmup)
     del pools
-    return ev[0].elapsed_time(ev[steps]) / steps, per_call, n_pages
+    return ms, per_call, n_pages
 
 
 def ws_bytes(fa, w, dev, mask=None, bounded=False) -> int:
@@ -169,8 +177,8 @@ def ws_bytes(fa, w, dev, mask=None, bounded=False) -> int:
 
 
 def summarize(w, ms: float, per) -> dict:
-    """Mean (`us`, over the bracketed calls), median and p10/p90 of the per-call times; the
-    rates are taken at the median."""
+    """`us` and the rates: the mean over the bracketed calls (the timed region); median and
+    p10/p90 of the per-call times (a second pass with an event after each call)."""
     per_sorted = sorted(per)
     n = len(per_sorted)
     med = statistics.median(per_sorted)
@@ -179,9 +187,9 @@ def summarize(w, ms: float, per) -> dict:
         "us_median": round(med * 1e3, 2),
         "us_p10_p50_p90": [round(per_sorted[n // 10] * 1e3, 2), round(per_sorted[n // 2] * 1e3, 2),
                            round(per_sorted[(9 * n) // 10] * 1e3, 2)],
-        "GBps": round(w.bytes() / (med * 1e-3) / 1e9, 1),
-        "TFLOPs": round(w.flops() / (med * 1e-3) / 1e12, 2),
-        "GBps_mean": round(w.bytes() / (ms * 1e-3) / 1e9, 1),
+        "GBps": round(w.bytes() / (ms * 1e-3) / 1e9, 1),
+        "TFLOPs": round(w.flops() / (ms * 1e-3) / 1e12, 2),
+        "GBps_median": round(w.bytes() / (med * 1e-3) / 1e9, 1),
         "bytes": w.bytes(),
         "flops": w.flops(),
     }
@@ -527,6 +535,21 @@ def operating_point(q_len: int, q8: bool):
 OPERATING_POINTS = tuple((ql, q8) for q8 in (False, True) for ql in (4, 6))
 
 
+def headline_only(steps: int, warmup: int) -> int:
+    """The headline call alone (the page pool with head-major pages), for the profiler."""
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    fa = sa.FlashAttnExt()
+    w = wl.config("batched_verify")
+    dev = wl.to_device(wl.make_host(w))
+    ms, per, n_pages = time_paged(fa, w, dev, max(1, steps), warmup, head_major=True)
+    r = summarize(w, ms, per)
+    _log(f"headline: {r}")
+    print(json.dumps(r), flush=True)
+    return 0
+
+
 def verify_op_only(steps: int, warmup: int) -> int:
     """The four operating-point verify calls alone (32 streams, q_len 4 and 6, 256-dim heads,
     f16 and q8_0 caches): eager median and graph-replay time per call, GB/s of each."""
@@ -602,7 +625,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_q8_bounded",
                                                                "prefill_d256_q8", "prefill_d256_q8_bounded", "layer",
-                                                               "gdn", "verify_q8", "verify_d256", "verify_d256_q8", "verify_op"])
+                                                               "gdn", "verify_q8", "verify_d256", "verify_d256_q8", "verify_op",
+                                                               "headline"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -631,6 +655,8 @@ def main() -> int:
         return verify_q8_only(args.steps, args.warmup)
     if args.workload == "verify_op":
         return verify_op_only(args.steps, args.warmup)
+    if args.workload == "headline":
+        return headline_only(args.steps, args.warmup)
     if args.workload.startswith("verify_d256"):
         return verify_q8_only(args.steps, args.warmup, head_dim=256, q8=args.workload.endswith("_q8"))
 
@@ -679,12 +705,13 @@ def main() -> int:
             "bytes_per_call": w.bytes(), "flops_per_call": w.flops(), "pool_pages": n_pages,
             "page_layout": "head-major",
         },
-        "value_stat": "median of the per-call times (HIP events between consecutive calls); "
-                      "ms_per_step is the mean over the bracketed steps; before the warm-up steps the call "
+        "value_stat": "algorithmic bytes / the mean time of the steps bracketed by synchronisation "
+                      "(ms_per_step); the per-call median and p10/p90 come from a second pass with an event "
+                      "after every call (those events add ~2 us per call); before the warm-up steps the call "
                       f"runs untimed for {PRECONDITION_S * 1e3:.0f} ms so that the timed steps see the GPU's "
                       "settled clocks, not the power-management dip of calls ~11-100 after an idle period",
-        "us_per_layer": head["us_median"],
-        "us_per_layer_mean": head["us"],
+        "us_per_layer": head["us"],
+        "us_per_layer_median": head["us_median"],
         "us_per_layer_p10_p50_p90": head["us_p10_p50_p90"],
         "workspace_bytes": ws_bytes(fa, w, dev),
         "verify_tflops": head["TFLOPs"],
