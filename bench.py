@@ -26,7 +26,9 @@ staging), and their `_bounded` forms with FLAG_BOUNDED_WORKSPACE (q8_0 tiles con
 `verify_q8`, `verify_d256` and `verify_d256_q8` time the batched verify alone over a q8_0 cache
 (128-dim heads) and at 256-dim heads over an f16 or q8_0 cache; `verify_op` the engine's own
 operating point (32 streams x q_len 4 and 6, 256-dim heads, f16 and q8_0 caches); `headline`
-the headline call alone (for the profiler).
+the headline call alone (for the profiler); `verify_mask` and `prefill_mask` the verify (over
+the contiguous cache) and the prefill with their masks handed over as llama.cpp's explicit f16
+KQ mask (the mask pre-pass, then the kernels it chooses between).
 """
 from __future__ import annotations
 
@@ -606,14 +608,36 @@ def verify_q8_only(steps: int, warmup: int, head_dim: int = 128, q8: bool = True
     return 0
 
 
-def prefill_only(steps: int, warmup: int, q8: bool = False, head_dim=None, bounded: bool = False) -> int:
+def verify_mask_only(steps: int, warmup: int) -> int:
+    """The 32 x 16 batched verify over the contiguous f16 cache with its block-causal mask handed
+    over as llama.cpp's explicit f16 KQ mask (the ggml hook's call)."""
+    import torch
+
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    fa = sa.FlashAttnExt()
+    w = wl.config("batched_verify")
+    dev = wl.to_device(wl.make_host(w))
+    mask = torch.from_numpy(wl.kq_mask(dev["k"].shape[1], w.n_q, w.kv_len, w.q_len)).view(torch.float16).cuda()
+    # the lengths-only call first, for comparison in the same trace
+    ms0, per0 = time_calls(fa, w, dev, max(1, steps), warmup)
+    ms, per = time_calls(fa, w, dev, max(1, steps), warmup, mask=mask)
+    print(json.dumps({"workload": "batched verify, explicit llama mask, contiguous f16 cache",
+                      **summarize(w, ms, per), "lengths_only": summarize(w, ms0, per0)}), flush=True)
+    return 0
+
+
+def prefill_only(steps: int, warmup: int, q8: bool = False, head_dim=None, bounded: bool = False,
+                 explicit_mask: bool = False) -> int:
     import sixi_attn as sa
 
     fa = sa.FlashAttnExt()
     tf, us, wsb = time_prefill(fa, max(1, steps), warmup, kv_type=sa.TYPE_Q8_0 if q8 else None, head_dim=head_dim,
-                               bounded=bounded)
+                               bounded=bounded, explicit_mask=explicit_mask)
     print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks" + (" over a q8_0 cache" if q8 else "") +
-                      (f", {head_dim}-dim heads" if head_dim else "") + (", bounded workspace" if bounded else ""),
+                      (f", {head_dim}-dim heads" if head_dim else "") + (", bounded workspace" if bounded else "") +
+                      (", explicit llama mask" if explicit_mask else ""),
                       "us_two_chunks": round(us, 2), "TFLOPs": round(tf, 2), "workspace_bytes": wsb}), flush=True)
     return 0
 
@@ -626,7 +650,7 @@ def main() -> int:
     ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_q8_bounded",
                                                                "prefill_d256_q8", "prefill_d256_q8_bounded", "layer",
                                                                "gdn", "verify_q8", "verify_d256", "verify_d256_q8", "verify_op",
-                                                               "headline"])
+                                                               "headline", "verify_mask", "prefill_mask"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -641,6 +665,10 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.workload == "copy":
         return copy_calibration(max(1, args.steps))
+    if args.workload == "prefill_mask":
+        return prefill_only(args.steps, args.warmup, explicit_mask=True)
+    if args.workload == "verify_mask":
+        return verify_mask_only(args.steps, args.warmup)
     if args.workload.startswith("prefill"):
         return prefill_only(args.steps, args.warmup, q8=args.workload != "prefill",
                             head_dim=256 if "d256" in args.workload else None,
@@ -773,7 +801,14 @@ def main() -> int:
                                            mask_mode=we.mask_mode), max(40, args.steps // 2), 3)
                 extra[name]["us_graph"] = round(usg, 2)
                 extra[name]["GBps_graph"] = round(we.bytes() / (usg * 1e-6) / 1e9, 1)
-                del de
+                # the same call with its block-causal mask as llama.cpp's explicit f16 KQ mask
+                # (the ggml hook's call: the mask pre-pass, then the kernels it chooses between)
+                me = torch.from_numpy(wl.kq_mask(de["k"].shape[1], we.n_q, we.kv_len, we.q_len)).view(
+                    torch.float16).cuda()
+                usm = _graph_us(lambda: fa(de["q"], de["k"], de["v"], oute, kv_len=de["kv_len"], q_len=de["q_len"],
+                                           mask_mode=sa.MASK_EXPLICIT, mask=me), max(40, args.steps // 2), 3)
+                extra[name]["us_graph_explicit_mask"] = round(usm, 2)
+                del de, me
             except sa.SixiAttnError as e:
                 extra[name] = {"unavailable": str(e)}
             _log(f"{name}: {extra[name]}")

@@ -46,7 +46,7 @@ def flags_for(src: str) -> list[str]:
     return [*HIP_FLAGS, *FILE_FLAGS.get(src, [])]
 
 
-HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "fa_q8_stage.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
+HIP_SOURCES = ["fa_decode.hip", "fa_prefill.hip", "fa_mask.hip", "fa_q8_stage.hip", "kv_write.hip", "sixi_attn_abi.cpp", "sixi_kv_abi.cpp",
                "sixi_kv_pool.cpp",
                "sixi_plan.cpp", "layer_prologue.hip", "sixi_layer_abi.cpp",
                "gdn_verify.hip", "sixi_gdn_abi.cpp"]

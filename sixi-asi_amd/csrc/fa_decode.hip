@@ -467,12 +467,14 @@ struct Piece {
     int64_t slot;  // partial slot (segment + logical work-group)
 };
 
-// One piece: tiles [tb, te) of segment (s, g).
-template <int NTW, int KV, int MODE, int D>
-__device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV, D>& sh, int causal, const Piece& pc) {
+// One piece: tiles [tb, te) of segment (s, g), for row tiles n0 .. n0 + NTW - 1 of the NTOT
+// that the launch's partial slots hold (all of them, n0 = 0, except in the per-row-tile
+// fallback of the dual kernel).
+template <int NTW, int KV, int MODE, int D, int NTOT = NTW>
+__device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTOT, KV, D>& sh, int causal, const Piece& pc,
+                                             int n0 = 0) {
     using TD = T16Dim<D>;
     constexpr int KS = TD::KS, DCH = D / 8;  // k-steps; 8-dim chunks of a Q row
-    constexpr int NTOT = NTW;
     constexpr int TL = Shape<KV>::lanes;   // tile lanes (one wave each)
     constexpr int NSLOT = Shape<KV>::slots;
     constexpr int NTHREADS = Shape<KV>::waves * 64;
@@ -491,20 +493,20 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV,
     const int G = a.Gr;                 // rows of one block row (heads of this launch)
     const int hb = g * a.G + a.hoff;    // first of those heads
     const int R = G * sd.ql;
-    const int n0 = rg * NTW;  // first row tile of this wave
+    (void)rg;
 
     // ---- Q rows of the group -> f16 B operands in LDS (row 16n+r, dims 32ks+8c..+7) ----
-    // Item idx = tid + k*NTHREADS is row idx/DCH, 8-dim chunk idx%DCH.  Every load is issued
-    // before any is used (padding rows read row 0, which every piece has), so the staging
-    // costs one memory latency.
-    constexpr int QIT = NTOT * 16 * DCH / NTHREADS;
-    static_assert(QIT * NTHREADS == NTOT * 16 * DCH, "Q items per thread");
+    // Item idx = tid + k*NTHREADS is row 16 n0 + idx/DCH, 8-dim chunk idx%DCH.  Every load is
+    // issued before any is used (padding rows read row 0, which every piece has), so the
+    // staging costs one memory latency.
+    constexpr int QIT = NTW * 16 * DCH / NTHREADS;
+    static_assert(QIT * NTHREADS == NTW * 16 * DCH, "Q items per thread");
     const char* qsrc[QIT];
     bool qok[QIT];
 #pragma unroll
     for (int k = 0; k < QIT; ++k) {
         const int idx = tid + k * NTHREADS;
-        const int row = idx / DCH;
+        const int row = 16 * n0 + idx / DCH;
         qok[k] = row < R;
         const int rr = qok[k] ? row : 0;
         qsrc[k] = a.q + (int64_t)(rr / G) * a.q_nb1 + (int64_t)(hb + rr % G) * a.q_nb2 + (int64_t)s * a.q_nb3 +
@@ -558,7 +560,7 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV,
             for (int e = 0; e < 8; ++e) hv[e] = (_Float16)xv[k][e];
         }
         const int idx = tid + k * NTHREADS;
-        const int row = idx / DCH;
+        const int row = 16 * n0 + idx / DCH;
         const int chunk = idx % DCH;  // ks = chunk/4, c = chunk%4
         const int n = row >> 4, rr = row & 15, ks = chunk >> 2, cc = chunk & 3;
         sh.t.q[(n * KS + ks) * 64 + cc * 16 + rr] = qok[k] ? as_u32x4(hv) : u32x4{0u, 0u, 0u, 0u};
@@ -684,7 +686,8 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTW, KV,
     }
 
     __syncthreads();  // every wave is past its ring (each drained its own loads)
-    if (merge_lanes<NTW, TL>(sh.mg, acc, rg, tl, lane)) {
+    auto& mg = reinterpret_cast<MergeBuf<NTW, TL / 2, TD::DT>&>(sh.mg);  // (NTW <= NTOT tiles)
+    if (merge_lanes<NTW, TL>(mg, acc, rg, tl, lane)) {
         if (tb == 0 && te == pc.nt_seg)
             write_rows(a, acc, n0, s, g, R, lane);
         else
@@ -2005,6 +2008,77 @@ void decode_wide_q8(FaArgs a, int causal) {
     for_each_piece<true>(a, sh.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide_q8<NTW, RS, MODE, D>(a, sh, causal, pc); });
 }
 
+// Explicit masks after the pre-pass (fa_mask.hip): the lengths-only block-causal body over the
+// offsets the rows imply when every row passed it, the staged-mask (or per-cell) body
+// otherwise.  Both run one grid, one slot layout and one merge, so the choice needs no host
+// round trip; the LDS is the union of the two bodies'.
+template <int NTW, int RS, int D>
+union WideDualLds {
+    WideLds<NTW, RS, D, false> fast;
+    WideLds<NTW, RS, D, true> mask;
+};
+template <int NTW, int RS, int D>
+__global__ __launch_bounds__((RS * wide_lanes<RS, D>() * 64), (RS * wide_lanes<RS, D>() * WideShape::groups_per_cu + 3) / 4)
+void decode_wide_dual(FaArgs a) {
+    __shared__ WideDualLds<NTW, RS, D> sh;
+    __shared__ int wbad[RS * wide_lanes<RS, D>()];
+    if (mask_rows_block_causal(a, wbad)) {
+        const FaArgs b = mask_as_lengths(a);
+        if (threadIdx.x < 64) build_tile_prefix(b, sh.fast.st.ps, sh.fast.st.dims);
+        __syncthreads();
+        for_each_piece<true>(b, sh.fast.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide<NTW, RS, MODE_FAST, D>(b, sh.fast, 1, pc); });
+    } else {
+        if (threadIdx.x < 64) build_tile_prefix(a, sh.mask.st.ps, sh.mask.st.dims);
+        __syncthreads();
+        for_each_piece<true>(a, sh.mask.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide<NTW, RS, MODE_MASK, D>(a, sh.mask, 0, pc); });
+    }
+}
+
+template <int NTW, int RS, int D>
+union WideQ8DualLds {
+    WideQ8Lds<NTW, RS, false, D> fast;
+    WideQ8Lds<NTW, RS, true, D> mask;
+};
+template <int NTW, int RS, int D>
+__global__ __launch_bounds__((RS * Q8Dim<D>::TL * 64), (RS * Q8Dim<D>::TL + 3) / 4)
+void decode_wide_q8_dual(FaArgs a) {
+    __shared__ WideQ8DualLds<NTW, RS, D> sh;
+    __shared__ int wbad[RS * Q8Dim<D>::TL];
+    if (mask_rows_block_causal(a, wbad)) {
+        const FaArgs b = mask_as_lengths(a);
+        if (threadIdx.x < 64) build_tile_prefix(b, sh.fast.st.ps, sh.fast.st.dims);
+        __syncthreads();
+        for_each_piece<true>(b, sh.fast.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide_q8<NTW, RS, MODE_FAST, D>(b, sh.fast, 1, pc); });
+    } else {
+        if (threadIdx.x < 64) build_tile_prefix(a, sh.mask.st.ps, sh.mask.st.dims);
+        __syncthreads();
+        for_each_piece<true>(a, sh.mask.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide_q8<NTW, RS, MODE_MASK, D>(a, sh.mask, 0, pc); });
+    }
+}
+
+// The 16-cell kernel's dual: the lengths-only body, or per row tile the per-cell body (one
+// row tile at a time fits the registers of two work-groups per CU; a mask that is not a
+// block-causal prefix then reads the piece's K/V once per row tile).
+template <int NTW, int KV, int D>
+__global__ __launch_bounds__((Shape<KV>::waves * 64), (Shape<KV>::waves * t16_groups_per_cu(D) / 4)) void
+decode_t16_dual(FaArgs a) {
+    __shared__ DecodeLds<NTW, KV, D> sh;
+    __shared__ int wbad[Shape<KV>::waves];
+    if (mask_rows_block_causal(a, wbad)) {
+        const FaArgs b = mask_as_lengths(a);
+        if (threadIdx.x < 64) build_tile_prefix(b, sh.ps);
+        __syncthreads();
+        for_each_piece<D == 256>(b, sh.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece<NTW, KV, MODE_FAST, D>(b, sh, 1, pc); });
+    } else {
+        if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);
+        __syncthreads();
+        for_each_piece<D == 256>(a, sh.ps, [&](const Piece& pc) __attribute__((always_inline)) {
+#pragma unroll 1
+            for (int n0 = 0; n0 < NTW; ++n0) decode_piece<1, KV, MODE_GENERIC, D, NTW>(a, sh, 0, pc, n0);
+        });
+    }
+}
+
 // Combines the pieces of every segment that more than one work-group touched, for segments of
 // many pieces (a few long streams: single-stream decode and verify).  grid = (S*Hkv segments,
 // rows); 256 threads = PG piece groups x D/4 threads of four dims.  Group pg folds
@@ -2227,6 +2301,104 @@ hipError_t launch_nt(const FaArgs& a_in, int mode, int causal, hipStream_t strea
     return hipGetLastError();
 }
 
+// The launches of the dual kernels: the fast launches' head-aligned split where they use it.
+template <int NTW, int RS, int D>
+hipError_t launch_wide_dual(const FaArgs& a_in, hipStream_t stream) {
+    const FaArgs a = head_split_args(a_in);
+    if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((decode_wide_dual<NTW, RS, D>), dim3(a.P), dim3(RS * wide_lanes<RS, D>() * 64), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_merge<D>(a, NTW * RS * 16, stream);
+    return hipGetLastError();
+}
+
+template <int NTW, int RS, int D>
+hipError_t launch_wide_q8_dual(const FaArgs& a_in, hipStream_t stream) {
+    const FaArgs a = head_split_args(a_in);
+    if (!slot_fits(a, NTW * RS * 16, D)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((decode_wide_q8_dual<NTW, RS, D>), dim3(a.P), dim3(RS * Q8Dim<D>::TL * 64), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_merge<D>(a, NTW * RS * 16, stream);
+    return hipGetLastError();
+}
+
+template <int NTW, int KV, int D>
+hipError_t launch_t16_dual(const FaArgs& a_in, hipStream_t stream) {
+    const FaArgs a = (D == 256) ? head_split_args(a_in) : a_in;
+    if (!slot_fits(a, NTW * 16, D)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((decode_t16_dual<NTW, KV, D>), dim3(a.P), dim3(Shape<KV>::waves * 64), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_merge<D>(a, NTW * 16, stream);
+    return hipGetLastError();
+}
+
+// Explicit-mask launches with the pre-pass's table (a.row_kl), planned as the lengths-only
+// call of the same shape: the 16-cell kernel's dual up to 48 rows (f16 and q8_0 at 128-dim
+// heads, q8_0 at 256), the 32-cell kernels' duals beyond (and for f16 at 256-dim heads).
+hipError_t launch_decode_dual(const FaArgs& a, int kv_type, int head_dim, int row_tiles, hipStream_t stream) {
+    if (!decode_wide_kernel(kv_type, row_tiles, head_dim, false)) {
+        if (kv_type == SIXI_TYPE_F16 && head_dim == 128) {
+            switch (row_tiles) {
+                case 1: return launch_t16_dual<1, SIXI_TYPE_F16, 128>(a, stream);
+                case 2: return launch_t16_dual<2, SIXI_TYPE_F16, 128>(a, stream);
+                case 3: return launch_t16_dual<3, SIXI_TYPE_F16, 128>(a, stream);
+                default: return hipErrorNotSupported;
+            }
+        }
+        if (kv_type == SIXI_TYPE_Q8_0 && head_dim == 128) {
+            switch (row_tiles) {
+                case 1: return launch_t16_dual<1, SIXI_TYPE_Q8_0, 128>(a, stream);
+                case 2: return launch_t16_dual<2, SIXI_TYPE_Q8_0, 128>(a, stream);
+                case 3: return launch_t16_dual<3, SIXI_TYPE_Q8_0, 128>(a, stream);
+                default: return hipErrorNotSupported;
+            }
+        }
+        if (kv_type == SIXI_TYPE_Q8_0 && head_dim == 256) {
+            switch (row_tiles) {
+                case 1: return launch_t16_dual<1, SIXI_TYPE_Q8_0, 256>(a, stream);
+                case 2: return launch_t16_dual<2, SIXI_TYPE_Q8_0, 256>(a, stream);
+                case 3: return launch_t16_dual<3, SIXI_TYPE_Q8_0, 256>(a, stream);
+                default: return hipErrorNotSupported;
+            }
+        }
+        return hipErrorNotSupported;
+    }
+    if (kv_type == SIXI_TYPE_F16 && head_dim == 128) {
+        switch (row_tiles) {
+            case 4: return launch_wide_dual<kWide64.ntw, kWide64.rs, 128>(a, stream);
+            case 6: return launch_wide_dual<kWide96.ntw, kWide96.rs, 128>(a, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
+    if (kv_type == SIXI_TYPE_F16 && head_dim == 256) {
+        switch (row_tiles) {
+            case 1: return launch_wide_dual<1, 1, 256>(a, stream);
+            case 2: return launch_wide_dual<2, 1, 256>(a, stream);
+            case 4: return launch_wide_dual<2, 2, 256>(a, stream);
+            case 6: return launch_wide_dual<2, 3, 256>(a, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
+    if (kv_type == SIXI_TYPE_Q8_0 && head_dim == 128) {
+        switch (row_tiles) {
+            case 4: return launch_wide_q8_dual<kWide64.ntw, kWide64.rs, 128>(a, stream);
+            case 6: return launch_wide_q8_dual<kWide96.ntw, kWide96.rs, 128>(a, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
+    if (kv_type == SIXI_TYPE_Q8_0 && head_dim == 256) {
+        switch (row_tiles) {
+            case 4: return launch_wide_q8_dual<2, 2, 256>(a, stream);
+            case 6: return launch_wide_q8_dual<2, 3, 256>(a, stream);
+            default: return hipErrorNotSupported;
+        }
+    }
+    return hipErrorNotSupported;
+}
+
 }  // namespace
 
 int decode_num_groups(const FaArgs& a, int cu_count, int per_cu) {
@@ -2243,6 +2415,7 @@ int decode_num_groups(const FaArgs& a, int cu_count, int per_cu) {
 
 hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream) {
+    if (a.row_kl) return launch_decode_dual(a, kv_type, head_dim, row_tiles, stream);
     // the 32-cell kernel's MASK mode: a staged explicit mask, no softcap, no ALiBi
     const int mode = (mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f)
                          ? ((mask_mode == SIXI_MASK_EXPLICIT && a.softcap == 0.0f && a.alibi_nlog2 == 0 && a.mask_stage)

@@ -478,10 +478,54 @@ __device__ __forceinline__ StreamDims stream_dims_from(const FaArgs& a, int q_ra
 // (such a load returns 0 and touches no memory), so they issue together, without a branch.
 __device__ __forceinline__ StreamDims stream_dims(const FaArgs& a, int s) {
     const buf_rsrc qr = make_rsrc(a.q_len, a.q_len ? (uint32_t)a.S * 4u : 0u);
-    const buf_rsrc kr = make_rsrc(a.kv_len, a.kv_len ? (uint32_t)a.S * 4u : 0u);
+    const uint32_t ks = (uint32_t)a.kv_len_stride;
+    const buf_rsrc kr = make_rsrc(a.kv_len, a.kv_len ? (uint32_t)a.S * 4u * ks : 0u);
     const int q_raw = (int)buf_ld4(qr, (uint32_t)s * 4u);
-    const int kv_raw = (int)buf_ld4(kr, (uint32_t)s * 4u);
+    const int kv_raw = (int)buf_ld4(kr, (uint32_t)s * 4u * ks);
     return stream_dims_from(a, q_raw, kv_raw);
+}
+
+// Explicit masks: whether the pre-pass found every row of every stream to be a block-causal
+// prefix with one kv offset per stream (each active row's entry >= 0 and equal to its stream's
+// row 0; rows past q_len marked idle).  Run by the whole work-group, eight entries and their
+// row-0 entries per thread and round, all loads issued before any is used (entries past the
+// table read 0, as does their row 0, which passes); `wbad` is LDS of one int per wave, free for
+// other use again when this returns (it ends with a barrier).  The result is uniform (an
+// SGPR), so the callers branch on it without divergence.
+__device__ __forceinline__ bool mask_rows_block_causal(const FaArgs& a, int* wbad) {
+    constexpr int U = 8;
+    const int n = a.S * a.n_q;
+    const int nt = (int)blockDim.x;
+    const buf_rsrc r = make_rsrc(a.row_kl, (uint32_t)n * 4u);
+    bool bad = false;
+    for (int i0 = (int)threadIdx.x; i0 < n; i0 += U * nt) {
+        int v[U], v0[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + u * nt;
+            v[u] = (int)buf_ld4(r, 4u * (uint32_t)i);
+            v0[u] = (int)buf_ld4(r, 4u * (uint32_t)(i / a.n_q * a.n_q));
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) bad |= !(v[u] == kMaskRowIdle || (v[u] == v0[u] && v[u] >= 0));
+    }
+    const bool wave_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    if ((threadIdx.x & 63) == 0) wbad[threadIdx.x >> 6] = wave_bad ? 1 : 0;
+    __syncthreads();
+    int any = 0;
+    for (int w = 0; w < nt / 64; ++w) any |= wbad[w];
+    any = __builtin_amdgcn_readfirstlane(any);
+    __syncthreads();
+    return any == 0;
+}
+// The arguments of the lengths-only body of a mask whose rows passed that test: each stream's
+// cached length is the offset its mask implies (row 0's entry of the table), block-causal.
+__device__ __forceinline__ FaArgs mask_as_lengths(const FaArgs& a) {
+    FaArgs b = a;
+    b.kv_len = a.row_kl;
+    b.kv_len_stride = a.n_q;
+    b.mask = nullptr;
+    return b;
 }
 
 // Page ids of a paged cache for one stream, 64 consecutive page indices at a time, one per

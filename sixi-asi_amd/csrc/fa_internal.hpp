@@ -28,8 +28,15 @@ struct FaArgs {
     char* out;             // row (d, h, j, s) at out + d*4 + h*o_nb1 + j*o_nb2 + s*o_nb3
     int64_t o_nb1, o_nb2, o_nb3;
 
-    const int32_t* kv_len; // device, may be null
+    const int32_t* kv_len; // device, may be null; stream s's entry at kv_len[s * kv_len_stride]
     const int32_t* q_len;  // device, may be null
+    int32_t kv_len_stride;
+
+    // explicit masks (the ggml hook): the pre-pass's result per (stream s, row j) at
+    // row_kl[s * n_q + j] -- the kv offset kl the row's mask implies when it is a block-causal
+    // prefix (zeros on cells [0, kl + j + 1), -inf on the rest of the scanned cells),
+    // kMaskNotPrefix when it is not, kMaskRowIdle for rows past the stream's q_len
+    int32_t* row_kl;
 
     const char* mask;      // EXPLICIT: f16 at mask + c*2 + j*m_nb1 + (s % m_ne3)*m_nb3
     int64_t m_nb1, m_nb3;
@@ -84,8 +91,13 @@ struct Q8StageArgs {
     char *k16, *v16, *q16;  // q16 null: Q is not staged (the prefill kernel converts it)
 };
 
+constexpr int32_t kMaskNotPrefix = INT32_MIN;
+constexpr int32_t kMaskRowIdle = INT32_MIN + 1;
+
 // Host-side launchers (defined in the .hip files).  hipErrorNotSupported = not built.
 hipError_t launch_q8_stage(const Q8StageArgs& a, hipStream_t stream);
+// The explicit-mask pre-pass (fa_mask.hip): fills a.row_kl from a.mask.
+hipError_t launch_mask_prefix(const FaArgs& a, hipStream_t stream);
 hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream);
 hipError_t launch_prefill(const FaArgs& a, int kv_type, int mask_mode, int head_dim,
@@ -152,6 +164,17 @@ inline int decode_row_tiles(int64_t rows, int head_dim, int kv_type, bool generi
     if (rt == 3 && head_dim != 256) return rt;
     return 2 * ((rt + 1) / 2);
 }
+// Explicit-mask split-K calls that take the mask pre-pass (fa_mask.hip) and its dual kernels,
+// planned as the lengths-only call of the same shape (`row_tiles` without the per-cell
+// mode): every shape of the 16-cell kernel (its fallback is the per-cell mode), and the
+// 32-cell kernels' shapes where their staged-mask mode can read the mask (mask_stage).
+inline bool mask_prepass_decode(int kv_type, int row_tiles, int head_dim, bool mask_stage) {
+    return mask_stage || !decode_wide_kernel(kv_type, row_tiles, head_dim, false);
+}
+// Rows (streams x rows per stream) of a call that takes the pre-pass: every work-group of the
+// dual kernels reads the table once.
+constexpr int64_t kMaskPrepassMaxRows = 16384;
+
 inline int64_t decode_slot_floats(int row_tiles, int head_dim) {
     // O/l rows [16*row_tiles][head_dim] f16 (head_dim/2 floats' worth), then m and l per row
     return (int64_t)row_tiles * 16 * (head_dim / 2 + 2);

@@ -97,13 +97,13 @@ __device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
 // QQ8: Q goes through ggml's conversion to the q8_0 dot type (a q8_0 cache, read as q8_0 tiles or
 // staged as f16 rows).
 template <int MODE, int D, int KV, bool QQ8>
-__device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nrb, int n_cu) {
+__device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nrb, int n_cu,
+                                             PrefillLds<D, MODE == MODE_MASK>& sh) {
     using P = PfDim<D>;
     constexpr bool Q8 = KV == SIXI_TYPE_Q8_0;
     static_assert(QQ8 || !Q8, "q8_0 tiles take a q8_0-converted Q");
     constexpr int GROUPS = P::GROUPS;
     constexpr int kKBytes = P::TILE, kVBytes = P::TILE;
-    __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int w = tid >> 6;
@@ -698,19 +698,37 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
 
 template <int MODE, int D>
 __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16(FaArgs a, int causal, int nrb, int n_cu) {
-    prefill_body<MODE, D, SIXI_TYPE_F16, false>(a, causal, nrb, n_cu);
+    __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
+    prefill_body<MODE, D, SIXI_TYPE_F16, false>(a, causal, nrb, n_cu, sh);
 }
 
 // f16 rows staged from a q8_0 cache: Q converted to the q8_0 dot type in the kernel
 template <int MODE, int D>
 __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_f16_qq8(FaArgs a, int causal, int nrb, int n_cu) {
-    prefill_body<MODE, D, SIXI_TYPE_F16, true>(a, causal, nrb, n_cu);
+    __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
+    prefill_body<MODE, D, SIXI_TYPE_F16, true>(a, causal, nrb, n_cu, sh);
 }
 
 // q8_0 KV: the same tiles, converted from q8_0 rows in place in LDS
 template <int MODE, int D>
 __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_q8(FaArgs a, int causal, int nrb, int n_cu) {
-    prefill_body<MODE, D, SIXI_TYPE_Q8_0, true>(a, causal, nrb, n_cu);
+    __shared__ PrefillLds<D, MODE == MODE_MASK> sh;
+    prefill_body<MODE, D, SIXI_TYPE_Q8_0, true>(a, causal, nrb, n_cu, sh);
+}
+
+// Explicit masks after the pre-pass (fa_mask.hip), as two launches on the stream: GATE 1 runs
+// the lengths-only block-causal body over the offsets the rows imply when every row passed the
+// pre-pass, GATE 2 the staged-mask body when one did not, and each work-group of the other
+// launch returns after reading the pre-pass's table.  (One kernel holding both bodies needs
+// more than the 256 registers per wave of two work-groups per CU.)
+template <int D, int KV, bool QQ8, int GATE>
+__global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_gated(FaArgs a, int nrb, int n_cu) {
+    __shared__ PrefillLds<D, GATE == 2> sh;
+    if (mask_rows_block_causal(a, reinterpret_cast<int*>(&sh)) != (GATE == 1)) return;
+    if constexpr (GATE == 1)
+        prefill_body<MODE_FAST, D, KV, QQ8>(mask_as_lengths(a), 1, nrb, n_cu, sh);
+    else
+        prefill_body<MODE_MASK, D, KV, QQ8>(a, 0, nrb, n_cu, sh);
 }
 
 template <int MODE, int D, int KV>
@@ -724,6 +742,21 @@ void launch_prefill_mode(const FaArgs& a, int causal, int nrb, hipStream_t strea
         hipLaunchKernelGGL((prefill_f16<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
 }
 
+template <int D, int KV>
+void launch_prefill_gated(const FaArgs& a, int nrb, hipStream_t stream) {
+    const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
+    if constexpr (KV == SIXI_TYPE_Q8_0) {
+        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_Q8_0, true, 1>), grid, block, 0, stream, a, nrb, a.P);
+        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_Q8_0, true, 2>), grid, block, 0, stream, a, nrb, a.P);
+    } else if (a.q_q8) {
+        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, true, 1>), grid, block, 0, stream, a, nrb, a.P);
+        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, true, 2>), grid, block, 0, stream, a, nrb, a.P);
+    } else {
+        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, false, 1>), grid, block, 0, stream, a, nrb, a.P);
+        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, false, 2>), grid, block, 0, stream, a, nrb, a.P);
+    }
+}
+
 }  // namespace
 
 template <int D, int KV>
@@ -735,7 +768,9 @@ hipError_t launch_prefill_d(const FaArgs& a, int mask_mode, hipStream_t stream) 
     const bool mask_only = mask_mode == SIXI_MASK_EXPLICIT && a.mask && a.softcap == 0.0f && a.alibi_nlog2 == 0 &&
                            reinterpret_cast<uintptr_t>(a.mask) % 16 == 0 && a.m_nb1 % 16 == 0 &&
                            (a.m_ne3 == 1 || a.m_nb3 % 16 == 0) && a.m_span < (int64_t)UINT32_MAX;
-    if (mask_only)
+    if (mask_only && a.row_kl)
+        launch_prefill_gated<D, KV>(a, nrb, stream);
+    else if (mask_only)
         launch_prefill_mode<MODE_MASK, D, KV>(a, causal, nrb, stream);
     else if (generic)
         launch_prefill_mode<MODE_GENERIC, D, KV>(a, causal, nrb, stream);

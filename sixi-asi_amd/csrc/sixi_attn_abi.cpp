@@ -72,8 +72,18 @@ struct Plan {
     bool q8_stage = false;     // q8_0 KV staged as f16 rows in the workspace, then the f16 kernels
     size_t stage_k = 0, stage_v = 0, stage_q = 0;  // byte offsets of the staged K, V and Q
     size_t stage_bytes = 0;    // the split-K workspace follows the staging area
+    bool mask_prepass = false; // explicit mask reduced to per-row offsets first (fa_mask.hip)
+    size_t prepass_offset = 0; // byte offset of its table (S * n_q int32), after the rest
     size_t ws_bytes = 0;
 };
+
+// Appends the pre-pass table to the workspace layout (after everything else, so that the
+// staging and split-K offsets do not move).
+void prepass_layout(Plan& pl) {
+    if (!pl.mask_prepass) return;
+    pl.prepass_offset = align_up(pl.ws_bytes, kWsAlign);
+    pl.ws_bytes = pl.prepass_offset + align_up((size_t)pl.a.S * pl.a.n_q * sizeof(int32_t), kWsAlign);
+}
 
 int cu_count_cached() {
     static int cached = -1;
@@ -210,6 +220,7 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
     a.out = static_cast<char*>(const_cast<void*>(o.data));
     a.o_nb1 = o.nb[1]; a.o_nb2 = o.nb[2]; a.o_nb3 = o.nb[3];
     a.kv_len = p->kv_len;
+    a.kv_len_stride = 1;
     a.q_len = p->q_len;
     if (mode == SIXI_MASK_EXPLICIT) {
         a.mask = static_cast<const char*>(m.data);
@@ -291,6 +302,21 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
             pl.stage_bytes = stage_bytes;
         }
     }
+    // An explicit mask alone (no softcap, no ALiBi) with 16-byte aligned rows within one 32-bit
+    // range is first reduced to the kv offset each row implies (fa_mask.hip); where every row is
+    // the block-causal prefix of its stream's offset, the dual kernels then run the lengths-only
+    // body on those offsets, and otherwise the mask.  A split-K call is then planned as the
+    // lengths-only call of its shape (mask_prepass_decode), a prefill call keeps its plan.
+    const bool mask_alone = mode == SIXI_MASK_EXPLICIT && softcap == 0.0f && a.alibi_nlog2 == 0 &&
+                            S * n_q <= sixi::kMaskPrepassMaxRows && aligned(m.data, 16) && m.nb[1] % 16 == 0 &&
+                            (m.ne[3] == 1 || m.nb[3] % 16 == 0) && a.m_span < (int64_t)UINT32_MAX;
+    if (mask_alone && !pl.splitk) pl.mask_prepass = true;
+    if (mask_alone && pl.splitk &&
+        sixi::mask_prepass_decode(pl.kv_type, sixi::decode_row_tiles(rows, pl.D, pl.kv_type, false), pl.D,
+                                  a.mask_stage != 0)) {
+        pl.mask_prepass = true;
+        pl.generic = false;
+    }
     if (pl.splitk) {
         pl.row_tiles = sixi::decode_row_tiles(rows, pl.D, pl.kv_type, pl.generic);
         a.slot_floats = sixi::decode_slot_floats(pl.row_tiles, pl.D);
@@ -307,6 +333,7 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
         if (S * H * ((n_q + 127) / 128) > (int64_t)INT32_MAX) return SIXI_E_UNSUPPORTED;
         pl.ws_bytes = pl.stage_bytes > 0 ? pl.stage_bytes : kWsAlign;
     }
+    prepass_layout(pl);
     *out = pl;
     return SIXI_OK;
 }
@@ -368,8 +395,12 @@ int run(Plan& pl, char* ws, hipStream_t stream) {
         a.k = st.k16; a.k_nb2 = row; a.k_nb1 = (int64_t)a.Hkv * row; a.k_nb3 = (int64_t)a.n_kv * a.Hkv * row;
         a.v = st.v16; a.v_nb2 = row; a.v_nb1 = a.k_nb1; a.v_nb3 = a.k_nb3;
         a.pt = nullptr;  // the staged rows are one range per stream
-        ws += pl.stage_bytes;
     }
+    if (pl.mask_prepass) {
+        a.row_kl = reinterpret_cast<int32_t*>(ws + pl.prepass_offset);
+        if (sixi::launch_mask_prefix(a, stream) != hipSuccess) return SIXI_E_BACKEND;
+    }
+    if (pl.q8_stage) ws += pl.stage_bytes;
     a.part = reinterpret_cast<float*>(ws);
     a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
     a.P = launch_groups(pl);
@@ -422,7 +453,10 @@ int sixi_attn_forward_noalloc(const sixi_attn_params* p) {
     int rc = resolve(p, &pl, kScratchBytes / 2);
     if (rc != SIXI_OK) return rc;
     // exact slots for this launch's work-groups, not the workspace bound of any launch
-    if (pl.splitk) splitk_layout(pl, (int64_t)pl.a.S * pl.a.Hkv + launch_groups(pl));
+    if (pl.splitk) {
+        splitk_layout(pl, (int64_t)pl.a.S * pl.a.Hkv + launch_groups(pl));
+        prepass_layout(pl);
+    }
     if (pl.ws_bytes > kScratchBytes) return SIXI_E_OUT_OF_BOUNDS;
     char* base = scratch_base();
     if (!base) return SIXI_E_BACKEND;

@@ -35,6 +35,7 @@ namespace sixi {
     std::abort();
 }
 hipError_t launch_q8_stage(const Q8StageArgs&, hipStream_t) { no_launch("q8 stage"); }
+hipError_t launch_mask_prefix(const FaArgs&, hipStream_t) { no_launch("mask pre-pass"); }
 hipError_t launch_decode(const FaArgs&, int, int, int, int, hipStream_t) { no_launch("decode"); }
 hipError_t launch_prefill(const FaArgs&, int, int, int, hipStream_t) { no_launch("prefill"); }
 int decode_num_groups(const FaArgs&, int cu_count, int per_cu) { return cu_count * per_cu; }
