@@ -633,12 +633,18 @@ def prefill_only(steps: int, warmup: int, q8: bool = False, head_dim=None, bound
     import sixi_attn as sa
 
     fa = sa.FlashAttnExt()
+    extra = {}
+    if explicit_mask:
+        # the lengths-only call first, for comparison in the same trace
+        tf0, us0, _ = time_prefill(fa, max(1, steps), warmup)
+        extra = {"lengths_only": {"us_two_chunks": round(us0, 2), "TFLOPs": round(tf0, 2)}}
     tf, us, wsb = time_prefill(fa, max(1, steps), warmup, kv_type=sa.TYPE_Q8_0 if q8 else None, head_dim=head_dim,
                                bounded=bounded, explicit_mask=explicit_mask)
     print(json.dumps({"workload": "prefill 4096 rows in two 2048-row chunks" + (" over a q8_0 cache" if q8 else "") +
                       (f", {head_dim}-dim heads" if head_dim else "") + (", bounded workspace" if bounded else "") +
                       (", explicit llama mask" if explicit_mask else ""),
-                      "us_two_chunks": round(us, 2), "TFLOPs": round(tf, 2), "workspace_bytes": wsb}), flush=True)
+                      "us_two_chunks": round(us, 2), "TFLOPs": round(tf, 2), "workspace_bytes": wsb, **extra}),
+          flush=True)
     return 0
 
 

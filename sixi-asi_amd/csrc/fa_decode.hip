@@ -1,5 +1,5 @@
 // fa_decode.hip -- split-K flash-decoding for single-token decode and speculative verify
-// on gfx950 (head_dim 128, f16 or q8_0 KV, up to 96 rows per GQA group).
+// on gfx950 (head_dim 128 and 256, f16 or q8_0 KV, up to 96 rows per GQA group).
 //
 // Work decomposition.  A segment is one (stream s, kv-head g): nt_s tiles of KV cells, and
 // all R = G*q_len_s query rows of the GQA group ride along with every tile, so each K/V
@@ -13,16 +13,23 @@
 // segment in a fixed order (decode_merge_rows; decode_merge_pieces for segments of many pieces).  The kernel boundary orders the two launches, so
 // neither needs device-scope fences or atomics.
 //
-// Two kernels share this split:
-//   decode_d128 (<= 48 rows, and q8_0 KV): tiles of 16 cells; two work-groups of four
-//     waves per CU, the waves independent tile lanes with private LDS rings (no barrier
-//     in the tile loop).  Described next.
-//   decode_wide (f16 KV: 49..96 rows of 128-dim heads, any rows of 256-dim heads): steps of
-//     32 cells; described further down.
+// Three kernels share this split:
+//   decode_t16 (<= 48 rows: f16 and q8_0 at 128-dim heads, q8_0 at 256): tiles of 16 cells;
+//     four waves per work-group (two work-groups per CU at 128-dim heads, one at 256), the
+//     waves independent tile lanes with private LDS rings (no barrier in the tile loop).
+//     Described next.
+//   decode_wide (f16 KV: 49..96 rows of 128-dim heads, any rows of 256-dim heads, and f16
+//     calls under a mask or softcap): steps of 32 cells; described further down.
+//   decode_wide_q8 (q8_0 KV beyond the 16-cell kernel): the 32-cell kernel over q8_0 rows
+//     converted to f16 in LDS.
+// Calls with an explicit ggml mask first run the mask pre-pass (fa_mask.hip); their kernels
+// (the *_dual forms) then choose on the device between the lengths-only body over the offsets
+// the mask implies and the mask body.
 // K/V reach LDS by direct global->LDS loads (buffer_load_dword{,x4} ... lds), so bytes in
 // flight cost no VGPRs.
 //
-// decode_d128, per 16-cell tile and wave:
+// decode_t16, per 16-cell tile and wave (128-dim heads; 256-dim heads run twice the k-steps
+// and output tiles):
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = 16 cells x 32 dims straight from the ring
 //                 (lane (r, c) holds cell r, dims 32ks+8c..+7), B = Q^T from LDS;
 //                 lane (r, c) receives cells 4c..4c+3 of row r;
@@ -2022,10 +2029,11 @@ __global__ __launch_bounds__((RS * wide_lanes<RS, D>() * 64), (RS * wide_lanes<R
 void decode_wide_dual(FaArgs a) {
     __shared__ WideDualLds<NTW, RS, D> sh;
     __shared__ int wbad[RS * wide_lanes<RS, D>()];
-    if (mask_rows_block_causal(a, wbad)) {
-        const FaArgs b = mask_as_lengths(a);
-        if (threadIdx.x < 64) build_tile_prefix(b, sh.fast.st.ps, sh.fast.st.dims);
-        __syncthreads();
+    static_assert(RS * wide_lanes<RS, D>() >= 2, "the table is read by the waves after the first");
+    // the first wave builds the lengths body's cost line while the others read the table
+    const FaArgs b = mask_as_lengths(a);
+    if (threadIdx.x < 64) build_tile_prefix(b, sh.fast.st.ps, sh.fast.st.dims);
+    if (mask_rows_block_causal(a, wbad, 64)) {
         for_each_piece<true>(b, sh.fast.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide<NTW, RS, MODE_FAST, D>(b, sh.fast, 1, pc); });
     } else {
         if (threadIdx.x < 64) build_tile_prefix(a, sh.mask.st.ps, sh.mask.st.dims);
@@ -2044,10 +2052,10 @@ __global__ __launch_bounds__((RS * Q8Dim<D>::TL * 64), (RS * Q8Dim<D>::TL + 3) /
 void decode_wide_q8_dual(FaArgs a) {
     __shared__ WideQ8DualLds<NTW, RS, D> sh;
     __shared__ int wbad[RS * Q8Dim<D>::TL];
-    if (mask_rows_block_causal(a, wbad)) {
-        const FaArgs b = mask_as_lengths(a);
-        if (threadIdx.x < 64) build_tile_prefix(b, sh.fast.st.ps, sh.fast.st.dims);
-        __syncthreads();
+    static_assert(RS * Q8Dim<D>::TL >= 2, "the table is read by the waves after the first");
+    const FaArgs b = mask_as_lengths(a);
+    if (threadIdx.x < 64) build_tile_prefix(b, sh.fast.st.ps, sh.fast.st.dims);
+    if (mask_rows_block_causal(a, wbad, 64)) {
         for_each_piece<true>(b, sh.fast.st.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece_wide_q8<NTW, RS, MODE_FAST, D>(b, sh.fast, 1, pc); });
     } else {
         if (threadIdx.x < 64) build_tile_prefix(a, sh.mask.st.ps, sh.mask.st.dims);
@@ -2064,10 +2072,10 @@ __global__ __launch_bounds__((Shape<KV>::waves * 64), (Shape<KV>::waves * t16_gr
 decode_t16_dual(FaArgs a) {
     __shared__ DecodeLds<NTW, KV, D> sh;
     __shared__ int wbad[Shape<KV>::waves];
-    if (mask_rows_block_causal(a, wbad)) {
-        const FaArgs b = mask_as_lengths(a);
-        if (threadIdx.x < 64) build_tile_prefix(b, sh.ps);
-        __syncthreads();
+    static_assert(Shape<KV>::waves >= 2, "the table is read by the waves after the first");
+    const FaArgs b = mask_as_lengths(a);
+    if (threadIdx.x < 64) build_tile_prefix(b, sh.ps);
+    if (mask_rows_block_causal(a, wbad, 64)) {
         for_each_piece<D == 256>(b, sh.ps, [&](const Piece& pc) __attribute__((always_inline)) { decode_piece<NTW, KV, MODE_FAST, D>(b, sh, 1, pc); });
     } else {
         if (threadIdx.x < 64) build_tile_prefix(a, sh.ps);

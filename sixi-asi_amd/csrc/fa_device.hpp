@@ -487,18 +487,21 @@ __device__ __forceinline__ StreamDims stream_dims(const FaArgs& a, int s) {
 
 // Explicit masks: whether the pre-pass found every row of every stream to be a block-causal
 // prefix with one kv offset per stream (each active row's entry >= 0 and equal to its stream's
-// row 0; rows past q_len marked idle).  Run by the whole work-group, eight entries and their
-// row-0 entries per thread and round, all loads issued before any is used (entries past the
-// table read 0, as does their row 0, which passes); `wbad` is LDS of one int per wave, free for
-// other use again when this returns (it ends with a barrier).  The result is uniform (an
-// SGPR), so the callers branch on it without divergence.
-__device__ __forceinline__ bool mask_rows_block_causal(const FaArgs& a, int* wbad) {
+// row 0; rows past q_len marked idle).  Called by the whole work-group; the threads from
+// t_first on read the table, eight entries and their row-0 entries per thread and round, all
+// loads issued before any is used (entries past the table read 0, as does their row 0, which
+// passes), so the waves below t_first can do other work meanwhile (the decode kernels' first
+// wave builds the lengths body's cost line).  `wbad` is LDS of one int per wave, free for
+// other use again when this returns (it ends with a barrier, which also publishes what the
+// other waves wrote to LDS before it).  The result is uniform (an SGPR), so the callers branch
+// on it without divergence.
+__device__ __forceinline__ bool mask_rows_block_causal(const FaArgs& a, int* wbad, int t_first = 0) {
     constexpr int U = 8;
     const int n = a.S * a.n_q;
-    const int nt = (int)blockDim.x;
+    const int nt = (int)blockDim.x - t_first;
     const buf_rsrc r = make_rsrc(a.row_kl, (uint32_t)n * 4u);
     bool bad = false;
-    for (int i0 = (int)threadIdx.x; i0 < n; i0 += U * nt) {
+    for (int i0 = (int)threadIdx.x - t_first; i0 >= 0 && i0 < n; i0 += U * nt) {
         int v[U], v0[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -513,7 +516,7 @@ __device__ __forceinline__ bool mask_rows_block_causal(const FaArgs& a, int* wba
     if ((threadIdx.x & 63) == 0) wbad[threadIdx.x >> 6] = wave_bad ? 1 : 0;
     __syncthreads();
     int any = 0;
-    for (int w = 0; w < nt / 64; ++w) any |= wbad[w];
+    for (int w = 0; w < (int)blockDim.x / 64; ++w) any |= wbad[w];
     any = __builtin_amdgcn_readfirstlane(any);
     __syncthreads();
     return any == 0;
