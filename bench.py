@@ -874,6 +874,11 @@ def main() -> int:
             result["configs"]["prefill_explicit_mask"] = {"us_two_chunks": round(um, 2), "TFLOPs": round(tm, 2),
                                                           "workspace_bytes": wsm}
             _log(f"prefill with the causal mask as an explicit ggml mask: {um:.1f} us for 2 chunks, {tm:.1f} TFLOP/s")
+            tmd, umd, wsmd = time_prefill(fa, max(10, args.steps // 4), max(3, args.warmup // 4), head_dim=256,
+                                          explicit_mask=True)
+            result["configs"]["prefill_d256_explicit_mask"] = {"us_two_chunks": round(umd, 2), "TFLOPs": round(tmd, 2),
+                                                               "workspace_bytes": wsmd}
+            _log(f"the same at 256-dim heads: {umd:.1f} us for 2 chunks, {tmd:.1f} TFLOP/s")
         except sa.SixiAttnError as e:
             result["prefill_tflops"] = None
             result["prefill_note"] = f"prefill kernel unavailable: {e}"

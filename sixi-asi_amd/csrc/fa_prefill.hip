@@ -716,19 +716,36 @@ __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_q8(FaArgs 
     prefill_body<MODE, D, SIXI_TYPE_Q8_0, true>(a, causal, nrb, n_cu, sh);
 }
 
-// Explicit masks after the pre-pass (fa_mask.hip), as two launches on the stream: GATE 1 runs
-// the lengths-only block-causal body over the offsets the rows imply when every row passed the
-// pre-pass, GATE 2 the staged-mask body when one did not, and each work-group of the other
-// launch returns after reading the pre-pass's table.  (One kernel holding both bodies needs
-// more than the 256 registers per wave of two work-groups per CU.)
+// Explicit masks after the pre-pass (fa_mask.hip).  GATE 1 runs the lengths-only block-causal
+// body over the offsets the rows imply when every row passed the pre-pass, GATE 2 the
+// staged-mask body when one did not; each returns after reading the pre-pass's table when the
+// other one's case holds, and the two run as a pair of launches at 128-dim heads (one kernel
+// holding both bodies needs more than the 256 registers per wave of two work-groups per CU).
+// GATE 0 holds both bodies (the LDS of the larger), one launch: 256-dim heads, which run one
+// work-group per CU either way.
+template <int D>
+union PrefillDualLds {
+    PrefillLds<D, false> fast;
+    PrefillLds<D, true> mask;
+};
+template <int D, int GATE>
+using GatedLds = std::conditional_t<GATE == 0, PrefillDualLds<D>, PrefillLds<D, GATE == 2>>;
 template <int D, int KV, bool QQ8, int GATE>
 __global__ __launch_bounds__(kThreads, PfDim<D>::GROUPS) void prefill_gated(FaArgs a, int nrb, int n_cu) {
-    __shared__ PrefillLds<D, GATE == 2> sh;
-    if (mask_rows_block_causal(a, reinterpret_cast<int*>(&sh)) != (GATE == 1)) return;
-    if constexpr (GATE == 1)
-        prefill_body<MODE_FAST, D, KV, QQ8>(mask_as_lengths(a), 1, nrb, n_cu, sh);
-    else
-        prefill_body<MODE_MASK, D, KV, QQ8>(a, 0, nrb, n_cu, sh);
+    __shared__ GatedLds<D, GATE> sh;
+    const bool lengths = mask_rows_block_causal(a, reinterpret_cast<int*>(&sh));
+    if constexpr (GATE == 0) {
+        if (lengths)
+            prefill_body<MODE_FAST, D, KV, QQ8>(mask_as_lengths(a), 1, nrb, n_cu, sh.fast);
+        else
+            prefill_body<MODE_MASK, D, KV, QQ8>(a, 0, nrb, n_cu, sh.mask);
+    } else {
+        if (lengths != (GATE == 1)) return;
+        if constexpr (GATE == 1)
+            prefill_body<MODE_FAST, D, KV, QQ8>(mask_as_lengths(a), 1, nrb, n_cu, sh);
+        else
+            prefill_body<MODE_MASK, D, KV, QQ8>(a, 0, nrb, n_cu, sh);
+    }
 }
 
 template <int MODE, int D, int KV>
@@ -742,19 +759,25 @@ void launch_prefill_mode(const FaArgs& a, int causal, int nrb, hipStream_t strea
         hipLaunchKernelGGL((prefill_f16<MODE, D>), grid, block, 0, stream, a, causal, nrb, a.P);
 }
 
+template <int D, int KV, bool QQ8>
+void launch_gated(const FaArgs& a, int nrb, hipStream_t stream) {
+    const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
+    if constexpr (PfDim<D>::GROUPS == 1) {
+        hipLaunchKernelGGL((prefill_gated<D, KV, QQ8, 0>), grid, block, 0, stream, a, nrb, a.P);
+    } else {
+        hipLaunchKernelGGL((prefill_gated<D, KV, QQ8, 1>), grid, block, 0, stream, a, nrb, a.P);
+        hipLaunchKernelGGL((prefill_gated<D, KV, QQ8, 2>), grid, block, 0, stream, a, nrb, a.P);
+    }
+}
+
 template <int D, int KV>
 void launch_prefill_gated(const FaArgs& a, int nrb, hipStream_t stream) {
-    const dim3 grid((unsigned)((int64_t)a.S * a.H * nrb)), block(kThreads);
-    if constexpr (KV == SIXI_TYPE_Q8_0) {
-        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_Q8_0, true, 1>), grid, block, 0, stream, a, nrb, a.P);
-        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_Q8_0, true, 2>), grid, block, 0, stream, a, nrb, a.P);
-    } else if (a.q_q8) {
-        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, true, 1>), grid, block, 0, stream, a, nrb, a.P);
-        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, true, 2>), grid, block, 0, stream, a, nrb, a.P);
-    } else {
-        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, false, 1>), grid, block, 0, stream, a, nrb, a.P);
-        hipLaunchKernelGGL((prefill_gated<D, SIXI_TYPE_F16, false, 2>), grid, block, 0, stream, a, nrb, a.P);
-    }
+    if constexpr (KV == SIXI_TYPE_Q8_0)
+        launch_gated<D, SIXI_TYPE_Q8_0, true>(a, nrb, stream);
+    else if (a.q_q8)
+        launch_gated<D, SIXI_TYPE_F16, true>(a, nrb, stream);
+    else
+        launch_gated<D, SIXI_TYPE_F16, false>(a, nrb, stream);
 }
 
 }  // namespace
