@@ -2423,7 +2423,7 @@ int decode_num_groups(const FaArgs& a, int cu_count, int per_cu) {
 
 hipError_t launch_decode(const FaArgs& a, int kv_type, int mask_mode, int head_dim, int row_tiles,
                          hipStream_t stream) {
-    if (a.row_kl) return launch_decode_dual(a, kv_type, head_dim, row_tiles, stream);
+    if (a.row_kl || a.mask_inline) return launch_decode_dual(a, kv_type, head_dim, row_tiles, stream);
     // the 32-cell kernel's MASK mode: a staged explicit mask, no softcap, no ALiBi
     const int mode = (mask_mode == SIXI_MASK_EXPLICIT || a.softcap != 0.0f)
                          ? ((mask_mode == SIXI_MASK_EXPLICIT && a.softcap == 0.0f && a.alibi_nlog2 == 0 && a.mask_stage)

@@ -485,32 +485,64 @@ __device__ __forceinline__ StreamDims stream_dims(const FaArgs& a, int s) {
     return stream_dims_from(a, q_raw, kv_raw);
 }
 
-// Explicit masks: whether the pre-pass found every row of every stream to be a block-causal
-// prefix with one kv offset per stream (each active row's entry >= 0 and equal to its stream's
-// row 0; rows past q_len marked idle).  Called by the whole work-group; the threads from
-// t_first on read the table, eight entries and their row-0 entries per thread and round, all
-// loads issued before any is used (entries past the table read 0, as does their row 0, which
+// Explicit masks: whether every row of every stream is a block-causal prefix with one kv offset
+// per stream.  With the pre-pass's table (a.row_kl): each active row's entry >= 0 and equal to
+// its stream's row 0 (rows past q_len marked idle).  Without it (a.mask_inline: one stream, one
+// row, a short row, which every work-group reads itself): the row is +0 or -0 on all of its
+// scanned cells [0, nc), i.e. it shows exactly the cells the lengths show.  Called by the whole
+// work-group; the threads from t_first on do the reading, eight loads per thread and round, all
+// issued before any is used (table entries past the table read 0, as does their row 0, which
 // passes), so the waves below t_first can do other work meanwhile (the decode kernels' first
-// wave builds the lengths body's cost line).  `wbad` is LDS of one int per wave, free for
-// other use again when this returns (it ends with a barrier, which also publishes what the
-// other waves wrote to LDS before it).  The result is uniform (an SGPR), so the callers branch
-// on it without divergence.
+// wave builds the lengths body's cost line).  `wbad` is LDS of one int per wave, free for other
+// use again when this returns (it ends with a barrier, which also publishes what the other
+// waves wrote to LDS before it).  The result is uniform (an SGPR), so the callers branch on it
+// without divergence.
 __device__ __forceinline__ bool mask_rows_block_causal(const FaArgs& a, int* wbad, int t_first = 0) {
     constexpr int U = 8;
-    const int n = a.S * a.n_q;
     const int nt = (int)blockDim.x - t_first;
-    const buf_rsrc r = make_rsrc(a.row_kl, (uint32_t)n * 4u);
     bool bad = false;
-    for (int i0 = (int)threadIdx.x - t_first; i0 >= 0 && i0 < n; i0 += U * nt) {
-        int v[U], v0[U];
+    if (a.row_kl) {
+        const int n = a.S * a.n_q;
+        const buf_rsrc r = make_rsrc(a.row_kl, (uint32_t)n * 4u);
+        for (int i0 = (int)threadIdx.x - t_first; i0 >= 0 && i0 < n; i0 += U * nt) {
+            int v[U], v0[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = i0 + u * nt;
-            v[u] = (int)buf_ld4(r, 4u * (uint32_t)i);
-            v0[u] = (int)buf_ld4(r, 4u * (uint32_t)(i / a.n_q * a.n_q));
+            for (int u = 0; u < U; ++u) {
+                const int i = i0 + u * nt;
+                v[u] = (int)buf_ld4(r, 4u * (uint32_t)i);
+                v0[u] = (int)buf_ld4(r, 4u * (uint32_t)(i / a.n_q * a.n_q));
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) bad |= !(v[u] == kMaskRowIdle || (v[u] == v0[u] && v[u] >= 0));
         }
+    } else {
+        // stream 0, row 0: 16-byte pieces of eight cells through a resource over the row's bytes
+        // (m_span); a piece that would run past them (the row's last cells) is read cell by cell
+        const StreamDims sd = stream_dims(a, 0);
+        const buf_rsrc r = make_rsrc(a.mask, (uint32_t)a.m_span);
+        const uint16_t* row = reinterpret_cast<const uint16_t*>(a.mask);
+        for (int c0 = 8 * ((int)threadIdx.x - t_first); c0 >= 0 && c0 < a.n_kv; c0 += 8 * U * nt) {
+            u32x4 w[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) bad |= !(v[u] == kMaskRowIdle || (v[u] == v0[u] && v[u] >= 0));
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + 8 * u * nt;
+                w[u] = (c < a.n_kv && 2 * (int64_t)c + 16 <= a.m_span) ? buf_ld16(r, 2u * (uint32_t)c)
+                                                                         : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int c = c0 + 8 * u * nt;
+                if (c < sd.nc && 2 * (int64_t)c + 16 > a.m_span) {
+                    for (int e = 0; e < 8 && c + e < sd.nc; ++e) bad |= (row[c + e] & 0x7fffu) != 0u;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t bits = (e & 1) ? (w[u][e >> 1] >> 16) : (w[u][e >> 1] & 0xffffu);
+                        bad |= c + e < sd.nc && (bits & 0x7fffu) != 0u;
+                    }
+                }
+            }
+        }
     }
     const bool wave_bad = __builtin_amdgcn_ballot_w64(bad) != 0;
     if ((threadIdx.x & 63) == 0) wbad[threadIdx.x >> 6] = wave_bad ? 1 : 0;
@@ -522,11 +554,14 @@ __device__ __forceinline__ bool mask_rows_block_causal(const FaArgs& a, int* wba
     return any == 0;
 }
 // The arguments of the lengths-only body of a mask whose rows passed that test: each stream's
-// cached length is the offset its mask implies (row 0's entry of the table), block-causal.
+// cached length is the offset its mask implies (row 0's entry of the table; without the table
+// the call's own lengths, which the single row matched), block-causal.
 __device__ __forceinline__ FaArgs mask_as_lengths(const FaArgs& a) {
     FaArgs b = a;
-    b.kv_len = a.row_kl;
-    b.kv_len_stride = a.n_q;
+    if (a.row_kl) {
+        b.kv_len = a.row_kl;
+        b.kv_len_stride = a.n_q;
+    }
     b.mask = nullptr;
     return b;
 }

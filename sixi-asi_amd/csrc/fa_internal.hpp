@@ -37,6 +37,8 @@ struct FaArgs {
     // prefix (zeros on cells [0, kl + j + 1), -inf on the rest of the scanned cells),
     // kMaskNotPrefix when it is not, kMaskRowIdle for rows past the stream's q_len
     int32_t* row_kl;
+    int32_t mask_inline;   // explicit mask, no table: one stream of one row whose mask row every
+                           // work-group of the dual kernels reads itself (mask_rows_block_causal)
 
     const char* mask;      // EXPLICIT: f16 at mask + c*2 + j*m_nb1 + (s % m_ne3)*m_nb3
     int64_t m_nb1, m_nb3;
@@ -174,6 +176,9 @@ inline bool mask_prepass_decode(int kv_type, int row_tiles, int head_dim, bool m
 // Rows (streams x rows per stream) of a call that takes the pre-pass: every work-group of the
 // dual kernels reads the table once.
 constexpr int64_t kMaskPrepassMaxRows = 16384;
+// Cells of a single-stream, single-row call's mask row that every work-group of the dual
+// kernels reads itself instead of a pre-pass launch (single-stream decode).
+constexpr int64_t kMaskInlineMaxCells = 16384;
 
 inline int64_t decode_slot_floats(int row_tiles, int head_dim) {
     // O/l rows [16*row_tiles][head_dim] f16 (head_dim/2 floats' worth), then m and l per row

@@ -314,8 +314,12 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
     if (mask_alone && pl.splitk &&
         sixi::mask_prepass_decode(pl.kv_type, sixi::decode_row_tiles(rows, pl.D, pl.kv_type, false), pl.D,
                                   a.mask_stage != 0)) {
-        pl.mask_prepass = true;
         pl.generic = false;
+        // single-stream decode: the kernels read the one mask row themselves (no pre-pass launch)
+        if (S == 1 && n_q == 1 && n_kv <= sixi::kMaskInlineMaxCells)
+            a.mask_inline = 1;
+        else
+            pl.mask_prepass = true;
     }
     if (pl.splitk) {
         pl.row_tiles = sixi::decode_row_tiles(rows, pl.D, pl.kv_type, pl.generic);

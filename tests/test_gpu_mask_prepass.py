@@ -213,3 +213,65 @@ def test_llama_mask_without_q_len(fa):
     fa(dev["q"], dev["k"], dev["v"], ref, kv_len=dev["kv_len"], q_len=None, mask_mode=sa.MASK_BLOCK_CAUSAL)
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+# Single-stream decode (one row): the dual kernels read the mask row themselves (no pre-pass).
+# label, kv_type, D, kv_len, H, Hkv
+DECODE_CASES = [
+    ("f16 decode", sa.TYPE_F16, 128, 4096, 24, 4),
+    ("q8_0 decode", sa.TYPE_Q8_0, 128, 3000, 24, 4),
+    ("f16 256-dim decode", sa.TYPE_F16, 256, 4100, 24, 4),
+    ("q8_0 256-dim decode", sa.TYPE_Q8_0, 256, 2500, 24, 4),
+    ("f16 decode, 48 rows", sa.TYPE_F16, 128, 777, 48, 1),
+]
+
+
+@pytest.mark.parametrize("kind", ["llama", "hole", "hidden_last", "neg_zero"])
+@pytest.mark.parametrize("label,kv_type,D,kv_len,H,Hkv", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+def test_single_stream_decode_mask(fa, label, kv_type, D, kv_len, H, Hkv, kind):
+    w, host, dev = _setup(label, kv_type, D, [kv_len], [1], H, Hkv)
+    cap = dev["k"].shape[1]
+    bits = _mask_host(w, cap, w.kv_len)
+    last = kv_len  # the row's last visible cell
+    if kind == "hole":
+        bits[0, 0, 0, last // 3] = F16_NEG_INF
+    elif kind == "hidden_last":
+        bits[0, 0, 0, last] = F16_NEG_INF
+    elif kind == "neg_zero":
+        bits[0, 0, 0, : last + 1 : 5] = F16_NEG_ZERO
+    _say(f"{label}: {kind}, kv_len {kv_len}")
+    got = _call(fa, w, dev, bits)
+    _oracle_check(w, host, got, bits, f"{label} {kind}")
+    if kind in ("llama", "neg_zero"):
+        ref = _call(fa, w, dev)
+        assert np.array_equal(got[0, :1], ref[0, :1]), label
+    if kind == "hidden_last":
+        # the same as the lengths call one cell shorter
+        ref = _call(fa, w, dev, kv_len=[kv_len - 1])
+        met = oracle.diff_metrics(ref[0, :1].ravel(), got[0, :1].ravel())
+        assert met["max_abs"] <= MAX_ABS, met
+
+
+def test_single_stream_decode_mask_tight_view(fa):
+    """The mask row ends one cell past the call's cells, not on a 16-byte piece: its last cells
+    are read one by one."""
+    w, host, dev = _setup("tight", sa.TYPE_F16, 128, [1000], [1], 24, 4)
+    n_kv = 1005
+    k = dev["k"][:, :n_kv]
+    v = dev["v"][:, :n_kv]
+    bits = _mask_host(w, 1024, w.kv_len)
+    for kind in ("llama", "hidden_last"):
+        b = bits.copy()
+        if kind == "hidden_last":
+            b[0, 0, 0, 1000] = F16_NEG_INF
+        mask = torch.from_numpy(b).cuda().view(torch.float16)[..., :n_kv]
+        out = torch.full((1, 1, 24, 128), float("nan"), device="cuda")
+        fa(dev["q"], k, v, out, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=sa.MASK_EXPLICIT, mask=mask)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        want = oracle.flash_attn_ext(host["q"].astype(np.float32), np.ascontiguousarray(host["k"][:, :n_kv]),
+                                     np.ascontiguousarray(host["v"][:, :n_kv]), w.kv_type,
+                                     np.ascontiguousarray(b[:, :, :1, :n_kv]))
+        met = oracle.diff_metrics(want[0, :1].ravel(), got[0, :1].ravel())
+        _say(f"tight view {kind}: max_abs={met['max_abs']:.3e}")
+        assert met["max_abs"] <= MAX_ABS and met["rel_l2"] <= REL_L2, (kind, met)
