@@ -10,9 +10,10 @@ cache per stream) is reported beside it.  A step is one call of the C ABI
 kernel, timed with HIP events on the stream the library launches on, inputs resident in HBM.
 
 Prints one JSON line: value = algorithmic HBM GB/s of the verify call (K/V of every attended
-cell + Q + O, counted once) at the median per-call time (p10/p90 beside it); roofline = that
-rate against the 8 TB/s HBM peak; verify_explicit_mask = the same call with the mask handed
-over as a ggml KQ mask (the drop-in path); the other
+cell + Q + O, counted once) at the mean time of the steps bracketed by synchronisation (the
+per-call median and p10/p90 beside it); roofline = that rate against the 8 TB/s HBM peak;
+verify_explicit_mask = the same call with the mask handed over as a ggml KQ mask (the drop-in
+path); the other
 configurations (single-stream decode and verify, long q8_0 decode/verify, chunked prefill)
 are reported beside it when their kernels are built; cpu_baseline = the oracle (a
 restatement of ggml's CPU flash_attn_ext, f16 V accumulator as upstream) on the host cores,
@@ -422,7 +423,8 @@ def time_layer(steps: int, warmup: int) -> dict:
     (Q/K RMS norm + RoPE on 64 dims, Q written, K and V stored in the f16 cache) and the output
     gate.  Algorithmic bytes: prologue 2*H*D*4 (Q half read, Q written) + 2*Hkv*D*4 (K, V read)
     + 2*Hkv*D*2 (cache rows written) per row; gate 3*H*D*4 per row (output and gate read,
-    output written)."""
+    output written).  `layer`: the prologue, the attention and the gate as three calls, and as
+    two with the gate fused into the attention's stores (GPU time per layer, graph replays)."""
     import ctypes
 
     import torch
@@ -467,6 +469,22 @@ def time_layer(steps: int, warmup: int) -> dict:
         nbytes = rows * per_row
         res[name] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes,
                      "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    # the layer around the attention: prologue -> attention -> gate (three calls) against
+    # prologue -> attention with the output gate fused into its stores (SIXI_ATTN_FLAG_GATE)
+    fa = sa.FlashAttnExt()
+    prologue, gate = call(lib.sixi_qk_prologue, pp), call(lib.sixi_attn_gate, pg)
+
+    def three():
+        prologue()
+        fa(q_out, kc, vc, out, kv_len=kl, q_len=ql)
+        gate()
+
+    def two():
+        prologue()
+        fa(q_out, kc, vc, out, kv_len=kl, q_len=ql, gate=qg)
+
+    res["layer"] = {"prologue_attention_gate_us": round(_graph_us(three, steps, warmup), 2),
+                    "prologue_attention_with_fused_gate_us": round(_graph_us(two, steps, warmup), 2)}
     return res
 
 

@@ -16,7 +16,8 @@
  *     src/core/core_execution.cpp:2600-2608 and scripts/build_llamacpp.sh:41-45.
  *     The view layout (ne/nb, ggml type ids) and the permuted output [D, H, n_q, S]
  *     are ggml's; the per-stream lengths replace the host-built KQ mask that llama.cpp
- *     derives from the positions set at src/core/core_execution.cpp:2047-2062.
+ *     derives from the positions set at src/core/core_execution.cpp:2047-2062, and such a
+ *     mask handed over as EXPLICIT is recognised on the device and run as those lengths.
  *   - status codes are the negated sixi_asi::ErrorCode values of
  *     include/sixi_asi/common.hpp:40-67 (no abort, no throw).
  *
@@ -34,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SIXI_ATTN_ABI_VERSION 2
+#define SIXI_ATTN_ABI_VERSION 3
 
 /* Cells per page of a paged KV cache (include/sixi_asi/manifest.hpp:124 page_size_tokens). */
 #define SIXI_KV_PAGE_CELLS 256
@@ -83,6 +84,13 @@ enum {
  * the reference (ggml's kernels take no workspace). */
 #define SIXI_ATTN_FLAG_BOUNDED_WORKSPACE 1
 #define SIXI_ATTN_STAGE_CAP_BYTES ((size_t)64 << 20)
+/* GATE (ABI version 3): multiply every written output element by sigmoid(gate), the output
+ * gate of Qwen3.8's full-attention layers (o = attention * sigmoid(gate); the layer graph in
+ * include/sixi_layer.h), with the gate read from `gate_qg` (the prologue's qg tensor: elements
+ * D .. 2D-1 of each head's row).  The result equals sixi_attn_forward followed by
+ * sixi_attn_gate bit for bit, without that second pass over the output.  No counterpart in
+ * ggml_flash_attn_ext (upstream runs the gate as a separate graph node). */
+#define SIXI_ATTN_FLAG_GATE 2
 
 /* ggml-compatible strided view.  ne[0] is the innermost extent (elements); nb[] are byte
  * strides; for q8_0, nb[0] = 34 (one 32-element block) and a row of ne[0] elements takes
@@ -125,6 +133,10 @@ typedef struct sixi_attn_params {
      * [0, n_pages) on the device.  Streams may share pages (sixi_kv_pool_seq_cp). */
     const int32_t* page_table;
     int64_t page_table_stride;
+    /* SIXI_ATTN_FLAG_GATE only (ABI version 3; not read otherwise): f32 [2D, H, >= n_q, S],
+     * per head D query values then D gate values (sixi_qk_prologue_params.qg); nb[0] = 4,
+     * 16-byte aligned rows; must not overlap `out` */
+    sixi_view gate_qg;
 } sixi_attn_params;
 
 /* Launches the attention for every stream, head and row.  Rows j >= q_len[s] are not

@@ -409,7 +409,8 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT, T16Dim<D>::DT
 }
 
 // Writes the normalised rows of row tiles n0 .. n0+NT-1 held by this lane: dims
-// (D/4)c + DT*i + tt of row 16n + r at o[tt][n][i].
+// (D/4)c + DT*i + tt of row 16n + r at o[tt][n][i].  (With the fused output gate the merge
+// kernel gates these rows afterwards.)
 template <int NT, int DT>
 __device__ __forceinline__ void write_rows(const FaArgs& a, const Acc<NT, DT>& acc, int n0, int s, int g,
                                            int R, int lane) {
@@ -1241,7 +1242,8 @@ __device__ __forceinline__ bool pipe_iteration(Acc<NT, 8>& acc, PipeState<NT>& p
     return need;
 }
 
-// Normalised rows (O layout of the 32-cell kernel).
+// Normalised rows (O layout of the 32-cell kernel).  (With the fused output gate the merge
+// kernel gates these rows afterwards.)
 template <int NT, int DT>
 __device__ __forceinline__ void write_rows_wide(const FaArgs& a, const Acc<NT, DT>& acc, int n0, int s, int g, int R,
                                                 int lane) {
@@ -2108,10 +2110,18 @@ __global__ __launch_bounds__(256) void decode_merge_pieces(FaArgs a, int rows_sl
     const int p_first = a.seg_pieces[2 * k], p_last = a.seg_pieces[2 * k + 1];
     const int row = blockIdx.y;
     if (row >= a.Gr * sd.ql) return;  // (a segment without rows has stale entries)
-    if (p_first == p_last) return;    // written whole by its only work-group
 
     const int pg = (int)(threadIdx.x / TPR), c = (int)(threadIdx.x % TPR);
     const int d0 = c * 4;
+    const int j = row / a.Gr;
+    const int h = g * a.G + a.hoff + row % a.Gr;
+    char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4;
+    const f32x4 gv = gate_load(a, s, j, h, d0);  // (fused gate: loaded beside the partials)
+    if (p_first == p_last) {
+        // written whole by its only work-group; with the fused gate, gated here
+        if (a.gate && pg == 0) st16(dst, gated(a, *reinterpret_cast<const f32x4*>(dst), gv));
+        return;
+    }
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
@@ -2147,9 +2157,7 @@ __global__ __launch_bounds__(256) void decode_merge_pieces(FaArgs a, int rows_sl
         merge_row<1>(M, L, &o, lm[q], ll[q], &oq);  // a group without pieces adds l = 0, o = 0
     }
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;
-    const int j = row / a.Gr;
-    const int h = g * a.G + a.hoff + row % a.Gr;
-    st16(a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4, o * inv);
+    st16(dst, gated(a, o * inv, gv));
 }
 
 // Combines the pieces of every segment that more than one work-group touched, for segments of
@@ -2168,9 +2176,23 @@ __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot
     const int p_first = a.seg_pieces[2 * k], p_last = a.seg_pieces[2 * k + 1];
     const int row = blockIdx.y * (256 / TPR) + (int)(threadIdx.x / TPR);
     if (row >= a.Gr * sd.ql) return;  // (a segment without rows has stale entries)
-    if (p_first == p_last) return;    // written whole by its only work-group
 
     const int d0 = (int)(threadIdx.x % TPR) * DPT;
+    const int j = row / a.Gr;
+    const int h = g * a.G + a.hoff + row % a.Gr;
+    char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4;
+    // (fused gate: its values load beside the partials)
+    const f32x4 gv0 = gate_load(a, s, j, h, d0);
+    const f32x4 gv1 = gate_load(a, s, j, h, d0 + 4);
+    if (p_first == p_last) {
+        // written whole by its only work-group; with the fused gate, gated here
+        if (a.gate) {
+            const f32x4 w0 = *reinterpret_cast<const f32x4*>(dst), w1 = *reinterpret_cast<const f32x4*>(dst + 16);
+            st16(dst, gated(a, w0, gv0));
+            st16(dst + 16, gated(a, w1, gv1));
+        }
+        return;
+    }
     const float* base = a.part + k * a.slot_floats;
     float M = neg_inf(), L = 0.0f;
     f32x4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -2206,11 +2228,8 @@ __global__ __launch_bounds__(256) void decode_merge_rows(FaArgs a, int rows_slot
         for (int p0 = p_first; p0 <= p_last; p0 += 8) merge_step(std::integral_constant<int, 8>{}, p0);
     }
     const float inv = L == 0.0f ? 0.0f : 1.0f / L;
-    const int j = row / a.Gr;
-    const int h = g * a.G + a.hoff + row % a.Gr;
-    char* dst = a.out + (int64_t)j * a.o_nb2 + (int64_t)h * a.o_nb1 + (int64_t)s * a.o_nb3 + d0 * 4;
-    st16(dst, o[0] * inv);
-    st16(dst + 16, o[1] * inv);
+    st16(dst, gated(a, o[0] * inv, gv0));
+    st16(dst + 16, gated(a, o[1] * inv, gv1));
 }
 
 // The merge form for a split launch: the piece-parallel one once segments average more than

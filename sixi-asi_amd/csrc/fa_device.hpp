@@ -431,6 +431,24 @@ __device__ __forceinline__ u32x4 ld16(const char* p) {
 }
 __device__ __forceinline__ void st16(char* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
+// The fused output gate of a call with SIXI_ATTN_FLAG_GATE: the four gate values of dims
+// d .. d+3 of head h, row j, stream s (zeros without the gate; load them early, use them with
+// gated()).
+__device__ __forceinline__ f32x4 gate_load(const FaArgs& a, int s, int j, int h, int d) {
+    if (!a.gate) return f32x4{0.f, 0.f, 0.f, 0.f};
+    return *reinterpret_cast<const f32x4*>(a.gate + (int64_t)s * a.g_nb3 + (int64_t)j * a.g_nb2 +
+                                           (int64_t)h * a.g_nb1 + (int64_t)d * 4);
+}
+// o * sigmoid(g) per element, in the arithmetic of the separate gate (sixi_attn_gate,
+// layer_prologue.hip), so a gated call equals the attention followed by the gate bit for bit;
+// o unchanged without the gate.
+__device__ __forceinline__ f32x4 gated(const FaArgs& a, f32x4 o, f32x4 g) {
+    if (!a.gate) return o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = o[i] * (1.0f / (1.0f + expf(-g[i])));
+    return o;
+}
+
 // Reductions over the four lanes l, l^16, l^32, l^48 (the lane groups of one MFMA column)
 // with the gfx950 row-swap permutes (VALU only, no LDS round trip).  Each swap returns both
 // halves, so max/sum of the pair is the reduction over {l, l^32} (resp. {l, l^16}).

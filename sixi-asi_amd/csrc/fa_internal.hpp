@@ -71,6 +71,9 @@ struct FaArgs {
     int32_t* seg_pieces;   // per segment: logical work-groups of its first and last piece
     int32_t q_q8;          // prefill over an f16-staged q8_0 cache: convert Q to the q8_0 dot type
                            // in the kernel (ggml's rule), as the q8_0 kernels do
+
+    const char* gate;      // fused output gate (SIXI_ATTN_FLAG_GATE), or null: element (d, h, j, s)
+    int64_t g_nb1, g_nb2, g_nb3;  // at gate + d*4 + h*g_nb1 + j*g_nb2 + s*g_nb3 (qg's gate half)
 };
 
 // q8_0 KV at 256-dim heads beyond the q8_0 kernel (fa_q8_stage.hip): K, V and Q staged as dense f16 rows in

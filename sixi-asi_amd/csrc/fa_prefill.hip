@@ -692,7 +692,8 @@ __device__ __forceinline__ void prefill_body(const FaArgs& a, int causal, int nr
 #pragma unroll
             for (int bq = 0; bq < 4; ++bq)
                 st16(dst + (32 * db + 8 * bq + 4 * hw) * 4,
-                     f32x4{acc[db][4 * bq], acc[db][4 * bq + 1], acc[db][4 * bq + 2], acc[db][4 * bq + 3]} * inv);
+                     gated(a, f32x4{acc[db][4 * bq], acc[db][4 * bq + 1], acc[db][4 * bq + 2], acc[db][4 * bq + 3]} * inv,
+                           gate_load(a, s, jw, h, 32 * db + 8 * bq + 4 * hw)));
     }
 }
 

@@ -55,6 +55,8 @@ bool workspace_overlaps(const sixi_attn_params* p, const void* ws, size_t bytes)
         return true;
     if (p->mask_mode == SIXI_MASK_EXPLICIT && ranges_overlap(ws, n, p->mask.data, view_span(p->mask, p->mask.ne[0] * 2)))
         return true;
+    if ((p->flags & SIXI_ATTN_FLAG_GATE) && ranges_overlap(ws, n, p->gate_qg.data, view_span(p->gate_qg, 2 * D * 4)))
+        return true;
     for (const DevRange& x : device_arrays(p, p->q.ne[3]))
         if (ranges_overlap(ws, n, x.p, x.bytes)) return true;
     return false;
@@ -111,7 +113,7 @@ void splitk_layout(Plan& pl, int64_t slots) {
 // avoided: 256-dim rows that are not 16-byte aligned).
 int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_STAGE_CAP_BYTES) {
     if (!p || !out) return SIXI_E_INVALID_ARGUMENT;
-    if ((p->flags & ~SIXI_ATTN_FLAG_BOUNDED_WORKSPACE) != 0) return SIXI_E_INVALID_ARGUMENT;
+    if ((p->flags & ~(SIXI_ATTN_FLAG_BOUNDED_WORKSPACE | SIXI_ATTN_FLAG_GATE)) != 0) return SIXI_E_INVALID_ARGUMENT;
     if (p->flags & SIXI_ATTN_FLAG_BOUNDED_WORKSPACE) stage_cap = 0;
     const sixi_view &q = p->q, &k = p->k, &v = p->v, &o = p->out;
     if (!q.data || !k.data || !v.data || !o.data) return SIXI_E_INVALID_ARGUMENT;
@@ -196,6 +198,21 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
         if (views_overlap(o, D * 4, m, m.ne[0] * 2)) return SIXI_E_INVALID_ARGUMENT;
     }
 
+    // the fused output gate: qg [2D, H, >= n_q, S] f32, read while `out` is written
+    const sixi_view& gq = p->gate_qg;
+    const bool gate = (p->flags & SIXI_ATTN_FLAG_GATE) != 0;
+    if (gate) {
+        if (!gq.data || gq.type != SIXI_TYPE_F32 || gq.nb[0] != 4) return SIXI_E_INVALID_ARGUMENT;
+        if (gq.ne[0] != 2 * D || gq.ne[1] != H || gq.ne[2] < n_q || gq.ne[3] != S) return SIXI_E_INVALID_ARGUMENT;
+        for (int d = 1; d < 4; ++d) {
+            if (gq.nb[d] <= 0) return SIXI_E_INVALID_ARGUMENT;
+            if (gq.nb[d] % 16) return SIXI_E_ALIGNMENT;
+        }
+        if (!aligned(gq.data, 16)) return SIXI_E_ALIGNMENT;
+        if (view_span(gq, 2 * D * 4) < 0) return SIXI_E_INTEGER_OVERFLOW;
+        if (views_overlap(o, D * 4, gq, 2 * D * 4)) return SIXI_E_INVALID_ARGUMENT;
+    }
+
     // scalars (ggml: ALiBi slopes multiply the mask, so they need one)
     if (!std::isfinite(p->scale) || !std::isfinite(p->max_bias) || !std::isfinite(p->logit_softcap))
         return SIXI_E_INVALID_ARGUMENT;
@@ -240,6 +257,10 @@ int resolve(const sixi_attn_params* p, Plan* out, size_t stage_cap = SIXI_ATTN_S
         a.m_span = (n_q - 1) * m.nb[1] + m.ne[0] * 2;
     } else {
         a.m_ne3 = 1;
+    }
+    if (gate) {
+        a.gate = static_cast<const char*>(gq.data) + D * 4;  // the gate half of each head's row
+        a.g_nb1 = gq.nb[1]; a.g_nb2 = gq.nb[2]; a.g_nb3 = gq.nb[3];
     }
     a.S = (int32_t)S; a.H = (int32_t)H; a.Hkv = (int32_t)Hkv; a.G = (int32_t)(H / Hkv);
     a.Gr = a.G; a.hoff = 0;
@@ -408,6 +429,7 @@ int run(Plan& pl, char* ws, hipStream_t stream) {
     a.part = reinterpret_cast<float*>(ws);
     a.seg_pieces = pl.splitk ? reinterpret_cast<int32_t*>(ws + pl.seg_offset) : nullptr;
     a.P = launch_groups(pl);
+
     if (pl.splitk) {
         a.xcd_remap = 0;
         a.head_split = 0;

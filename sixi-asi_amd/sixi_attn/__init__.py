@@ -29,6 +29,7 @@ TYPE_F32, TYPE_F16, TYPE_Q8_0 = 0, 1, 8
 MASK_NONE, MASK_BLOCK_CAUSAL, MASK_EXPLICIT = 0, 1, 2
 # sixi_attn_params.flags; the f16 staging of a q8_0 cache stays under STAGE_CAP_BYTES
 FLAG_BOUNDED_WORKSPACE = 1
+FLAG_GATE = 2
 STAGE_CAP_BYTES = 64 << 20
 # status codes (negated sixi_asi::ErrorCode, include/sixi_asi/common.hpp:40-67)
 OK = 0
@@ -107,6 +108,7 @@ class SixiAttnParams(ctypes.Structure):
         ("stream", ctypes.c_void_p),
         ("page_table", ctypes.c_void_p),
         ("page_table_stride", ctypes.c_int64),
+        ("gate_qg", SixiView),
     ]
 
 
@@ -326,11 +328,12 @@ class FlashAttnExt:
 
     def params(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
                scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None,
-               page_table=None, bounded_workspace=False) -> SixiAttnParams:
+               page_table=None, bounded_workspace=False, gate=None) -> SixiAttnParams:
         """``page_table`` (an int32 device tensor [S, pages per stream]): k and v are page pools
         ``[n_pages, 256, Hkv, D]`` (uint8 q8_0 blocks as for a cache) read through it.
         ``bounded_workspace`` sets SIXI_ATTN_FLAG_BOUNDED_WORKSPACE (no f16 staging of a q8_0
-        cache: the workspace does not grow with the cache)."""
+        cache: the workspace does not grow with the cache).  ``gate`` (the layer prologue's qg,
+        f32 [S, rows, H, 2D]) sets SIXI_ATTN_FLAG_GATE: out = attention * sigmoid(qg[..., D:])."""
         import torch
 
         D = q.shape[-1]
@@ -344,6 +347,9 @@ class FlashAttnExt:
         p.q_len = q_len.data_ptr() if q_len is not None else None
         p.mask_mode = mask_mode
         p.flags = FLAG_BOUNDED_WORKSPACE if bounded_workspace else 0
+        if gate is not None:
+            p.flags |= FLAG_GATE
+            p.gate_qg = view_of(gate, tokens_heads=False)
         if mask is not None:
             # mask tensor [S or 1, 1, n_q_pad, n_kv] f16
             p.mask = view_of(mask, TYPE_F16, tokens_heads=False)
@@ -374,14 +380,15 @@ class FlashAttnExt:
 
     def __call__(self, q, k, v, out, kv_len=None, q_len=None, mask_mode=MASK_BLOCK_CAUSAL, mask=None,
                  scale=None, max_bias=0.0, logit_softcap=0.0, kv_type=None, stream=None, check=True,
-                 workspace=None, noalloc=False, page_table=None, bounded_workspace=False) -> int:
+                 workspace=None, noalloc=False, page_table=None, bounded_workspace=False, gate=None) -> int:
         """One call.  ``noalloc=True`` runs sixi_attn_forward_noalloc (the library's fixed
         device scratch, no workspace); ``page_table`` reads k and v as page pools;
-        ``bounded_workspace`` never stages a q8_0 cache as f16."""
+        ``bounded_workspace`` never stages a q8_0 cache as f16; ``gate`` fuses the layer's
+        output gate (see :meth:`params`)."""
         import torch
 
         p = self.params(q, k, v, out, kv_len, q_len, mask_mode, mask, scale, max_bias, logit_softcap,
-                        kv_type, stream, page_table, bounded_workspace)
+                        kv_type, stream, page_table, bounded_workspace, gate)
         if p.stream is None:
             p.stream = torch.cuda.current_stream(self.device).cuda_stream
         if noalloc:

@@ -25,7 +25,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert declared == sorted(sa.EXPORTED_SYMBOLS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.sixi_attn_abi_version() == 2
+    assert lib.sixi_attn_abi_version() == 3
 
 
 def test_status_strings():
@@ -455,3 +455,58 @@ def test_gdn_verify_input_state_rows_must_not_overlap():
     p.state_out = sa.make_view(FAKE + (1 << 44), sa.TYPE_F32, list(p.state_in.ne), list(p.state_in.nb))
     p.state_in.nb[1] = 256                       # input rows of 512 bytes 256 apart
     assert sa.load_library().sixi_gdn_verify(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT
+
+
+GATE = FAKE + (8 << 36)  # the fused gate's qg view, in an address range of its own
+
+
+def _gated(S=2, n_q=16, H=24, D=128):
+    p = _params(S=S, n_q=n_q, H=H, D=D)
+    p.flags = sa.FLAG_GATE
+    p.gate_qg = sa.make_view(GATE, sa.TYPE_F32, [2 * D, H, n_q, S], [4, 2 * D * 4, H * 2 * D * 4, n_q * H * 2 * D * 4])
+    return p
+
+
+def test_gated_descriptions_pass():
+    for D in (128, 256):
+        for n_q in (1, 16, 300):
+            assert _validate(_gated(n_q=n_q, D=D)) == sa.OK, (D, n_q)
+    p = _gated()
+    p.gate_qg.ne[2] = 20  # more rows than the call's (a padded block)
+    assert _validate(p) == sa.OK
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda p: setattr(p.gate_qg, "data", None), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.gate_qg, "type", sa.TYPE_F16), sa.E_INVALID_ARGUMENT),
+    (lambda p: p.gate_qg.ne.__setitem__(0, 128), sa.E_INVALID_ARGUMENT),   # not 2D per head
+    (lambda p: p.gate_qg.ne.__setitem__(1, 12), sa.E_INVALID_ARGUMENT),    # not H heads
+    (lambda p: p.gate_qg.ne.__setitem__(2, 15), sa.E_INVALID_ARGUMENT),    # fewer rows than n_q
+    (lambda p: p.gate_qg.ne.__setitem__(3, 1), sa.E_INVALID_ARGUMENT),     # not S streams
+    (lambda p: p.gate_qg.nb.__setitem__(0, 8), sa.E_INVALID_ARGUMENT),
+    (lambda p: setattr(p.gate_qg, "data", GATE + 8), sa.E_ALIGNMENT),
+    (lambda p: p.gate_qg.nb.__setitem__(2, 24 * 256 * 4 + 4), sa.E_ALIGNMENT),
+    (lambda p: setattr(p.gate_qg, "data", ADDR["out"] + 4096), sa.E_INVALID_ARGUMENT),  # the output over the gate
+    (lambda p: setattr(p, "flags", sa.FLAG_GATE | 4), sa.E_INVALID_ARGUMENT),           # an unknown flag
+])
+def test_gated_descriptions_are_checked(mutate, code):
+    p = _gated()
+    mutate(p)
+    assert _validate(p) == code
+
+
+def test_gate_is_not_read_without_its_flag():
+    p = _gated()
+    p.flags = 0
+    p.gate_qg = sa.make_view(0, sa.TYPE_F16, [1, 1, 1, 1], [0, 0, 0, 0])  # garbage, ignored
+    assert _validate(p) == sa.OK
+
+
+def test_workspace_must_not_overlap_the_gate():
+    lib = sa.load_library()
+    p = _gated()
+    n = ctypes.c_size_t(0)
+    assert lib.sixi_attn_workspace_bytes(ctypes.byref(p), ctypes.byref(n)) == sa.OK
+    p.workspace = GATE - 256
+    p.workspace_bytes = n.value + 512
+    assert lib.sixi_attn_forward(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT
