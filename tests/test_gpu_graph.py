@@ -101,6 +101,59 @@ def test_layer_graph():
         _replays(layer, [q, out])
 
 
+def test_masked_calls_graph():
+    """llama-mask calls (the ggml hook): the mask pre-pass and the dual kernels of a verify batch,
+    the prefill pair, and single-stream decode (no pre-pass) replay the eager result."""
+    fa = sa.FlashAttnExt()
+    for name, kv_len, q_len in (("verify", [900, 5000, 37, 2000], [16, 16, 9, 16]),
+                                ("prefill", [200, 700], [150, 260]),
+                                ("decode", [4096], [1])):
+        w = wl.Workload(f"graph mask {name}", 0x51A7_B000 + len(name), len(kv_len), kv_len, q_len)
+        dev = wl.to_device(wl.make_host(w))
+        mask = torch.from_numpy(wl.kq_mask(dev["k"].shape[1], w.n_q, w.kv_len, w.q_len)).view(torch.float16).cuda()
+        out = torch.empty((w.S, w.n_q, w.H, w.D), device="cuda")
+        _say(f"graph: {name} with the llama mask S={w.S} rows={w.n_q}")
+
+        def call():
+            fa(dev["q"], dev["k"], dev["v"], out, kv_len=dev["kv_len"], q_len=dev["q_len"],
+               mask_mode=sa.MASK_EXPLICIT, mask=mask)
+
+        _replays(call, [out])
+
+
+def test_layer_graph_fused_gate():
+    """Prologue -> attention with the output gate fused (SIXI_ATTN_FLAG_GATE) replays the eager
+    result, which equals the three-call layer bit for bit."""
+    S, R, H, Hkv, D, n_cells = 4, 16, 24, 4, 256, 1040
+    kv_len = torch.tensor([1000, 3, 517, 64], dtype=torch.int32, device="cuda")
+    q_len = torch.tensor([16, 16, 5, 1], dtype=torch.int32, device="cuda")
+    qg = torch.randn((S, R, H, 2 * D), device="cuda")
+    k = torch.randn((S, R, Hkv, D), device="cuda")
+    v = torch.randn_like(k)
+    wq = torch.rand(D, device="cuda") + 0.5
+    wk = torch.rand(D, device="cuda") + 0.5
+    q = torch.zeros((S, R, H, D), device="cuda")
+    kc = (torch.randn((S, n_cells, Hkv, D), device="cuda") * 0.5).half()
+    vc = kc.clone()
+    out = torch.empty((S, R, H, D), device="cuda")
+    fa = sa.FlashAttnExt()
+    _say("graph: layer prologue/attention with the fused gate")
+
+    def layer():
+        sa.qk_prologue(qg, k, v, wq, wk, q, kc, vc, kv_len, q_len)
+        fa(q, kc, vc, out, kv_len=kv_len, q_len=q_len, gate=qg)
+
+    fa(q, kc, vc, out, kv_len=kv_len, q_len=q_len, gate=qg)   # size the workspace before capture
+    _replays(layer, [q, out])
+    fused = out.clone()
+    out.zero_()
+    sa.qk_prologue(qg, k, v, wq, wk, q, kc, vc, kv_len, q_len)
+    fa(q, kc, vc, out, kv_len=kv_len, q_len=q_len)
+    sa.attn_gate(out, qg, q_len)
+    torch.cuda.synchronize()
+    assert torch.equal(out, fused)
+
+
 def test_gdn_graph():
     """GDN verify out of place (the input state stays fixed, so every replay has the same input)."""
     S, n, G, K, HD = 8, 16, 48, 128, 128

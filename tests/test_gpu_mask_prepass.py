@@ -275,3 +275,22 @@ def test_single_stream_decode_mask_tight_view(fa):
         met = oracle.diff_metrics(want[0, :1].ravel(), got[0, :1].ravel())
         _say(f"tight view {kind}: max_abs={met['max_abs']:.3e}")
         assert met["max_abs"] <= MAX_ABS and met["rel_l2"] <= REL_L2, (kind, met)
+
+
+def test_noalloc_with_the_pre_pass_table(fa):
+    """The no-allocation entry point holds the pre-pass's table in its scratch: the same output as
+    sixi_attn_forward, for a verify batch and a prefill block, twice in a row (the second smaller)."""
+    for name, kv_len, q_len in (("verify", [900, 5000, 37, 2000], [16, 16, 9, 16]), ("verify small", [300, 40], [4, 2]),
+                                ("prefill", [200, 700], [150, 260]), ("prefill small", [90], [120])):
+        w, host, dev = _setup(f"noalloc {name}", sa.TYPE_F16, 128, kv_len, q_len, 24, 4)
+        bits = _mask_host(w, dev["k"].shape[1], w.kv_len)
+        mask = torch.from_numpy(bits).cuda().view(torch.float16)
+        a = torch.full((w.S, w.n_q, w.H, w.D), float("nan"), device="cuda")
+        b = torch.full_like(a, float("nan"))
+        fa(dev["q"], dev["k"], dev["v"], a, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=sa.MASK_EXPLICIT,
+           mask=mask)
+        fa(dev["q"], dev["k"], dev["v"], b, kv_len=dev["kv_len"], q_len=dev["q_len"], mask_mode=sa.MASK_EXPLICIT,
+           mask=mask, noalloc=True)
+        torch.cuda.synchronize()
+        _say(f"noalloc {name}")
+        assert torch.equal(torch.nan_to_num(a, nan=7.0), torch.nan_to_num(b, nan=7.0)), name
