@@ -424,7 +424,8 @@ def time_layer(steps: int, warmup: int) -> dict:
     gate.  Algorithmic bytes: prologue 2*H*D*4 (Q half read, Q written) + 2*Hkv*D*4 (K, V read)
     + 2*Hkv*D*2 (cache rows written) per row; gate 3*H*D*4 per row (output and gate read,
     output written).  `layer`: the prologue, the attention and the gate as three calls, and as
-    two with the gate fused into the attention's stores (GPU time per layer, graph replays)."""
+    two with the gate fused into the attention's stores, also with the prologue's Q in f16 (GPU
+    time per layer, graph replays)."""
     import ctypes
 
     import torch
@@ -483,8 +484,17 @@ def time_layer(steps: int, warmup: int) -> dict:
         prologue()
         fa(q_out, kc, vc, out, kv_len=kl, q_len=ql, gate=qg)
 
+    q16 = torch.empty((S, R, H, D), dtype=torch.float16, device="cuda")
+    pp16 = sa.qk_prologue_params(qg, k, v, wq, wk, q16, kc, vc, kl, ql)
+    prologue16 = call(lib.sixi_qk_prologue, pp16)
+
+    def two16():
+        prologue16()
+        fa(q16, kc, vc, out, kv_len=kl, q_len=ql, gate=qg)
+
     res["layer"] = {"prologue_attention_gate_us": round(_graph_us(three, steps, warmup), 2),
-                    "prologue_attention_with_fused_gate_us": round(_graph_us(two, steps, warmup), 2)}
+                    "prologue_attention_with_fused_gate_us": round(_graph_us(two, steps, warmup), 2),
+                    "prologue_f16_q_attention_with_fused_gate_us": round(_graph_us(two16, steps, warmup), 2)}
     return res
 
 

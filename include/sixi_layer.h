@@ -38,7 +38,11 @@ typedef struct sixi_qk_prologue_params {
     int32_t flags;          /* reserved, must be 0                                                */
     const int32_t* kv_len;  /* device [S]: cells cached before the block = position of row 0       */
     const int32_t* q_len;   /* device [S]: rows of stream s (<= n_rows), or NULL (= n_rows)        */
-    sixi_view q_out;        /* [D, n_rows, H, S] f32: the attention's Q (sixi_attn_params.q)       */
+    sixi_view q_out;        /* [D, n_rows, H, S] f32, or f16 (rounded to nearest even) with an f16
+                               cache: the attention's Q (sixi_attn_params.q); f16 halves its bytes
+                               and leaves the attention's result the same bit for bit (it rounds Q
+                               to f16 itself); a q8_0 cache needs f32 (ggml converts Q to the q8_0
+                               dot type from its f32 values)                                      */
     sixi_view k_cache;      /* [D, n_cells, Hkv, S] f16 or q8_0; paged: the page pool
                                [D, SIXI_KV_PAGE_CELLS, Hkv, n_pages], nb[3] = page stride           */
     sixi_view v_cache;      /* same shape and type as k_cache                                     */

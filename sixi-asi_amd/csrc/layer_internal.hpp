@@ -25,6 +25,7 @@ struct QkPrologueArgs {
     const int32_t* q_len;            // may be null: every row
     char* q_out;
     int64_t qo_nb1, qo_nb2, qo_nb3;  // row, head, stream
+    int q_out_f16;                   // q_out rows in f16 (RNE) rather than f32
     char* kc;
     int64_t kc_nb1, kc_nb2, kc_nb3;  // cell, head, stream
     char* vc;

@@ -229,7 +229,10 @@ __global__ __launch_bounds__(256) void qk_prologue(QkPrologueArgs a) {
             const int slot = first + 4 * b;
             if (slot >= slots) break;
             if (slot < a.H) {
-                store_row<E>(qo_row + (int64_t)slot * a.qo_nb2, lane, x[b]);
+                if (a.q_out_f16)
+                    store_f16<E>(qo_row + (int64_t)slot * a.qo_nb2, lane, x[b]);
+                else
+                    store_row<E>(qo_row + (int64_t)slot * a.qo_nb2, lane, x[b]);
                 continue;
             }
             if (!in_cache) continue;

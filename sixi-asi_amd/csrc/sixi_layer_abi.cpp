@@ -38,7 +38,11 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     const sixi_view &qg = p->qg, &k = p->k, &v = p->v, &qo = p->q_out, &kc = p->k_cache, &vc = p->v_cache;
     for (const sixi_view* x : {&qg, &k, &v, &qo, &kc, &vc})
         if (!nonneg(*x)) return SIXI_E_INVALID_ARGUMENT;
-    if (!f32_rows_ok(qg) || !f32_rows_ok(k) || !f32_rows_ok(v) || !f32_rows_ok(qo)) return SIXI_E_INVALID_ARGUMENT;
+    // q_out: f32, or f16 over an f16 cache (half the bytes written here and read by the attention,
+    // which rounds Q to f16 for an f16 cache anyway)
+    const bool qo_f16 = qo.type == SIXI_TYPE_F16 && qo.nb[0] == 2 && qo.data != nullptr;
+    if (!f32_rows_ok(qg) || !f32_rows_ok(k) || !f32_rows_ok(v) || (!f32_rows_ok(qo) && !qo_f16))
+        return SIXI_E_INVALID_ARGUMENT;
     const int64_t D = qo.ne[0];
     if (D != 128 && D != 256) return SIXI_E_UNSUPPORTED;
     const int64_t H = qg.ne[1], n_rows = qg.ne[2], S = qg.ne[3], Hkv = k.ne[1];
@@ -53,6 +57,9 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     if (qg.ne[0] != 2 * D || !dims_are(qo, D, n_rows, H, S)) return SIXI_E_INVALID_ARGUMENT;
     if (!dims_are(k, D, Hkv, n_rows, S) || !dims_are(v, D, Hkv, n_rows, S)) return SIXI_E_INVALID_ARGUMENT;
     if (kc.type != vc.type || (kc.type != SIXI_TYPE_F16 && kc.type != SIXI_TYPE_Q8_0)) return SIXI_E_INVALID_ARGUMENT;
+    // an f16 Q only for an f16 cache: over q8_0 the attention converts Q to the q8_0 dot type from
+    // its f32 values (ggml's rule), which an f16 Q would change
+    if (qo_f16 && kc.type != SIXI_TYPE_F16) return SIXI_E_INVALID_ARGUMENT;
     if (!kc.data || !vc.data) return SIXI_E_INVALID_ARGUMENT;
     if (!dims_are(kc, D, c_ne1, Hkv, c_ne3) || !dims_are(vc, D, c_ne1, Hkv, c_ne3)) return SIXI_E_INVALID_ARGUMENT;
     const int64_t cnb0 = kc.type == SIXI_TYPE_F16 ? 2 : 34;
@@ -65,10 +72,11 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     if (!mul_ok(S, n_rows, &rows) || rows >= (int64_t)UINT32_MAX) return SIXI_E_INTEGER_OVERFLOW;
     const int64_t crb = row_bytes(kc.type, D);
     if (view_span(qg, 2 * D * 4) < 0 || view_span(k, D * 4) < 0 || view_span(v, D * 4) < 0 ||
-        view_span(qo, D * 4) < 0 || view_span(kc, crb) < 0 || view_span(vc, crb) < 0)
+        view_span(qo, D * (qo_f16 ? 2 : 4)) < 0 || view_span(kc, crb) < 0 || view_span(vc, crb) < 0)
         return SIXI_E_INTEGER_OVERFLOW;
     // written rows must not alias one another
-    if (!rows_disjoint(qo, D * 4) || !rows_disjoint(kc, crb) || !rows_disjoint(vc, crb)) return SIXI_E_INVALID_ARGUMENT;
+    if (!rows_disjoint(qo, D * (qo_f16 ? 2 : 4)) || !rows_disjoint(kc, crb) || !rows_disjoint(vc, crb))
+        return SIXI_E_INVALID_ARGUMENT;
     if (!rows16(qg) || !rows16(k) || !rows16(v) || !rows16(qo)) return SIXI_E_ALIGNMENT;
     if (!aligned(p->q_norm, 16) || !aligned(p->k_norm, 16)) return SIXI_E_ALIGNMENT;
     if (kc.type == SIXI_TYPE_F16 ? (!rows16(kc) || !rows16(vc))
@@ -101,6 +109,7 @@ int resolve_prologue(const sixi_qk_prologue_params* p, sixi::QkPrologueArgs* out
     a.qo_nb1 = qo.nb[1];
     a.qo_nb2 = qo.nb[2];
     a.qo_nb3 = qo.nb[3];
+    a.q_out_f16 = qo_f16 ? 1 : 0;
     a.kc = static_cast<char*>(const_cast<void*>(kc.data));
     a.kc_nb1 = kc.nb[1];
     a.kc_nb2 = kc.nb[2];

@@ -607,7 +607,7 @@ def qk_prologue_params(qg, k, v, q_norm, k_norm, q_out, k_cache, v_cache, kv_len
                        stream=None, page_table=None) -> SixiQkPrologueParams:
     """Parameters of ``sixi_qk_prologue`` for torch tensors: ``qg[S, n_rows, H, 2D]`` (per head
     the query, then its gate), ``k/v[S, n_rows, Hkv, D]`` f32, ``q_norm/k_norm[D]`` f32,
-    ``q_out[S, n_rows, H, D]`` f32 (the attention's Q), caches ``[S, n_cells, Hkv, D]`` f16 or
+    ``q_out[S, n_rows, H, D]`` f32 or f16 (the attention's Q), caches ``[S, n_cells, Hkv, D]`` f16 or
     uint8 q8_0 blocks (with ``page_table``, int32 device [S, pages per stream]: page pools
     ``[n_pages, 256, Hkv, D]``)."""
     D = q_out.shape[-1]

@@ -377,6 +377,22 @@ def test_qk_prologue_rejects(mutate, code):
     assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == code
 
 
+def test_qk_prologue_takes_an_f16_q_out():
+    D, R, H = 256, 16, 24
+    f16 = lambda p: setattr(p, "q_out", sa.make_view(FAKE, sa.TYPE_F16, [D, R, H, 0], [2, H * D * 2, D * 2, R * H * D * 2]))
+    p = _prologue_params(S=0)
+    f16(p)
+    assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == sa.OK      # (no rows: no launch)
+    p.q_out.nb[1] = H * D * 2 + 2                                            # rows not 16-byte aligned
+    assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == sa.E_ALIGNMENT
+    p.q_out.nb[1] = H * D * 2
+    p.q_out.nb[2] = D                                                         # heads would alias
+    assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT
+    p = _prologue_params(S=0, cache_type=sa.TYPE_Q8_0)                       # q8_0 cache: f32 Q only
+    f16(p)
+    assert sa.load_library().sixi_qk_prologue(ctypes.byref(p)) == sa.E_INVALID_ARGUMENT
+
+
 def test_qk_prologue_q8_cache_and_empty_block():
     p = _prologue_params(cache_type=sa.TYPE_Q8_0)
     p.k_cache.data = FAKE + 2                      # q8_0 rows need 2-byte alignment only

@@ -224,3 +224,59 @@ def test_layer_core(kv_type):
     _say(f"layer core kv_type={kv_type}: max_abs={m['max_abs']:.3e} rel_l2={m['rel_l2']:.3e}")
     assert np.all(np.isfinite(g))
     assert m["max_abs"] <= MAX_ABS and m["rel_l2"] <= REL_L2, m
+
+
+@pytest.mark.parametrize("kv_type", [sa.TYPE_F16, sa.TYPE_Q8_0])
+def test_layer_core_f16_q_and_fused_gate(kv_type):
+    """The same layer with the gate fused into the attention and, over an f16 cache, the
+    prologue's Q written in f16 (the f32 Q rounded to nearest even, bit for bit): the output
+    equals the f32-Q, three-call layer bit for bit (the attention rounds Q to f16 itself).  Over
+    a q8_0 cache, whose Q conversion starts from the f32 values, the prologue refuses an f16 Q
+    and the f32-Q layer with the fused gate meets the oracle's bar."""
+    S, R, H, Hkv, D, n_cells = 3, 16, 24, 4, 256, 2304
+    kv_len, q_len = [2000, 17, 700], [16, 16, 5]
+    q8 = kv_type == sa.TYPE_Q8_0
+    _say(f"layer f16 Q + fused gate: kv_type={kv_type}")
+    qg, k, v, wq, wk = _inputs(S, R, H, Hkv, D, 53)
+    rng = np.random.default_rng(54)
+    zero = np.zeros((S, n_cells, Hkv, D // 32 * 34), np.uint8) if q8 else np.zeros((S, n_cells, Hkv, D), np.uint16)
+    hk = rng.standard_normal((S, n_cells, Hkv, D)).astype(np.float32)
+    hv = rng.standard_normal((S, n_cells, Hkv, D)).astype(np.float32)
+    kc = oracle.kv_write(hk, zero, None, None)
+    vc = oracle.kv_write(hv, zero, None, None)
+    dkc, dvc = _dev_cache(kc), _dev_cache(vc)
+    d_qg, dk, dv = torch.from_numpy(qg).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+    dwq, dwk = torch.from_numpy(wq).cuda(), torch.from_numpy(wk).cuda()
+    kl = torch.tensor(kv_len, dtype=torch.int32, device="cuda")
+    ql = torch.tensor(q_len, dtype=torch.int32, device="cuda")
+    fa = sa.FlashAttnExt()
+    q32 = torch.zeros((S, R, H, D), dtype=torch.float32, device="cuda")
+    sa.qk_prologue(d_qg, dk, dv, dwq, dwk, q32, dkc, dvc, kl, ql)
+    ref = torch.full((S, R, H, D), float("nan"), dtype=torch.float32, device="cuda")
+    fa(q32, dkc, dvc, ref, kv_len=kl, q_len=ql)
+    sa.attn_gate(ref, d_qg, ql)
+    q16 = torch.zeros((S, R, H, D), dtype=torch.float16, device="cuda")
+    got = torch.full_like(ref, float("nan"))
+    if q8:
+        assert sa.qk_prologue(d_qg, dk, dv, dwq, dwk, q16, dkc, dvc, kl, ql, check=False) == sa.E_INVALID_ARGUMENT
+        fa(q32, dkc, dvc, got, kv_len=kl, q_len=ql, gate=d_qg)
+    else:
+        sa.qk_prologue(d_qg, dk, dv, dwq, dwk, q16, dkc, dvc, kl, ql)
+        fa(q16, dkc, dvc, got, kv_len=kl, q_len=ql, gate=d_qg)
+    torch.cuda.synchronize()
+    r, g = ref.cpu().numpy(), got.cpu().numpy()
+    for s in range(S):
+        if not q8:
+            assert torch.equal(q16[s, :q_len[s]], q32[s, :q_len[s]].half()), s
+        assert np.array_equal(g[s, :q_len[s]], r[s, :q_len[s]]), s
+    wq_out, _, wkc, wvc = oracle.qk_prologue(qg, k, v, wq, wk, kc, vc, kv_len, q_len)
+    n_kv = max(a + b for a, b in zip(kv_len, q_len))
+    mask = oracle.build_kq_mask(n_kv, R, np.array(kv_len), np.array(q_len), True)
+    att = oracle.flash_attn_ext(np.nan_to_num(wq_out), np.ascontiguousarray(wkc[:, :n_kv]),
+                                np.ascontiguousarray(wvc[:, :n_kv]), kv_type, mask)
+    want = oracle.attn_gate(att, qg, q_len)
+    gg = np.concatenate([g[s, :q_len[s]].ravel() for s in range(S)])
+    ww = np.concatenate([want[s, :q_len[s]].ravel() for s in range(S)])
+    m = oracle.diff_metrics(ww, gg)
+    _say(f"layer f16 Q kv_type={kv_type}: max_abs={m['max_abs']:.3e} rel_l2={m['rel_l2']:.3e}")
+    assert m["max_abs"] <= MAX_ABS and m["rel_l2"] <= REL_L2, m
