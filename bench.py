@@ -167,8 +167,9 @@ def time_paged(fa, w, dev, steps: int, warmup: int, head_major: bool = False, ou
 
 
 def ws_bytes(fa, w, dev, mask=None, bounded=False) -> int:
-    """sixi_attn_workspace_bytes of a call of workload w (only 256-dim q8_0 rows that are not
-    16-byte aligned include an f16 staging of the cache)."""
+    """sixi_attn_workspace_bytes of a call of workload w: the split-K partial slots; q8_0 prefill
+    blocks add the f16 staging of K and V while it fits the 64 MiB cap (none with `bounded`);
+    explicit llama masks add the pre-pass's row table."""
     import torch
 
     import sixi_attn as sa
@@ -298,10 +299,10 @@ def copy_calibration(steps: int) -> int:
 
 def time_prefill(fa, steps: int, warmup: int, kv_type=None, head_dim=None, explicit_mask=False, bounded=False):
     """Both 2048-row chunks of the 4k causal prefill: (TFLOP/s, us for the two chunks).
-    kv_type q8_0 runs the same chunks over a q8_0 cache (128-dim heads: tiles converted in LDS;
-    256-dim heads: staged as f16 operands per call);
+    kv_type q8_0 runs the same chunks over a q8_0 cache (K and V staged as f16 per call under the
+    64 MiB cap, at 128- and 256-dim heads);
     explicit_mask hands the causal mask over as a ggml f16 KQ mask (the ggml hook's path);
-    bounded sets FLAG_BOUNDED_WORKSPACE (a 256-dim q8_0 cache converted in LDS, not staged)."""
+    bounded sets FLAG_BOUNDED_WORKSPACE (the q8_0 tiles converted in LDS, nothing staged)."""
     import dataclasses
 
     import torch

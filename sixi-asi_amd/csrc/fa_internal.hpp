@@ -76,8 +76,10 @@ struct FaArgs {
     int64_t g_nb1, g_nb2, g_nb3;  // at gate + d*4 + h*g_nb1 + j*g_nb2 + s*g_nb3 (qg's gate half)
 };
 
-// q8_0 KV at 256-dim heads beyond the q8_0 kernel (fa_q8_stage.hip): K, V and Q staged as dense f16 rows in
-// the workspace, then the f16 kernels.  k16/v16: [S][n_kv][Hkv][D], q16: [S][n_q][H][D].
+// q8_0 KV in blocks beyond the decode kernels (prefill chunks, 128- and 256-dim heads), while the
+// copy takes at most the staging cap and SIXI_ATTN_FLAG_BOUNDED_WORKSPACE is not set
+// (fa_q8_stage.hip): K and V staged as dense f16 rows in the workspace (Q too where q16 is set),
+// then the f16 prefill kernel.  k16/v16: [S][n_kv][Hkv][D], q16: [S][n_q][H][D].
 struct Q8StageArgs {
     const char* q;
     int64_t q_nb1, q_nb2, q_nb3;
