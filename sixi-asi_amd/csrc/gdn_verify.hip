@@ -7,12 +7,16 @@
 //   delta = beta * (v[h] - sk);   S[h][s] = alpha S[h][s] + delta k[s];   y[h] = sum_s S[h][s] q[s]
 // The reference runs one launch per token and stream with the state in HBM; here one work-group
 // owns the Hd x K state of one (stream, group) in registers for the whole block, so the state is
-// read once and written once (at the snapshot row), and each token costs 3 Hd K FMAs on chip.
+// read once and written once (at the snapshot row), and each token costs 3 Hd K FMAs on chip:
+// the decay alpha goes into a scalar factor of the carried state (S = cs * st, below), not into
+// every element.
 //
 // Two work-groups share each (stream, group), each owning half of the HD state rows (the rows
-// update independently; q, k, alpha and beta are staged by both): 94 instead of 136 registers at
-// 128 x 128, five waves per SIMD instead of three, so more work-groups' state loads overlap other
-// work-groups' token steps (Qwen verify batch 79 -> 68 us; a four-way split measured slower).
+// update independently; q, k, alpha and beta are staged by both): 101 instead of 136 registers
+// at 128 x 128, four waves per SIMD instead of three, so more work-groups' state loads overlap
+// other work-groups' token steps (Qwen verify batch 79 -> 68 us; a four-way split measured
+// slower).  The scalar factor took the element update from a multiply and an FMA to one FMA
+// (65.2 -> 62.9 us) at the cost of 7 registers, i.e. of the fifth wave per SIMD.
 //
 // Mapping (256 threads): a thread holds R consecutive state rows x C = 16 consecutive columns;
 // the TPR = K/16 lanes that share the rows form a row group (adjacent lanes), whose partial
@@ -23,6 +27,8 @@
 // Roofline: the state dominates the bytes (2 * 4 Hd K per group and stream: read + write);
 // each token adds 3 Hd K FMAs, so a block of n rows does 3n/8 FMA per state byte moved --
 // a 16-row verify block is VALU-bound on gfx950's FP32 rate (packed FP32 is not used).
+// Rounding differs from the step-by-step recurrence (S is cs * st, sums run over 16 columns
+// then a lane tree) at the level of f32 rounding.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -85,7 +91,12 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
     int snap = a.snap ? a.snap[s] : ql;
     snap = snap < 0 ? 0 : (snap > ql ? ql : snap);
 
+    // The state is carried as S = cs * st: a token's decay multiplies the scalar cs (the same in
+    // every lane) instead of every element, and the element update is st += (delta / cs) k^T --
+    // one FMA per element instead of a multiply and an FMA.  A token that takes cs outside
+    // [2^-30, 2^30] (a gate near 0 or above 1, or not finite) folds it into st first.
     float st[R][kC];
+    float cs = 1.0f;
     const char* sin_base = a.s_in + (int64_t)g * a.si_nb2 + (int64_t)s * a.si_nb3 + part * kC * 4;
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -102,7 +113,7 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
 #pragma unroll
             for (int u = 0; u < kC / 4; ++u)
                 *reinterpret_cast<f32x4*>(sout_base + (int64_t)(row0 + r) * a.so_nb1 + 16 * u) =
-                    f32x4{st[r][4 * u], st[r][4 * u + 1], st[r][4 * u + 2], st[r][4 * u + 3]};
+                    f32x4{st[r][4 * u], st[r][4 * u + 1], st[r][4 * u + 2], st[r][4 * u + 3]} * cs;
     };
     if (snap == 0) write_state();
 
@@ -130,34 +141,55 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
                                                       (int64_t)s * a.b_nb2);
         }
         __syncthreads();
+#pragma unroll 1
         for (int t = 0; t < nt; ++t) {
             float kv[kC], qv[kC];
 #pragma unroll
             for (int u = 0; u < kC / 4; ++u) {
-                const f32x4 x = lk[t][part * (kC / 4) + u], y = lq[t][part * (kC / 4) + u];
+                const f32x4 x = lk[t][part * (kC / 4) + u];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    kv[4 * u + e] = x[e];
-                    qv[4 * u + e] = y[e];
-                }
+                for (int e = 0; e < 4; ++e) kv[4 * u + e] = x[e];
             }
             const float al = la[t], be = lb[t];
+            // the factor after the token's decay; outside [2^-30, 2^30] (or not finite) the token
+            // folds it into st and the factor returns to 1 (the same in every lane)
+            const float cn = cs * al;
+            const bool fold = !(cn >= 0x1p-30f && cn <= 0x1p30f);
+            // S k with the state before the token (decayed first: after it)
+            float sk[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float x = 0.0f;
+#pragma unroll
+                for (int c = 0; c < kC; ++c) x += st[r][c] * kv[c];
+                sk[r] = group_sum<TPR>(x) * (DECAY_FIRST ? cn : cs);
+            }
+            if (fold) {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int c = 0; c < kC; ++c) st[r][c] *= cn;
+            }
+            cs = fold ? 1.0f : cn;
+            const float bi = be / cs;
+            // (q is read once the fold is done: fewer registers live across it)
+#pragma unroll
+            for (int u = 0; u < kC / 4; ++u) {
+                const f32x4 y = lq[t][part * (kC / 4) + u];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qv[4 * u + e] = y[e];
+            }
             float yo[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                float sk = 0.0f;
-#pragma unroll
-                for (int c = 0; c < kC; ++c) sk += st[r][c] * kv[c];
-                sk = group_sum<TPR>(sk);
-                if (DECAY_FIRST) sk *= al;
-                const float delta = be * (lv[t][rw + r] - sk);
+                const float dn = bi * (lv[t][rw + r] - sk[r]);
                 float yv = 0.0f;
 #pragma unroll
                 for (int c = 0; c < kC; ++c) {
-                    st[r][c] = al * st[r][c] + delta * kv[c];
+                    st[r][c] = fmaf(dn, kv[c], st[r][c]);
                     yv += st[r][c] * qv[c];
                 }
-                yo[r] = group_sum<TPR>(yv);
+                yo[r] = group_sum<TPR>(yv) * cs;
             }
             if (part == 0) {
                 char* yp = a.y + (int64_t)g * a.y_nb1 + (int64_t)(t0 + t) * a.y_nb2 + (int64_t)s * a.y_nb3 + row0 * 4;

@@ -110,3 +110,34 @@ def test_extreme_gates():
     be[:, :, ::3] = 0.0
     be[:, :, 1::3] = 1.0
     _run(q, k, v, al, be, S0, q_len=[8, 5], snap=[8, 4], label="alpha 0/1, beta 0/1")
+
+
+@pytest.mark.parametrize("decay_first", [False, True])
+def test_decays_that_leave_the_carried_scale_range(decay_first):
+    # the kernel carries the state as a scalar times a matrix and folds the scalar in when the
+    # running product of the gates leaves [2^-30, 2^30]: gates of 2^-20 (the product leaves the range
+    # at the second), 2^-40 (at once), 0 (a reset) and 4 (growth, the product passes 2^30 at the
+    # 16th row), across staging passes, against the oracle's step by step recurrence
+    q, k, v, al, be, S0 = _inputs(4, 40, 6, 128, 128, 61)
+    al[0, 3:6] = 2.0 ** -20
+    al[1, 10] = 2.0 ** -40
+    al[1, 20] = 0.0
+    al[2, :] = 4.0
+    al[3, 14:18] = 2.0 ** -20
+    S, n, G, K = q.shape
+    d = [torch.from_numpy(x).cuda() for x in (q, k, v, al, be)]
+    st = torch.from_numpy(S0).cuda()
+    y = torch.full((S, n, G, 128), float("nan"), dtype=torch.float32, device="cuda")
+    snap = [40, 4, 17, 16]
+    _say(f"gdn gate range: S={S} n={n} G={G} decay_first={decay_first} snap={snap}")
+    sa.gdn_verify(*d, y, st, None, None, torch.tensor(snap, dtype=torch.int32, device="cuda"), decay_first)
+    torch.cuda.synchronize()
+    want_y, want_st = oracle.gdn_verify(q, k, v, al, be, S0, None, snap, decay_first)
+    # the gates of 4 grow the state by up to 4^40: the bar is relative to each stream's scale
+    for s in range(S):
+        for got, want, what in ((y.cpu().numpy()[s], want_y[s], "y"), (st.cpu().numpy()[s], want_st[s], "state")):
+            assert np.all(np.isfinite(got)), (s, what)
+            m = oracle.diff_metrics(want, got)
+            scale = float(np.abs(want).max())
+            _say(f"stream {s} {what}: max_abs/scale={m['max_abs'] / scale:.3e} rel_l2={m['rel_l2']:.3e}")
+            assert m["max_abs"] <= 1e-5 * scale and m["rel_l2"] < 1e-5 and m["cosine"] > 0.99999, (s, what, m)
