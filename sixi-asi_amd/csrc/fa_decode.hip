@@ -26,7 +26,12 @@
 // (the *_dual forms) then choose on the device between the lengths-only body over the offsets
 // the mask implies and the mask body.
 // K/V reach LDS by direct global->LDS loads (buffer_load_dword{,x4} ... lds), so bytes in
-// flight cost no VGPRs.
+// flight cost no VGPRs.  f16 rows go in with the non-temporal policy (nt): each is read by one
+// work-group once and fills whole cache lines, so it should leave L2 before the lines that are
+// reused (Q, partial slots, page tables, q8_0 lines shared by neighbouring heads); measured
+// 138.2 -> 128.8 us on the 32 x 16 verify over head-major pages, 237.9 -> 208.5 us on the
+// 256-dim 32 x 4 verify.  q8_0 rows keep the default policy (nt measured 23% slower on the
+// long q8_0 decode: a 136-byte head row shares lines with the next head's).
 //
 // decode_t16, per 16-cell tile and wave (128-dim heads; 256-dim heads run twice the k-steps
 // and output tiles):
@@ -643,8 +648,8 @@ __device__ __forceinline__ void decode_piece(const FaArgs& a, DecodeLds<NTOT, KV
                 ko4[e] = off + e * 64;
                 vo4[e] = vo + e * vnb;
             }
-            dma16x4_to_lds(krs, ko4, base);
-            dma16x4_to_lds(vrs, vo4, base + 4 * 1024);
+            dma16x4_to_lds<true>(krs, ko4, base);  // (f16 rows: streamed once, non-temporal)
+            dma16x4_to_lds<true>(vrs, vo4, base + 4 * 1024);
         } else {
             static_assert(kQ8Dma == 9, "dword LDS-DMA batch of nine loads");
             uint32_t ko[Q8L], vo[Q8L];
@@ -1395,7 +1400,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
                     const uint32_t cell = W::CPL * (8 * b8 + u) + (uint32_t)lane / W::CPR;
                     o8[u] = cell * knb + 16u * (pos ^ (cell & 15u));
                 }
-                dma16x8_to_lds(krs, o8, base + 8192u * b8);
+                dma16x8_to_lds<true>(krs, o8, base + 8192u * b8);
             }
             if (rg == (RS == 1 ? 0 : 1)) {  // one row group stages both halves
 #pragma unroll
@@ -1403,7 +1408,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
                     const uint32_t cell = W::CPL * (8 * b8 + u) + (uint32_t)lane / W::CPR;
                     o8[u] = cell * vnb + 32u * ((pos >> 1) ^ (cell & 7u)) + 16u * (pos & 1u);
                 }
-                dma16x8_to_lds(vrs, o8, base + 32 * W::ROW + 8192u * b8);
+                dma16x8_to_lds<true>(vrs, o8, base + 32 * W::ROW + 8192u * b8);
             }
         }
     };
@@ -1438,7 +1443,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
                 const uint32_t cell = W::CPL * u + (uint32_t)lane / W::CPR;
                 o8[u] = cell * knb + 16u * (pos ^ (cell & 15u));
             }
-            dma16x8_to_lds(krs, o8, ring_base + (uint32_t)(j % kPipeK) * KB);
+            dma16x8_to_lds<true>(krs, o8, ring_base + (uint32_t)(j % kPipeK) * KB);
         };
         auto issue_v = [&](int j) {  // row group 1: V of step j into V slot j % kPipeV
             const uint32_t c0 = (uint32_t)(t0 + j * TL) * kWide;
@@ -1452,7 +1457,7 @@ __device__ __forceinline__ void decode_piece_wide(const FaArgs& a, WideLds<NTW, 
                 const uint32_t cell = W::CPL * u + (uint32_t)lane / W::CPR;
                 o8[u] = cell * vnb + 32u * ((pos >> 1) ^ (cell & 7u)) + 16u * (pos & 1u);
             }
-            dma16x8_to_lds(vrs, o8, vring_base + (uint32_t)(j % kPipeV) * KB);
+            dma16x8_to_lds<true>(vrs, o8, vring_base + (uint32_t)(j % kPipeV) * KB);
         };
         if constexpr (PIPE) {
             static_assert(RS == 2 && W::LOADS == 8, "the pipelined ring: one K and one V loader wave per lane");

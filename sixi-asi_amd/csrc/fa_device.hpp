@@ -112,61 +112,84 @@ __device__ __forceinline__ uint32_t buf_ld4(buf_rsrc r, uint32_t off) {
 // SGPR written by a VALU instruction needs (v_readfirstlane, SGPR-spill restores: the
 // compiler does not see the resource read inside the asm), and the s_nop after each M0
 // write covers the M0 -> LDS-DMA hazard.  M0 is restored at the end.
+// NT sets the loads' non-temporal policy (nt): for K/V rows that no other work-group reads,
+// i.e. f16 head rows (256 or 512 bytes, whole cache lines) streamed once by the decode
+// kernels, so that they leave L2 first and the lines the kernel does reuse stay.  Not for
+// q8_0 rows (136-byte head rows share lines with the neighbouring head's work-group) nor for
+// the prefill tiles (every row block of a head reads them).
+#define SIXI_DMA16X4_ASM(POL) \
+    "s_nop 4\n\t" \
+    "s_mov_b32 %0, m0\n\t" \
+    "s_mov_b32 m0, %1\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %2, %6, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %3, %6, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %4, %6, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %5, %6, 0 offen " POL "lds\n\t" \
+    "s_mov_b32 m0, %0"
+template <bool NT = false>
 __device__ __forceinline__ void dma16x4_to_lds(buf_rsrc rs, const uint32_t (&v)[4], uint32_t lds) {
     int saved;
-    asm volatile(
-        "s_nop 4\n\t"
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %6, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %3, %6, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %4, %6, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %5, %6, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "s"(rs)
-        : "memory", "scc");
+    if constexpr (NT)
+        asm volatile(SIXI_DMA16X4_ASM("nt ")
+                     : "=&s"(saved)
+                     : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "s"(rs)
+                     : "memory", "scc");
+    else
+        asm volatile(SIXI_DMA16X4_ASM("")
+                     : "=&s"(saved)
+                     : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "s"(rs)
+                     : "memory", "scc");
 }
+#define SIXI_DMA16X8_ASM(POL) \
+    "s_nop 4\n\t" \
+    "s_mov_b32 %0, m0\n\t" \
+    "s_mov_b32 m0, %1\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %2, %10, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %3, %10, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %4, %10, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %5, %10, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %6, %10, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %7, %10, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %8, %10, 0 offen " POL "lds\n\t" \
+    "s_add_u32 m0, m0, 1024\n\t" \
+    "s_nop 0\n\t" \
+    "buffer_load_dwordx4 %9, %10, 0 offen " POL "lds\n\t" \
+    "s_mov_b32 m0, %0"
+template <bool NT = false>
 __device__ __forceinline__ void dma16x8_to_lds(buf_rsrc rs, const uint32_t (&v)[8], uint32_t lds) {
     int saved;
-    asm volatile(
-        "s_nop 4\n\t"
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %10, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %3, %10, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %4, %10, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %5, %10, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %6, %10, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %7, %10, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %8, %10, 0 offen lds\n\t"
-        "s_add_u32 m0, m0, 1024\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %9, %10, 0 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]), "v"(v[7]), "s"(rs)
-        : "memory", "scc");
+    if constexpr (NT)
+        asm volatile(SIXI_DMA16X8_ASM("nt ")
+                     : "=&s"(saved)
+                     : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]),
+                       "v"(v[5]), "v"(v[6]), "v"(v[7]), "s"(rs)
+                     : "memory", "scc");
+    else
+        asm volatile(SIXI_DMA16X8_ASM("")
+                     : "=&s"(saved)
+                     : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]),
+                       "v"(v[5]), "v"(v[6]), "v"(v[7]), "s"(rs)
+                     : "memory", "scc");
 }
 // Five 16-byte-per-lane loads (5 KB): 16 q8_0 rows of 256 dims (17 x 256 B) and a spare tail.
 __device__ __forceinline__ void dma16x5_to_lds(buf_rsrc rs, const uint32_t (&v)[5], uint32_t lds) {
