@@ -161,3 +161,27 @@ def test_q8_prefill_explicit_mask(fa):
     in_lds = _run(fa, w, dev, mask_mode=sa.MASK_EXPLICIT, mask=dmask, bounded_workspace=True)
     for s in range(w.S):
         assert np.array_equal(got[s, :w.q_len[s]], in_lds[s, :w.q_len[s]]), s
+
+
+def _shifted(t, nbytes):
+    """The same q8_0 cache bytes at a base `nbytes` past a 256-byte aligned allocation."""
+    buf = torch.empty(t.numel() + 256, dtype=torch.uint8, device="cuda")
+    view = buf[nbytes:nbytes + t.numel()].view(t.shape)
+    view.copy_(t)
+    return view
+
+
+def test_q8_more_than_48_rows_any_row_alignment(fa):
+    """The 32-cell q8_0 kernel moves 136-byte rows with dword loads, so the rows' alignment does not
+    matter: a cache moved by 4, 8 or 12 bytes (every head row's position within 16 bytes changes)
+    gives the aligned cache's output bit for bit."""
+    kv_len, q_len = [2000, 37, 513, 4097], [16, 16, 9, 11]
+    w = wl.Workload("q8_align", 0x51A7_7100, len(kv_len), kv_len, q_len, H=24, Hkv=4, kv_type=sa.TYPE_Q8_0)
+    host = wl.make_host(w, poison=True)
+    dev = wl.to_device(host)
+    base = _run(fa, w, dev)
+    _check(w, host, base, list(range(w.S)), "q8 96 rows, aligned")
+    for shift in (4, 8, 12):
+        _say(f"q8 96 rows, cache moved by {shift} bytes")
+        got = _run(fa, w, dev, k=_shifted(dev["k"], shift), v=_shifted(dev["v"], shift))
+        assert np.array_equal(got, base, equal_nan=True), f"{shift}-byte shift changed the output"
