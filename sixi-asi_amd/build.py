@@ -38,8 +38,11 @@ HIP_FLAGS = [
 ]
 # Per-source flags.  fa_decode.hip: MFMA accumulators in VGPR form (the software-pipelined
 # step loop keeps O in the 256 VGPRs and its operands in AGPRs; in AGPR form the compiler
-# copies the 96 accumulator registers across every iteration).
-FILE_FLAGS = {"fa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+# copies the 96 accumulator registers across every iteration).  gdn_verify.hip: the same, for
+# the chunked kernel's state, which is an MFMA operand and accumulator at once (in AGPR form it
+# took 52 AGPRs and 244 VGPRs).
+FILE_FLAGS = {"fa_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+              "gdn_verify.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 
 
 def flags_for(src: str) -> list[str]:

@@ -5,30 +5,40 @@
 // GdnOperator::step_token; src/cuda/sixi_kernels.cu:241-281 is its CUDA twin):
 //   sk = sum_s S[h][s] k[s]    (times alpha first with SIXI_GDN_DECAY_FIRST, ggml's order)
 //   delta = beta * (v[h] - sk);   S[h][s] = alpha S[h][s] + delta k[s];   y[h] = sum_s S[h][s] q[s]
-// The reference runs one launch per token and stream with the state in HBM; here one work-group
-// owns the Hd x K state of one (stream, group) in registers for the whole block, so the state is
-// read once and written once (at the snapshot row), and each token costs 3 Hd K FMAs on chip:
+// The reference runs one launch per token and stream with the state in HBM; here the state of a
+// (stream, group) is read once and written once (at the snapshot row), and a block of rows runs on
+// chip.  Two kernels:
+//
+// gdn_verify_chunked_kernel (128-dim keys, states of 128 or 64 rows: the model's linear-attention
+// layers hold 128 x 128) runs 16 rows at a time in the closed ("WY") form of the delta rule, on the f32 matrix
+// cores; its comment below has the algebra and layout.  It is persistent: each work-group runs
+// several (stream, group, 64-row half) items and reads the next item's state while it computes
+// the current one.  Qwen verify batch (32 streams x 16 rows, 48 groups): 55-57 us against 64-65 us
+// for the step by step kernel below in the same process; launching one item per work-group it
+// measured 63.7 us (every work-group of a CU then loads, computes and stores in step), and without
+// the XCD pairing of the two halves of a state 60.5 us.
+//
+// gdn_verify_kernel (64-dim keys) steps token by token on the VALU with the state in registers;
 // the decay alpha goes into a scalar factor of the carried state (S = cs * st, below), not into
-// every element.
+// every element.  Two work-groups share each (stream, group) when the state has 128 rows, each
+// owning half of the rows (the rows update independently; q, k, alpha and beta are staged by
+// both).  At 128 x 128 this form took 101 registers (four waves per SIMD) and 62.9 us on the
+// Qwen verify batch (the scalar factor took the element update from a multiply and an FMA to one
+// FMA: 65.2 -> 62.9 us).
 //
-// Two work-groups share each (stream, group), each owning half of the HD state rows (the rows
-// update independently; q, k, alpha and beta are staged by both): 101 instead of 136 registers
-// at 128 x 128, four waves per SIMD instead of three, so more work-groups' state loads overlap
-// other work-groups' token steps (Qwen verify batch 79 -> 68 us; a four-way split measured
-// slower).  The scalar factor took the element update from a multiply and an FMA to one FMA
-// (65.2 -> 62.9 us) at the cost of 7 registers, i.e. of the fifth wave per SIMD.
+// Mapping of gdn_verify_kernel (256 threads): a thread holds R consecutive state rows x C = 16
+// consecutive columns; the TPR = K/16 lanes that share the rows form a row group (adjacent lanes),
+// whose partial dot products are summed by DPP lane moves (ds_bpermute shuffles measured 94
+// against 83 us).  The block's tokens are staged through LDS TC at a time (q, k, v, alpha, beta of
+// TC rows); every lane of a row group reads the same q/k columns, so those LDS reads are
+// broadcasts.  y leaves from the row group's first lane as R floats.
 //
-// Mapping (256 threads): a thread holds R consecutive state rows x C = 16 consecutive columns;
-// the TPR = K/16 lanes that share the rows form a row group (adjacent lanes), whose partial
-// dot products are summed by DPP lane moves (ds_bpermute shuffles measured 94 against 83 us).  The block's tokens are staged through LDS TC at a
-// time (q, k, v, alpha, beta of TC rows); every lane of a row group reads the same q/k columns,
-// so those LDS reads are broadcasts.  y leaves from the row group's first lane as R floats.
-//
-// Roofline: the state dominates the bytes (2 * 4 Hd K per group and stream: read + write);
-// each token adds 3 Hd K FMAs, so a block of n rows does 3n/8 FMA per state byte moved --
-// a 16-row verify block is VALU-bound on gfx950's FP32 rate (packed FP32 is not used).
-// Rounding differs from the step-by-step recurrence (S is cs * st, sums run over 16 columns
-// then a lane tree) at the level of f32 rounding.
+// Roofline: the state dominates the bytes (2 * 4 Hd K per group and stream: read + write); each
+// row adds 3 Hd K FMAs, so a block of n rows does 3n/8 FMA per state byte moved -- 6 FMA per byte
+// for a 16-row verify block: above the 4.9 FMA per HBM byte of the unpacked FP32 VALU (78.6
+// TFLOP/s against 8 TB/s), below the 9.8 of the f32 matrix cores (157.3 TFLOP/s).  Rounding differs from the step by
+// step recurrence (sums in another order, the scalar factor, the closed form) at the level of f32
+// rounding.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -205,6 +215,308 @@ __global__ __launch_bounds__(256) void gdn_verify_kernel(GdnArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Chunked form on the f32 matrix cores (128-dim keys).  Over a chunk of T = 16 rows the T steps
+// of the recurrence are one closed form (the "WY" / "UT" form of the delta rule; every quantity
+// below is exact in exact arithmetic, the step by step loop is the definition):
+//   A_t = alpha_0 ... alpha_t,   E[t][s] = alpha_{s+1} ... alpha_t (s <= t, 1 at s = t)
+//   P = S0 k^T, Z = S0 q^T       (S0 the state before the chunk; P, Z are Hd x T)
+//   c_t = A_{t-1} (A_{-1} = 1), or A_t when the decay comes first (ggml's order)
+//   L[t][s] = beta_t e(t, s) (k_s . k_t) for s < t, e(t, s) = E[t-1][s] (E[t][s] decay-first)
+//   R[h][t] = beta_t (v_t[h] - c_t P[h][t]);  U = R (I + L)^-T  (U[h][t] is token t's delta)
+//   y_t[h] = A_t Z[h][t] + sum_{s<=t} U[h][s] E[t][s] (k_s . q_t)
+//   S_sigma = A_sigma S0 + sum_{s<=sigma} E[sigma][s] U[:, s] k_s^T
+// so a chunk costs the products P and Z (Hd x 128 by 128 x 16 each), one Hd x 16 by 16 x 128
+// product per state it writes or carries, k k^T and k q^T (16 x 128 by 128 x 16, shared by the
+// work-group) and 16 x 16 work -- the step by step form's 3 Hd K FMAs per row, on the matrix cores
+// at twice the unpacked VALU rate.  No gate product spans more than one chunk (the carried state
+// is the plain matrix), so the gates' range is that of the step by step recurrence.
+//
+// Layout: a work-group owns 64 state rows (HD / 64 work-groups per state), wave w rows 16w ..
+// 16w+15.  v_mfma_f32_16x16x4f32: lane l supplies A[l%16][l/16] and B[l/16][l%16] and holds
+// D[4(l/16) + r][l%16] in register r.  Lane l = 16 gl + lr holds state row lr of its wave, columns
+// 16 m + 4 gl + j in register 4 m + j (m = 0..7, j = 0..3): read as eight 16-byte pieces, and at the
+// same time the B operand of P^T = k S0^T (k-index 16 m + 4 gl + j at step (m, j)) and the output
+// layout of S^T = k^T U'^T whose tile m covers columns 16 m .. 16 m + 15 -- so the state never
+// leaves registers between chunks.
+constexpr int kCT = 16;    // rows per chunk
+constexpr int kCP = 132;   // LDS pitch (floats) of staged k, q rows: 16-byte reads of 8 rows hit distinct banks
+
+__device__ __forceinline__ f32x4 mma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int HD, bool DECAY_FIRST>
+__global__ __launch_bounds__(256) void gdn_verify_chunked_kernel(GdnArgs a, int n_items, int pair) {
+    constexpr int K = 128, HR = 64, SPLIT = HD / HR, T = kCT;
+    static_assert(HD % HR == 0, "64 state rows per work-group");
+    __shared__ __align__(16) float lk[T][kCP], lq[T][kCP];
+    __shared__ __align__(16) float lv[T][HR];
+    __shared__ __align__(16) float la[T], lb[T];
+    __shared__ __align__(16) float lE[T][T];          // E[t][s], 0 for s > t
+    __shared__ __align__(16) float lred[4][2][T][T];  // per wave: partial k k^T, k q^T over 32 columns
+    __shared__ __align__(16) float lLT[T][T];         // lLT[s][t] = L[t][s]
+    __shared__ __align__(16) float lWT[T][T];         // lWT[t][s] = E[t][s] (k_s . q_t)
+
+    const int tid = threadIdx.x;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gl0 = (tid >> 4) & 3;  // the lane's group: columns 16 m + 4 gl0 .. + 3 of its state row
+    // Work item x = 64 rows of one (stream, group) state.  With pair set (two items per state,
+    // states a multiple of 8) items x and x + 8 are the two halves of one state: launched
+    // round-robin over the 8 XCDs by work-groups b and b + 8, they share the XCD's L2 for the
+    // state's q and k rows.
+    auto locate = [&](int x, int& g, int& s, int& hr0) {
+        int state, half;
+        if (pair) {
+            state = ((x >> 3) >> 1) * 8 + (x & 7);
+            half = (x >> 3) & 1;
+        } else {
+            state = x / SPLIT;
+            half = x % SPLIT;
+        }
+        g = state % a.G;
+        s = state / a.G;
+        hr0 = half * HR;
+    };
+    auto load_state = [&](int x, float (&dst)[32]) {
+        int g, s, hr0;
+        locate(x, g, s, hr0);
+        const char* p = a.s_in + (int64_t)g * a.si_nb2 + (int64_t)s * a.si_nb3 +
+                        (int64_t)(hr0 + 16 * wv + (tid & 15)) * a.si_nb1 + 16 * gl0;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(p + 64 * m);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[4 * m + j] = v4[j];
+        }
+    };
+
+    // A work-group runs items blockIdx.x, + gridDim.x, ...: the next item's state is read into
+    // nst while this item's chunks run, so the state transfers of one work-group overlap its own
+    // matrix-core work (launched one item per work-group, all of a CU's work-groups would load,
+    // compute and store in step).
+    float st[32], nst[32];
+    load_state(blockIdx.x, st);
+    for (int x = blockIdx.x; x < n_items; x += gridDim.x) {
+        int g, s, hr0;
+        locate(x, g, s, hr0);
+        const int xn = x + (int)gridDim.x;
+        const int h = hr0 + 16 * wv + (tid & 15);  // this lane's state row
+        int ql = a.q_len ? a.q_len[s] : a.n_rows;
+        ql = ql < 0 ? 0 : (ql > a.n_rows ? a.n_rows : ql);
+        int snap = a.snap ? a.snap[s] : ql;
+        snap = snap < 0 ? 0 : (snap > ql ? ql : snap);
+
+        char* const sout = a.s_out + (int64_t)g * a.so_nb2 + (int64_t)s * a.so_nb3 + (int64_t)h * a.so_nb1 + 16 * gl0;
+        if (snap == 0) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+                *reinterpret_cast<f32x4*>(sout + 64 * m) =
+                    f32x4{st[4 * m], st[4 * m + 1], st[4 * m + 2], st[4 * m + 3]};
+        }
+        if (ql == 0 && xn < n_items) load_state(xn, nst);
+
+        for (int t0 = 0; t0 < ql; t0 += T) {
+            const int nt = ql - t0 < T ? ql - t0 : T;
+            // the lane's LDS addresses and constants are derived anew in every chunk (an opaque copy
+            // of the thread index): hoisted out of the loop they would hold some 60 VGPRs
+            int tx;
+            asm volatile("v_mov_b32 %0, %1" : "=v"(tx) : "v"(tid));
+            const int lr = tx & 15, gl = (tx >> 4) & 3, hw = 16 * wv + lr;
+            // stage rows t0 .. t0+nt-1; rows past nt are zero keys, queries and values with gate 1 and
+            // beta 0, which leave the state and every other row's result unchanged
+            for (int i = tx; i < T * (K / 4); i += 256) {
+                const int t = i / (K / 4), c = i % (K / 4);
+                f32x4 kx = {0.0f, 0.0f, 0.0f, 0.0f}, qx = kx;
+                if (t < nt) {
+                    kx = *reinterpret_cast<const f32x4*>(a.k + (int64_t)g * a.k_nb1 + (int64_t)(t0 + t) * a.k_nb2 +
+                                                         (int64_t)s * a.k_nb3 + 16 * c);
+                    qx = *reinterpret_cast<const f32x4*>(a.q + (int64_t)g * a.q_nb1 + (int64_t)(t0 + t) * a.q_nb2 +
+                                                         (int64_t)s * a.q_nb3 + 16 * c);
+                }
+                *reinterpret_cast<f32x4*>(&lk[t][4 * c]) = kx;
+                *reinterpret_cast<f32x4*>(&lq[t][4 * c]) = qx;
+            }
+            for (int i = tx; i < T * (HR / 4); i += 256) {
+                const int t = i / (HR / 4), c = i % (HR / 4);
+                f32x4 vx = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (t < nt)
+                    vx = *reinterpret_cast<const f32x4*>(a.v + (int64_t)g * a.v_nb1 + (int64_t)(t0 + t) * a.v_nb2 +
+                                                         (int64_t)s * a.v_nb3 + 4 * hr0 + 16 * c);
+                *reinterpret_cast<f32x4*>(&lv[t][4 * c]) = vx;
+            }
+            if (tx < T) {
+                const int64_t ra = (int64_t)g * a.a_nb0 + (int64_t)(t0 + tx) * a.a_nb1 + (int64_t)s * a.a_nb2;
+                const int64_t rb = (int64_t)g * a.b_nb0 + (int64_t)(t0 + tx) * a.b_nb1 + (int64_t)s * a.b_nb2;
+                la[tx] = tx < nt ? *reinterpret_cast<const float*>(a.alpha + ra) : 1.0f;
+                lb[tx] = tx < nt ? *reinterpret_cast<const float*>(a.beta + rb) : 0.0f;
+            }
+            __syncthreads();
+            if (t0 == 0 && xn < n_items) load_state(xn, nst);  // in flight during this item's work
+
+            // E[t][s], one entry per thread, multiplied in row order
+            {
+                const int et = tx >> 4, es = tx & 15;
+                float e = 1.0f;
+#pragma unroll
+                for (int r = 1; r < T; ++r)
+                    if (r > es && r <= et) e *= la[r];
+                lE[et][es] = es <= et ? e : 0.0f;
+            }
+            // P^T = k S0^T and Z^T = q S0^T (lane: P[h][4 gl + j] in register j); wave w also sums
+            // k k^T and k q^T over columns 32 w .. 32 w + 31
+            f32x4 pt = {0.0f, 0.0f, 0.0f, 0.0f}, zt = pt, gk = pt, gq = pt;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                const f32x4 kx = *reinterpret_cast<const f32x4*>(&lk[lr][16 * m + 4 * gl]);
+                const f32x4 qx = *reinterpret_cast<const f32x4*>(&lq[lr][16 * m + 4 * gl]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    pt = mma4(kx[j], st[4 * m + j], pt);
+                    zt = mma4(qx[j], st[4 * m + j], zt);
+                }
+                if ((m >> 1) == wv) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        gk = mma4(kx[j], kx[j], gk);
+                        gq = mma4(kx[j], qx[j], gq);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                lred[wv][0][4 * gl + r][lr] = gk[r];  // k_{4gl+r} . k_lr, partial
+                lred[wv][1][4 * gl + r][lr] = gq[r];  // k_{4gl+r} . q_lr, partial
+            }
+            __syncthreads();
+
+            // L and W, one entry per thread: row ta, column tb
+            {
+                const int ta = tx >> 4, tb = tx & 15;
+                const float kk = lred[0][0][tb][ta] + lred[1][0][tb][ta] + lred[2][0][tb][ta] + lred[3][0][tb][ta];
+                const float kq = lred[0][1][tb][ta] + lred[1][1][tb][ta] + lred[2][1][tb][ta] + lred[3][1][tb][ta];
+                float l = 0.0f;
+                if (tb < ta) l = lb[ta] * (DECAY_FIRST ? lE[ta][tb] : lE[ta - 1][tb]) * kk;
+                lLT[tb][ta] = l;                  // L[ta][tb]
+                lWT[ta][tb] = lE[ta][tb] * kq;    // E[ta][tb] (k_tb . q_ta), 0 for tb > ta
+            }
+            __syncthreads();
+
+            // row lr of M = (I + L)^-1 by back substitution: M[s][t] = [s = t] - sum_{r>t} M[s][r] L[r][t]
+            // (row t - 1 of lLT is read while row t is used; the empty asm pins each step in place,
+            // else the compiler reads all 36 pieces up front into 144 VGPRs)
+            float mr[T];
+            mr[T - 1] = lr == T - 1 ? 1.0f : 0.0f;
+            f32x4 cur[T / 4], nxt[T / 4];
+#pragma unroll
+            for (int c = (T - 1) / 4; c < T / 4; ++c) cur[c] = *reinterpret_cast<const f32x4*>(&lLT[T - 2][4 * c]);
+#pragma unroll
+            for (int t = T - 2; t >= 0; --t) {
+                if (t > 0) {
+#pragma unroll
+                    for (int c = t / 4; c < T / 4; ++c) nxt[c] = *reinterpret_cast<const f32x4*>(&lLT[t - 1][4 * c]);
+                }
+                float x = lr == t ? 1.0f : 0.0f;
+#pragma unroll
+                for (int c = (t + 1) / 4; c < T / 4; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * c + e > t) x = fmaf(-mr[4 * c + e], cur[c][e], x);
+                asm volatile("" : "+v"(x) : : "memory");
+                mr[t] = x;
+#pragma unroll
+                for (int c = 0; c < T / 4; ++c) cur[c] = nxt[c];
+            }
+            // R[h][4 gl + j] and U^T = M R^T (lane: U[h][4 gl + j] in register j)
+            const float a0 = la[0];
+            f32x4 ut = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * gl + j;
+                const float ct = DECAY_FIRST ? lE[t][0] * a0 : (t ? lE[t - 1][0] * a0 : 1.0f);
+                const float rv = lb[t] * (lv[t][hw] - ct * pt[j]);
+                const float mv = gl == 0 ? mr[j] : gl == 1 ? mr[4 + j] : gl == 2 ? mr[8 + j] : mr[12 + j];
+                ut = mma4(mv, rv, ut);
+            }
+            // y^T = diag(A) Z^T + W^T U^T
+            {
+                f32x4 yt;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) yt[j] = lE[4 * gl + j][0] * a0 * zt[j];
+                const f32x4 wx = *reinterpret_cast<const f32x4*>(&lWT[lr][4 * gl]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) yt = mma4(wx[j], ut[j], yt);
+                char* yp = a.y + (int64_t)g * a.y_nb1 + (int64_t)(t0 + 4 * gl) * a.y_nb2 + (int64_t)s * a.y_nb3 + h * 4;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (4 * gl + j < nt) *reinterpret_cast<float*>(yp + (int64_t)j * a.y_nb2) = yt[j];
+            }
+            // S_sigma = A_sigma S0 + k^T (U E[sigma])^T, tile by tile; written to the snapshot and/or
+            // kept as the next chunk's S0
+            const bool more = t0 + T < ql;
+            const bool snap_here = snap > t0 && snap <= t0 + nt;
+            auto advance = [&](int sig, bool write, bool keep) {
+                const float as = lE[sig][0] * a0;
+                float ub[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) ub[j] = ut[j] * lE[sig][4 * gl + j];
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {
+                    f32x4 acc = f32x4{st[4 * m], st[4 * m + 1], st[4 * m + 2], st[4 * m + 3]} * as;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc = mma4(lk[4 * gl + j][16 * m + lr], ub[j], acc);
+                    if (write) *reinterpret_cast<f32x4*>(sout + 64 * m) = acc;
+                    if (keep) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) st[4 * m + j] = acc[j];
+                    }
+                }
+            };
+            if (snap_here) advance(snap - 1 - t0, true, more && snap == t0 + T);
+            if (more && !(snap_here && snap == t0 + T)) advance(T - 1, false, true);
+            if (more) __syncthreads();  // the next chunk overwrites the staged rows
+        }
+        __syncthreads();  // the next item overwrites the staged rows
+#pragma unroll
+        for (int i = 0; i < 32; ++i) st[i] = nst[i];
+    }
+}
+
+// Work-groups of the chunked kernel that fit the device at once (each then runs several items).
+template <int HD, bool DECAY_FIRST>
+int chunked_resident_groups() {
+    static int cached = -1;
+    if (cached < 0) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gdn_verify_chunked_kernel<HD, DECAY_FIRST>, 256, 0) ==
+                hipSuccess &&
+            cus > 0 && per_cu > 0)
+            cached = cus * per_cu;
+        else
+            cached = 0;  // unknown: one item per work-group
+    }
+    return cached;
+}
+
+template <int HD, bool DECAY_FIRST>
+hipError_t launch_chunked_df(const GdnArgs& a, hipStream_t stream) {
+    const int64_t items = (int64_t)a.S * a.G * (HD / 64);
+    if (items > INT32_MAX) return hipErrorInvalidValue;
+    const int resident = chunked_resident_groups<HD, DECAY_FIRST>();
+    const int64_t groups = resident > 0 && resident < items ? resident : items;
+    const int pair = HD == 128 && ((int64_t)a.S * a.G) % 8 == 0;
+    hipLaunchKernelGGL((gdn_verify_chunked_kernel<HD, DECAY_FIRST>), dim3((unsigned)groups), dim3(256), 0, stream, a,
+                       (int)items, pair);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_chunked(const GdnArgs& a, hipStream_t stream) {
+    return a.decay_first ? launch_chunked_df<HD, true>(a, stream) : launch_chunked_df<HD, false>(a, stream);
+}
+
 template <int K, int HD, int SPLIT>
 hipError_t launch_split(const GdnArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)((int64_t)a.S * a.G * SPLIT)), block(256);
@@ -224,8 +536,8 @@ hipError_t launch_shape(const GdnArgs& a, hipStream_t stream) {
 
 hipError_t launch_gdn_verify(const GdnArgs& a, hipStream_t stream) {
     if ((int64_t)a.S * a.G == 0) return hipSuccess;
-    if (a.K == 128 && a.HD == 128) return launch_shape<128, 128>(a, stream);
-    if (a.K == 128 && a.HD == 64) return launch_shape<128, 64>(a, stream);
+    if (a.K == 128 && a.HD == 128) return launch_chunked<128>(a, stream);
+    if (a.K == 128 && a.HD == 64) return launch_chunked<64>(a, stream);
     if (a.K == 64 && a.HD == 128) return launch_shape<64, 128>(a, stream);
     if (a.K == 64 && a.HD == 64) return launch_shape<64, 64>(a, stream);
     return hipErrorInvalidValue;
