@@ -97,6 +97,22 @@ def test_long_block_several_staging_passes():
     _run(*args, q_len=[40, 33], snap=[17, 33], label="40 rows")
 
 
+@pytest.mark.parametrize("decay_first", [False, True])
+def test_several_items_per_work_group(decay_first):
+    # 32 streams x 48 groups x 2 halves = 3072 items of 64 state rows: more than the work-groups
+    # that fit the device at once (768 on MI355X), so each work-group runs several items and reads
+    # the next item's state while it computes the current one; ragged lengths (0, 1, a chunk and a
+    # half, every row), snapshot rows anywhere in the block, in place
+    S, n, G = 32, 24, 48
+    args = _inputs(S, n, G, 128, 128, 71 + int(decay_first))
+    rng = np.random.default_rng(72 + int(decay_first))
+    q_len = [int(x) for x in rng.integers(0, n + 1, S)]
+    q_len[:4] = [0, 1, n, 16]
+    snap = [int(rng.integers(0, ql + 1)) for ql in q_len]
+    snap[2:4] = [17, 16]
+    _run(*args, q_len=q_len, snap=snap, decay_first=decay_first, label="3072 items")
+
+
 def test_no_lengths():
     _run(*_inputs(2, 3, 3, 128, 128, 41), label="no lengths")
 
