@@ -357,15 +357,21 @@ __global__ __launch_bounds__(256) void gdn_verify_chunked_kernel(GdnArgs a, int 
             // E[t][s], one entry per thread, multiplied in row order
             {
                 const int et = tx >> 4, es = tx & 15;
+                f32x4 a4[T / 4];  // every gate of the chunk (the same address in every lane)
+#pragma unroll
+                for (int u = 0; u < T / 4; ++u) a4[u] = *reinterpret_cast<const f32x4*>(&la[4 * u]);
                 float e = 1.0f;
 #pragma unroll
                 for (int r = 1; r < T; ++r)
-                    if (r > es && r <= et) e *= la[r];
+                    if (r > es && r <= et) e *= a4[r / 4][r % 4];
                 lE[et][es] = es <= et ? e : 0.0f;
             }
             // P^T = k S0^T and Z^T = q S0^T (lane: P[h][4 gl + j] in register j); wave w also sums
             // k k^T and k q^T over columns 32 w .. 32 w + 31
             f32x4 pt = {0.0f, 0.0f, 0.0f, 0.0f}, zt = pt, gk = pt, gq = pt;
+            // (raised wave priority while this wave issues the products: 55.0 -> 53.6-53.9 us on the
+            // verify batch; raised around the state's product as well, 54.5 us)
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
                 const f32x4 kx = *reinterpret_cast<const f32x4*>(&lk[lr][16 * m + 4 * gl]);
@@ -383,6 +389,7 @@ __global__ __launch_bounds__(256) void gdn_verify_chunked_kernel(GdnArgs a, int 
                     }
                 }
             }
+            __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 lred[wv][0][4 * gl + r][lr] = gk[r];  // k_{4gl+r} . k_lr, partial
