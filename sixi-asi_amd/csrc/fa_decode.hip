@@ -300,12 +300,19 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT, T16Dim<D>::DT
 
     // ---- S^T = K Q^T for every row tile ----
     f32x4 st[NT];
+    // Raised wave priority while a wave issues its MFMAs (here and around O^T += V^T P^T below):
+    // at 128-dim heads two work-groups share a CU, so two waves share each SIMD, and the one with
+    // matrix work goes first while the other dequantises (the 8 x 64k q8_0 verify, 48 rows:
+    // 161.9 -> 157.9 us; the other calls unchanged, outputs bitwise equal).  At 256-dim heads a
+    // wave has its SIMD to itself.
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
         st[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) st[n] = mfma16x16x32(kop[ks], as_f16x8(qs[(n * KS + ks) * 64 + lane]), st[n]);
     }
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(0);
     after_reads();
 
     // V^T operands: tile tt holds dim VD*r + tt of cells 4c..4c+3
@@ -376,6 +383,7 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT, T16Dim<D>::DT
     }
 
     // ---- probabilities (f32 row sums, f16 MFMA operand) and O^T += V^T P^T ----
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
         const float ref = acc.m[n];
@@ -411,6 +419,7 @@ __device__ __forceinline__ void tile_step(const FaArgs& a, Acc<NT, T16Dim<D>::DT
                 acc.o[tt][n] = mfma16x16x16(__builtin_bit_cast(f16x4, vt[tt]), pf, acc.o[tt][n]);
         }
     }
+    if constexpr (D == 128) __builtin_amdgcn_s_setprio(0);
 }
 
 // Writes the normalised rows of row tiles n0 .. n0+NT-1 held by this lane: dims
