@@ -637,6 +637,24 @@ def verify_q8_only(steps: int, warmup: int, head_dim: int = 128, q8: bool = True
     return 0
 
 
+def long_q8_only(steps: int, warmup: int) -> int:
+    """The long-context q8_0 configurations alone: 8 streams x 64k cells of q8_0 KV, a decode
+    (q_len 1) and an 8-row verify, one after the other, for the profiler."""
+    import sixi_attn as sa
+    from sixi_attn import workloads as wl
+
+    fa = sa.FlashAttnExt()
+    res = {}
+    for name in ("long_q8_decode", "long_q8_verify"):
+        w = wl.config(name)
+        dev = wl.to_device(wl.make_host(w))
+        ms, per = time_calls(fa, w, dev, max(1, steps), warmup)
+        res[name] = summarize(w, ms, per)
+    print(json.dumps({"workload": "8 streams x 65536 cells, q8_0 KV, 24 q-heads / 4 kv-heads x 128: q_len 1 and 8",
+                      **res}), flush=True)
+    return 0
+
+
 def verify_mask_only(steps: int, warmup: int) -> int:
     """The 32 x 16 batched verify over the contiguous f16 cache with its block-causal mask handed
     over as llama.cpp's explicit f16 KQ mask (the ggml hook's call)."""
@@ -685,7 +703,7 @@ def main() -> int:
     ap.add_argument("--workload", default="verify", choices=["verify", "copy", "prefill", "prefill_q8", "prefill_q8_bounded",
                                                                "prefill_d256_q8", "prefill_d256_q8_bounded", "layer",
                                                                "gdn", "verify_q8", "verify_d256", "verify_d256_q8", "verify_op",
-                                                               "headline", "verify_mask", "prefill_mask"])
+                                                               "headline", "verify_mask", "prefill_mask", "long_q8"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     args = ap.parse_args()
@@ -720,6 +738,8 @@ def main() -> int:
         return verify_op_only(args.steps, args.warmup)
     if args.workload == "headline":
         return headline_only(args.steps, args.warmup)
+    if args.workload == "long_q8":
+        return long_q8_only(args.steps, args.warmup)
     if args.workload.startswith("verify_d256"):
         return verify_q8_only(args.steps, args.warmup, head_dim=256, q8=args.workload.endswith("_q8"))
 
