@@ -12,9 +12,9 @@
 // gdn_verify_chunked_kernel (128-dim keys, states of 128 or 64 rows: the model's linear-attention
 // layers hold 128 x 128) runs 16 rows at a time in the closed ("WY") form of the delta rule, on the f32 matrix
 // cores; its comment below has the algebra and layout.  It is persistent: each work-group runs
-// several (stream, group, 64-row half) items and reads the next item's state while it computes
-// the current one.  Qwen verify batch (32 streams x 16 rows, 48 groups): 55-57 us against 64-65 us
-// for the step by step kernel below in the same process; launching one item per work-group it
+// several (stream, group, 64-row half) items and reads half of the next item's state while it
+// computes the current one.  Qwen verify batch (32 streams x 16 rows, 48 groups): 52.1-52.8 us
+// against 64-65 us for the step by step kernel below; launching one item per work-group it
 // measured 63.7 us (every work-group of a CU then loads, computes and stores in step), and without
 // the XCD pairing of the two halves of a state 60.5 us.
 //
@@ -290,14 +290,32 @@ __global__ __launch_bounds__(256) void gdn_verify_chunked_kernel(GdnArgs a, int 
             for (int j = 0; j < 4; ++j) dst[4 * m + j] = v4[j];
         }
     };
+    // columns 16 m0 .. 16 m0 + 63 of item x's state rows (registers 4 m0 .. 4 m0 + 15 of st)
+    auto load_half = [&](int x, int m0, float* dst) {
+        int g, s, hr0;
+        locate(x, g, s, hr0);
+        const char* p = a.s_in + (int64_t)g * a.si_nb2 + (int64_t)s * a.si_nb3 +
+                        (int64_t)(hr0 + 16 * wv + (tid & 15)) * a.si_nb1 + 16 * gl0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(p + 64 * (m0 + m));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[4 * m + j] = v4[j];
+        }
+    };
 
-    // A work-group runs items blockIdx.x, + gridDim.x, ...: the next item's state is read into
-    // nst while this item's chunks run, so the state transfers of one work-group overlap its own
-    // matrix-core work (launched one item per work-group, all of a CU's work-groups would load,
-    // compute and store in step).
-    float st[32], nst[32];
+    // A work-group runs items blockIdx.x, + gridDim.x, ...: the first half of the next item's state
+    // (columns 0 .. 63) is read into nst while this item's chunks run, so a work-group's state
+    // transfers overlap its own matrix-core work (launched one item per work-group, all of a CU's
+    // work-groups load, compute and store in step: 63.7 against 55 us on the verify batch).  The
+    // other half is read at the item's start: registers for all of it (148 VGPRs) leave three
+    // work-groups per CU, with half of it (125) four fit (54.5 -> 52.8 us).
+    float st[32], nst[16];
     load_state(blockIdx.x, st);
+    bool first = true;
     for (int x = blockIdx.x; x < n_items; x += gridDim.x) {
+        if (!first) load_half(x, 4, st + 16);  // the half not read ahead
+        first = false;
         int g, s, hr0;
         locate(x, g, s, hr0);
         const int xn = x + (int)gridDim.x;
@@ -314,7 +332,7 @@ __global__ __launch_bounds__(256) void gdn_verify_chunked_kernel(GdnArgs a, int 
                 *reinterpret_cast<f32x4*>(sout + 64 * m) =
                     f32x4{st[4 * m], st[4 * m + 1], st[4 * m + 2], st[4 * m + 3]};
         }
-        if (ql == 0 && xn < n_items) load_state(xn, nst);
+        if (ql == 0 && xn < n_items) load_half(xn, 0, nst);
 
         for (int t0 = 0; t0 < ql; t0 += T) {
             const int nt = ql - t0 < T ? ql - t0 : T;
@@ -352,7 +370,7 @@ __global__ __launch_bounds__(256) void gdn_verify_chunked_kernel(GdnArgs a, int 
                 lb[tx] = tx < nt ? *reinterpret_cast<const float*>(a.beta + rb) : 0.0f;
             }
             __syncthreads();
-            if (t0 == 0 && xn < n_items) load_state(xn, nst);  // in flight during this item's work
+            if (t0 == 0 && xn < n_items) load_half(xn, 0, nst);  // in flight during this item's work
 
             // E[t][s], one entry per thread, multiplied in row order
             {
@@ -485,7 +503,7 @@ __global__ __launch_bounds__(256) void gdn_verify_chunked_kernel(GdnArgs a, int 
         }
         __syncthreads();  // the next item overwrites the staged rows
 #pragma unroll
-        for (int i = 0; i < 32; ++i) st[i] = nst[i];
+        for (int i = 0; i < 16; ++i) st[i] = nst[i];
     }
 }
 
