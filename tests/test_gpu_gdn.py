@@ -113,6 +113,53 @@ def test_several_items_per_work_group(decay_first):
     _run(*args, q_len=q_len, snap=snap, decay_first=decay_first, label="3072 items")
 
 
+def test_strided_views():
+    # ggml views that are not packed: q and k stored group-major ([S][G][n][K] seen as [S][n][G][K]),
+    # v, y and both states in padded rows, alpha and beta every other float; out of place, so the
+    # padding of y and of the output state must stay untouched; 16 streams x 48 groups = 1536 items
+    # (several per work-group, the XCD pairing on), blocks of up to 20 rows
+    S, n, G, K, HD = 16, 20, 48, 128, 128
+    q, k, v, al, be, S0 = _inputs(S, n, G, K, HD, 81)
+    rng = np.random.default_rng(82)
+    q_len = [int(x) for x in rng.integers(0, n + 1, S)]
+    q_len[:3] = [n, 0, 16]
+    snap = [int(rng.integers(0, ql + 1)) for ql in q_len]
+    snap[0] = 17
+
+    def dev(x):
+        return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+    def group_major(x):
+        return dev(x.transpose(0, 2, 1, 3)).permute(0, 2, 1, 3)
+
+    def padded(x, pad, fill=0.0):
+        buf = torch.full(x.shape[:-1] + (x.shape[-1] + pad,), fill, dtype=torch.float32, device="cuda")
+        buf[..., :x.shape[-1]] = dev(x)
+        return buf, buf[..., :x.shape[-1]]
+
+    def every_other(x):
+        buf = torch.zeros(x.shape[:-1] + (2 * x.shape[-1],), dtype=torch.float32, device="cuda")
+        buf[..., ::2] = dev(x)
+        return buf[..., ::2]
+
+    _, vd = padded(v, 4)
+    _, st_in = padded(S0, 16)
+    y_buf, yd = padded(np.full(v.shape, np.nan, np.float32), 8, float("nan"))
+    so_buf, st_out = padded(np.full(S0.shape, np.nan, np.float32), 32, float("nan"))
+    _say(f"gdn strided views: S={S} n={n} G={G} q_len={q_len} snap={snap}")
+    sa.gdn_verify(group_major(q), group_major(k), vd, every_other(al), every_other(be), yd, st_in, st_out,
+                  torch.tensor(q_len, dtype=torch.int32, device="cuda"),
+                  torch.tensor(snap, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    want_y, want_st = oracle.gdn_verify(q, k, v, al, be, S0, q_len, snap)
+    got_y = yd.cpu().numpy()
+    assert np.array_equal(np.isnan(got_y), np.isnan(want_y)), "rows past q_len written or missing"
+    valid = ~np.isnan(want_y)
+    _check(got_y[valid], want_y[valid], "strided views y")
+    _check(st_out.cpu().numpy(), want_st, "strided views state")
+    assert torch.isnan(y_buf[..., HD:]).all() and torch.isnan(so_buf[..., K:]).all(), "padding written"
+
+
 def test_no_lengths():
     _run(*_inputs(2, 3, 3, 128, 128, 41), label="no lengths")
 
