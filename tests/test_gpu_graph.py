@@ -155,8 +155,10 @@ def test_layer_graph_fused_gate():
 
 
 def test_gdn_graph():
-    """GDN verify out of place (the input state stays fixed, so every replay has the same input)."""
-    S, n, G, K, HD = 8, 16, 48, 128, 128
+    """GDN verify out of place (the input state stays fixed, so every replay has the same input);
+    16 streams x 48 groups = 1536 items, more than the work-groups that fit at once, so the
+    captured launch runs several items per work-group."""
+    S, n, G, K, HD = 16, 16, 48, 128, 128
     _say(f"graph: gdn S={S} n={n} G={G}")
     q = torch.randn((S, n, G, K), device="cuda") / K ** 0.5
     k = torch.nn.functional.normalize(torch.randn((S, n, G, K), device="cuda"), dim=-1)
@@ -166,8 +168,8 @@ def test_gdn_graph():
     st_in = torch.randn((S, G, HD, K), device="cuda")
     st_out = torch.empty_like(st_in)
     y = torch.zeros((S, n, G, HD), device="cuda")
-    q_len = torch.tensor([16, 9, 1, 16, 0, 4, 16, 12], dtype=torch.int32, device="cuda")
-    snap = torch.tensor([16, 3, 1, 0, 0, 4, 8, 12], dtype=torch.int32, device="cuda")
+    q_len = torch.tensor([16, 9, 1, 16, 0, 4, 16, 12] * 2, dtype=torch.int32, device="cuda")
+    snap = torch.tensor([16, 3, 1, 0, 0, 4, 8, 12] * 2, dtype=torch.int32, device="cuda")
 
     def run():
         sa.gdn_verify(q, k, v, al, be, y, st_in, st_out, q_len, snap)
