@@ -290,3 +290,24 @@ def test_other_kernels_use_no_scratch(src, tmp_path_factory):
     assert asm.count(".private_segment_fixed_size:") > 0
     bad = kernels_with_scratch(asm)
     assert not bad, f"{len(bad)} kernels with scratch: {bad[:4]}"
+
+
+def kernel_vgprs(asm, fragment):
+    """{kernel: VGPRs + AGPRs} from the metadata of every kernel whose name contains fragment."""
+    meta = asm[asm.index("amdhsa.kernels:"):]
+    found = {}
+    for blk in meta.split("\n  - ")[1:]:
+        name = re.search(r"^    \.name:\s+(\S+)", blk, re.M)
+        vgpr = re.search(r"^    \.vgpr_count:\s+(\d+)", blk, re.M)
+        if name and vgpr and fragment in name.group(1):
+            found[name.group(1)] = int(vgpr.group(1))
+    return found
+
+
+def test_gdn_chunked_kernel_fits_four_work_groups_per_cu(tmp_path_factory):
+    # The chunked GDN kernel runs four 4-wave work-groups per CU (four waves per SIMD) only at
+    # <= 128 registers; at 129 it drops to three and the 32 x 16 verify batch slows by ~5 %, with
+    # every output unchanged, so only this test would notice.
+    counts = kernel_vgprs(_asm_of("gdn_verify.hip", tmp_path_factory), "gdn_verify_chunked_kernel")
+    assert len(counts) == 4, counts
+    assert max(counts.values()) <= 128, counts
